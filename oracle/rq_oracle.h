@@ -1,0 +1,139 @@
+/*
+ * rq_oracle.h — CPU restatement of Raster's block-quantized matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP kernels in
+ * raster_amd/csrc: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it. No product code path calls into it.
+ *
+ * Every function restates one reference function (Clojure, read as text from
+ * replikativ/raster); the citation is the reference file:line it follows.
+ * Numerics follow the JVM semantics of those functions:
+ *   - Clojure arithmetic on float and double operands widens to double;
+ *   - Math/round is Java Math.round(double): ties toward +infinity;
+ *   - (float d) is one IEEE round-to-nearest-even narrowing.
+ * Built with -O2 -ffp-contract=off and no fast-math so every rounding is the
+ * one written.
+ */
+#ifndef RQ_ORACLE_H
+#define RQ_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- java.util.Random (JDK LCG) — used to regenerate the reference tests'
+ *      inputs (e.g. test/raster/quant/train_test.clj:14-16, pack_test.clj:125-128,
+ *      tile_test.clj:195-196). nextGaussian uses the C library log/sqrt where
+ *      the JDK uses StrictMath (fdlibm); the two can differ in the last bit on
+ *      rare inputs, so Gaussian draws only feed tolerance-based checks. */
+typedef struct {
+  int64_t seed;
+  double next_next_gaussian;
+  int have_next_next_gaussian;
+} rqo_jrandom;
+
+void rqo_jrandom_init(rqo_jrandom* r, int64_t seed);
+int32_t rqo_jrandom_next(rqo_jrandom* r, int bits);
+int32_t rqo_jrandom_next_int(rqo_jrandom* r);
+double rqo_jrandom_next_double(rqo_jrandom* r);
+double rqo_jrandom_next_gaussian(rqo_jrandom* r);
+void rqo_jrandom_next_bytes(rqo_jrandom* r, int8_t* out, int64_t n);
+/* fill helpers matching the reference tests' generators */
+void rqo_jfill_gauss(int64_t seed, double mult, float* out, int64_t n);       /* train_test.clj:14-16 */
+void rqo_jfill_uniform_centered(int64_t seed, float* out, int64_t n);         /* pack_test.clj:125-128 */
+void rqo_jfill_bytes(int64_t seed, int8_t* out, int64_t n);                   /* tile_test.clj:195-196 */
+
+/* Java Math.round(double): floor(x + 0.5) evaluated exactly; NaN -> 0. */
+int64_t rqo_java_round(double x);
+
+/* ---- scalar conversions ---- */
+float rqo_f16_to_f32(uint16_t h);          /* Float.float16ToFloat, raster/types/float16.clj:40-43 */
+uint16_t rqo_f32_to_f16(float f);          /* Float.floatToFloat16 (RNE) */
+float rqo_bf16_to_f32(uint16_t b);         /* exact widening */
+uint16_t rqo_f32_to_bf16(float f);         /* RNE narrowing (NaN stays NaN) */
+
+/* ---- int8 MAC seam ---- */
+/* par/dp4a: raster/par.clj:421-440 (signed little-endian byte lanes). */
+int64_t rqo_dp4a(int32_t a, int32_t b, int64_t acc);
+/* wi8-dot-q4: raster/quant/kernels.clj:33-46 (16 packed bytes, lo=k, hi=k+16). */
+int64_t rqo_wi8_dot_q4(const uint8_t* wq, int64_t woff, const int8_t* xq, int64_t xoff);
+/* wi8-dot: raster/quant/kernels.clj:48-61 (unsigned byte x signed int8). */
+int64_t rqo_wi8_dot(const uint8_t* wq, int64_t woff, const int8_t* xq, int64_t xoff, int64_t len);
+
+/* ---- Q8_0 row-major (signed codes, f32 scale per 32) ---- */
+/* q8-quantize: raster/quant/train.clj:34-58. Returns 0, or -1 if in % 32 != 0. */
+int rqo_q8_quantize(const float* W, int64_t out, int64_t in, int8_t* codes, float* scales);
+/* dequant-q8-dense: raster/quant/train.clj:60-71. */
+void rqo_dequant_q8_dense(const int8_t* codes, const float* scales, int64_t in, int64_t out, float* W);
+/* qlinear-q8: raster/quant/train.clj:77-108 (f32 products, f64 accumulator, f32 store). */
+void rqo_qlinear_q8(const float* x, const int8_t* codes, const float* scales,
+                    int64_t m, int64_t in, int64_t out, float* y);
+/* qlinear-q8-dx: raster/quant/train.clj:110-137. */
+void rqo_qlinear_q8_dx(const float* dy, const int8_t* codes, const float* scales,
+                       int64_t m, int64_t in, int64_t out, float* dx);
+
+/* ---- parametric unsigned-offset quantizer (Q4_0 / unsigned Q8_0) ---- */
+/* quantize-weight: raster/compiler/backend/cpu/quant.clj:42-70. nibble != 0 selects
+ * :nibble-interleaved (wq has len/2 bytes), else :byte-direct (len bytes). */
+void rqo_quantize_weight(const float* w, int64_t len, int weight_bits, int zero_point,
+                         int nibble, uint8_t* wq, float* ws);
+/* Inverse used by test/raster/compiler/backend/cpu/quant_encode_test.clj:9-24. */
+void rqo_dequant_weight(const uint8_t* wq, const float* ws, int64_t len, int zero_point,
+                        int nibble, float* out);
+/* Q4_0 rows with fp16 scales (the configs' storage): W[o,i] = f32(d)*(q-8), one rounding. */
+void rqo_dequant_q4_f16(const uint8_t* wq, const uint16_t* ws_f16, int64_t in, int64_t out, float* W);
+/* Q4_0 rows with f32 scales. */
+void rqo_dequant_q4_f32(const uint8_t* wq, const float* ws, int64_t in, int64_t out, float* W);
+/* f32-activation Q4_0 linear: qlinear-q8's loop (train.clj:92-107) over the Q4_0
+ * dequant (quant_encode_test.clj:19-20); scale is fp16 when ws_f16 != NULL, else f32. */
+void rqo_qlinear_q4(const float* x, const uint8_t* wq, const uint16_t* ws_f16, const float* ws_f32,
+                    int64_t m, int64_t in, int64_t out, float* y);
+
+/* ---- activation quantizer + int-activation GEMVs ---- */
+/* quantize-act-blocks! / quantize-act-i8: cpu/quant.clj:282-305 (clamped, Java round). */
+void rqo_quantize_act_i8(const float* x, int64_t M, int64_t in, int8_t* xq, float* xs, int32_t* xsum);
+/* qmatmul-q4-composable!: raster/quant/kernels.clj:161-184 (row-major Q4_0, f32 scales). */
+void rqo_qmatmul_q4_composable(const int8_t* xq, const float* xs, const int32_t* xsum,
+                               const uint8_t* wq, const float* ws, float* y,
+                               int64_t in, int64_t out, int64_t o_start, int64_t o_count);
+/* Row-major Q8 (signed codes) twin of the composable fold: y[o] = sum_b xs*ws*dot. */
+void rqo_qmatmul_q8_composable(const int8_t* xq, const float* xs, const int8_t* codes,
+                               const float* ws, float* y, int64_t in, int64_t out);
+
+/* ---- column-interleaved x8 layout (CPU stream-gemv layout) ---- */
+/* repack: raster/compiler/core/layout.clj:246-286 (tile 8, k-group 4).
+ * nibble: src wq row-major Q4_0 [out*in/2] -> wqi [(out/8)*(in/32)*128];
+ * byte-direct: src wq unsigned bytes [out*in] -> wqi [(out/8)*(in/32)*256]. */
+int rqo_repack_x8(const uint8_t* wq, const float* ws, int64_t out, int64_t in, int nibble,
+                  uint8_t* wqi, float* wsi);
+/* wi8-dot-q4-x8 / wi8-dot-q8-x8: raster/quant/kernels.clj:63-90, 258-278. */
+void rqo_wi8_dot_q4_x8(const uint8_t* wqi, int64_t woff, const int8_t* xq, int64_t xoff, int32_t* out8);
+void rqo_wi8_dot_q8_x8(const uint8_t* wqi, int64_t woff, const int8_t* xq, int64_t xoff, int32_t* out8);
+/* qmatmul-q4-x8! / qmatmul-q8-x8!: raster/quant/kernels.clj:216-247, 308-333. */
+void rqo_qmatmul_q4_x8(const int8_t* xq, const float* xs, const int32_t* xsum,
+                       const uint8_t* wqi, const float* wsi, float* y,
+                       int64_t in, int64_t out, int64_t g_start, int64_t g_count);
+void rqo_qmatmul_q8_x8(const int8_t* xq, const float* xs, const int32_t* xsum,
+                       const uint8_t* wqi, const float* wsi, float* y,
+                       int64_t in, int64_t out, int64_t g_start, int64_t g_count);
+
+/* ---- signed q8_0 x q8_0 prefill path ---- */
+/* quantize-one-q8: raster/quant/pack.clj:210-236. Returns -1 if in % 32 != 0. */
+int rqo_quantize_one_q8(const float* W, int64_t in, int64_t out, int32_t* wp, float* ws);
+/* quant-act-i8-rows-gpu!: raster/quant/kernels_k.clj:309-342 (no clamp). */
+void rqo_quant_act_i8_rows(const float* x, int32_t* xp, float* xs, int64_t in, int64_t nrows);
+/* qmatmul-i8-gemm!: raster/quant/kernels_k.clj:344-370. */
+void rqo_qmatmul_i8_gemm(const int32_t* xp, const float* xs, const int32_t* wp, const float* ws,
+                         float* y, int64_t in, int64_t out, int64_t nrows);
+/* i8gemv-dp4a!: raster/quant/kernels_k.clj:141-150. */
+void rqo_i8gemv_dp4a(const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out);
+
+/* ---- dense helpers (brute force, f64) used to pin the restatements ---- */
+void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t in, int64_t out,
+                             double* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,367 @@
+"""Pins the C oracle (oracle/rq_oracle.c) before anything is compared against it.
+
+Three kinds of checks, each chosen so a plausible slip in the restatement
+(dropped zero-point, swapped nibble, wrong block index, C-style rounding) fails:
+  * known answers and properties asserted by the reference's own tests
+    (file:line cited per test, paths inside replikativ/raster);
+  * closed forms computed independently here in numpy (IEEE f32 multiply,
+    int64 dot products, f64 brute force);
+  * JDK constants for java.util.Random and Math.round.
+"""
+import numpy as np
+import pytest
+
+
+# ---------------------------------------------------------------- JDK semantics
+def test_java_random_known_values(orc):
+    # JDK constants: new Random(42).nextInt() == -1170105035,
+    # new Random(0).nextInt() == -1155484576, new Random(0).nextGaussian() == 0.8025330637390305
+    b = orc.jfill_bytes(42, 4).view(np.int32)[0]
+    assert b == -1170105035
+    b0 = orc.jfill_bytes(0, 4).view(np.int32)[0]
+    assert b0 == -1155484576
+    g = orc.jfill_gauss(0, 1.0, 1)[0]
+    assert g == np.float32(0.8025330637390305)
+    u = orc.jfill_uniform_centered(0, 1)[0]
+    assert u == np.float32(0.730967787376657 - 0.5)
+
+
+def test_java_round_ties_toward_positive_infinity(orc):
+    # raster/compiler/backend/intrinsics.clj:39-45: :round is Java floor(x+0.5)
+    cases = {2.5: 3, -2.5: -2, -0.5: 0, 0.5: 1, 1.5: 2, -1.5: -1,
+             0.49999999999999994: 0, -127.5: -127, 126.5: 127, float("nan"): 0}
+    for x, want in cases.items():
+        assert orc.java_round(x) == want, x
+
+
+# ---------------------------------------------------------------- conversions
+def test_f16_widening_is_exact_for_every_half(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    ours = orc.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(ours[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.all(np.isnan(ours[np.isnan(ref)]))
+
+
+def test_f16_narrowing_matches_ieee_rne(orc):
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(0.005, 0.05, 4000), rng.standard_normal(4000) * 1e-5,
+                        rng.standard_normal(4000) * 1e4]).astype(np.float32)
+    L = orc.lib()
+    ours = np.array([L.rqo_f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(ours, x.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_rne(orc):
+    # RNE: exact ties go to even; compare with float64 nearest-even arithmetic
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(20000).astype(np.float32)
+    ties = (np.arange(1, 200, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties, -ties])
+    bits = orc.f32_to_bf16_bits(x)
+    back = orc.bf16_bits_to_f32(bits).astype(np.float64)
+    err = np.abs(back - x.astype(np.float64))
+    # the nearest bf16 neighbours: truncation and truncation + 1 ulp
+    u = x.view(np.uint32)
+    lo = (u & 0xFFFF0000).view(np.float32).astype(np.float64)
+    hi = ((u & 0xFFFF0000) + 0x10000).view(np.float32).astype(np.float64)
+    best = np.minimum(np.abs(lo - x), np.abs(hi - x))
+    assert np.all(err == best)
+    tie_out = orc.f32_to_bf16_bits(ties)
+    assert np.all(tie_out % 2 == 0)
+    L = orc.lib()
+    assert all(L.rqo_f32_to_bf16(float(v)) == b for v, b in zip(x[:500], bits[:500]))
+
+
+# ---------------------------------------------------------------- int MAC seam
+def test_dp4a_known_answers(orc):
+    # test/raster/quant/kernels_k_gpu_test.clj:131-137
+    assert orc.dp4a(0x01020304, 0x01010101, 0) == 10
+    assert orc.dp4a(0x01000000, 0x05000000, 95) == 100
+    assert orc.dp4a(0x000000FF, 0x00000002, 0) == -2
+
+
+def test_dp4a_matches_bytewise_dot(orc):
+    rng = np.random.default_rng(11)
+    a = rng.integers(-2**31, 2**31, 200, dtype=np.int64)
+    b = rng.integers(-2**31, 2**31, 200, dtype=np.int64)
+    for x, y in zip(a, b):
+        xa = np.array([x], np.int64).astype(np.int32).view(np.int8).astype(np.int64)
+        ya = np.array([y], np.int64).astype(np.int32).view(np.int8).astype(np.int64)
+        assert orc.dp4a(int(x), int(y), 7) == 7 + int(np.dot(xa, ya))
+
+
+def test_wi8_dot_q4_nibble_order(orc):
+    # lo nibble = element k, hi nibble = element k+16 (cpu/quant.clj:27-31, kernels.clj:33-46)
+    rng = np.random.default_rng(2)
+    q = rng.integers(0, 16, 32)
+    x = rng.integers(-127, 128, 32).astype(np.int8)
+    wq = (q[:16] | (q[16:] << 4)).astype(np.uint8)
+    assert orc.wi8_dot_q4(wq, 0, x, 0) == int(np.dot(q, x.astype(np.int64)))
+
+
+# ---------------------------------------------------------------- Q8_0 (train.clj)
+def test_q8_codec_roundtrip(orc):
+    # test/raster/quant/train_test.clj:18-24
+    out, in_ = 4, 64
+    W = orc.jfill_gauss(1, 0.3, out * in_)
+    codes, scales = orc.q8_quantize(W, out, in_)
+    Wr = orc.dequant_q8_dense(codes, scales, in_, out)
+    assert np.max(np.abs(W - Wr)) < 0.01
+    assert codes.min() >= -127 and codes.max() <= 127
+
+
+def test_q8_quantize_requires_in_multiple_of_32(orc):
+    with pytest.raises(AssertionError):
+        orc.q8_quantize(np.zeros(30, np.float32), 1, 30)
+
+
+def test_dequant_q8_is_one_ieee_f32_multiply(orc):
+    rng = np.random.default_rng(0)
+    out, in_ = 16, 256
+    codes = rng.integers(-127, 128, out * in_).astype(np.int8)
+    scales = rng.uniform(0.002, 0.02, out * in_ // 32).astype(np.float32)
+    W = orc.dequant_q8_dense(codes, scales, in_, out)
+    ref = np.repeat(scales.reshape(out, -1), 32, axis=1).ravel() * codes.astype(np.float32)
+    assert ref.dtype == np.float32
+    assert np.array_equal(W.view(np.uint32), ref.view(np.uint32))
+
+
+def test_qlinear_forward_matches_dense(orc):
+    # test/raster/quant/train_test.clj:26-40 (< 1e-5)
+    out, in_, m = 4, 64, 2
+    W = orc.jfill_gauss(1, 0.3, out * in_)
+    X = orc.jfill_gauss(2, 0.3, m * in_)
+    codes, scales = orc.q8_quantize(W, out, in_)
+    Wd = orc.dequant_q8_dense(codes, scales, in_, out)
+    y = orc.qlinear_q8(X, codes, scales, m, in_, out)
+    ref = (X.reshape(m, in_).astype(np.float64) @ Wd.reshape(out, in_).astype(np.float64).T).ravel()
+    assert np.max(np.abs(y - ref)) < 1e-5
+
+
+@pytest.mark.parametrize("m,in_,out", [(1, 32, 1), (3, 96, 5), (4, 256, 16)])
+def test_qlinear_q8_brute_force(orc, m, in_, out):
+    rng = np.random.default_rng(m * 100 + out)
+    codes = rng.integers(-127, 128, out * in_).astype(np.int8)
+    scales = rng.uniform(0.002, 0.02, out * in_ // 32).astype(np.float32)
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    y = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    # independent: exact per-element products in f64, summed in f64
+    s = np.repeat(scales.reshape(out, -1), 32, axis=1).astype(np.float64)
+    ref = x.reshape(m, in_).astype(np.float64) @ (s * codes.reshape(out, in_)).T
+    assert np.max(np.abs(y - ref.ravel())) <= 1e-5 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_dx_pullback_matches_finite_differences(orc):
+    # test/raster/quant/train_test.clj:52-68 (< 2e-3 at eps 1e-3)
+    out, in_, m = 4, 64, 2
+    W = orc.jfill_gauss(1, 0.3, out * in_)
+    x = orc.jfill_gauss(2, 0.3, m * in_)
+    tgt = orc.jfill_gauss(3, 0.3, m * out)
+    codes, scales = orc.q8_quantize(W, out, in_)
+
+    def loss(xv):
+        y = orc.qlinear_q8(xv, codes, scales, m, in_, out).astype(np.float64)
+        return float(np.sum(0.5 * (y - tgt) ** 2))
+
+    y = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    gx = orc.qlinear_q8_dx((y - tgt).astype(np.float32), codes, scales, m, in_, out)
+    eps = 1e-3
+    for idx in [3, 17, 40, 63, 64, 100]:
+        xp, xm = x.copy(), x.copy()
+        xp[idx] += np.float32(eps)
+        xm[idx] -= np.float32(eps)
+        num = (loss(xp) - loss(xm)) / (2 * eps)
+        assert abs(gx[idx] - num) < 2e-3
+
+
+# ---------------------------------------------------------------- parametric encoder
+def test_parametric_encode(orc):
+    # test/raster/compiler/backend/cpu/quant_encode_test.clj:26-44
+    n = 256
+    w = orc.jfill_uniform_centered(42, n)
+    wq4, ws4 = orc.quantize_weight_q4(w)
+    wq8, ws8 = orc.quantize_weight_q8u(w)
+    assert wq4.size == n // 2 and wq8.size == n
+    e4 = np.max(np.abs(w - orc.dequant_weight(wq4, ws4, n, 8, True)))
+    e8 = np.max(np.abs(w - orc.dequant_weight(wq8, ws8, n, 128, False)))
+    assert e4 > 0
+    assert e8 < 0.2 * e4
+
+
+def test_q4_dequant_closed_form(orc):
+    rng = np.random.default_rng(9)
+    out, in_ = 8, 128
+    q = rng.integers(0, 16, (out, in_))
+    # pack: byte k of block b = q[b*32+k] | q[b*32+k+16] << 4
+    qb = q.reshape(out, in_ // 32, 2, 16)
+    wq = (qb[:, :, 0, :] | (qb[:, :, 1, :] << 4)).astype(np.uint8).ravel()
+    sc16 = rng.uniform(0.005, 0.05, out * in_ // 32).astype(np.float16)
+    W = orc.dequant_q4(wq, sc16.view(np.uint16), in_, out)
+    ref = np.repeat(sc16.astype(np.float32).reshape(out, -1), 32, axis=1) * (q - 8).astype(np.float32)
+    assert np.array_equal(W.view(np.uint32), ref.astype(np.float32).ravel().view(np.uint32))
+    W32 = orc.dequant_q4(wq, sc16.astype(np.float32), in_, out)
+    assert np.array_equal(W32, W)
+
+
+def test_qlinear_q4_brute_force(orc):
+    rng = np.random.default_rng(4)
+    m, in_, out = 3, 128, 12
+    wq = rng.integers(0, 256, out * in_ // 2).astype(np.uint8)
+    sc16 = rng.uniform(0.005, 0.05, out * in_ // 32).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    y = orc.qlinear_q4(x, wq, sc16, m, in_, out)
+    W = orc.dequant_q4(wq, sc16, in_, out).reshape(out, in_).astype(np.float64)
+    ref = x.reshape(m, in_).astype(np.float64) @ W.T
+    assert np.max(np.abs(y - ref.ravel())) <= 1e-5 * np.max(np.abs(ref))
+
+
+# ---------------------------------------------------------------- act quant / int GEMV
+def test_quantize_act_i8_properties(orc):
+    rng = np.random.default_rng(8)
+    M, in_ = 3, 256
+    x = rng.standard_normal(M * in_).astype(np.float32)
+    x[:32] = 0.0  # an all-zero block: d = 0, id = 0, codes 0
+    xq, xs, xsum = orc.quantize_act_i8(x, M, in_)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    d = np.max(np.abs(blocks), axis=1) / 127.0
+    assert np.array_equal(xs, d.astype(np.float32))
+    q = xq.reshape(-1, 32).astype(np.int64)
+    assert np.array_equal(xsum, q.sum(axis=1))
+    nz = d > 0
+    recon = q[nz] * d[nz, None]
+    assert np.all(np.abs(recon - blocks[nz]) <= d[nz, None] / 2 + 1e-12)
+    assert np.all(q[0] == 0) and xs[0] == 0
+
+
+def test_q4_composable_equals_independent_int_dot(orc):
+    # kernels.clj:140-184 vs the scalar oracle of bench/raster/quant_faithfulness.clj:55-75
+    rng = np.random.default_rng(12)
+    in_, out = 256, 24
+    w = rng.uniform(-0.5, 0.5, out * in_).astype(np.float32)
+    x = rng.uniform(-0.5, 0.5, in_).astype(np.float32)
+    wq, ws = orc.quantize_weight_q4(w)
+    xq, xs, xsum = orc.quantize_act_i8(x, 1, in_)
+    y = orc.qmatmul_q4_composable(xq, xs, xsum, wq, ws, in_, out)
+    q = np.empty((out, in_), np.int64)
+    wr = wq.reshape(out, in_ // 32, 16).astype(np.int64)
+    q.reshape(out, in_ // 32, 32)[:, :, :16] = wr & 0xF
+    q.reshape(out, in_ // 32, 32)[:, :, 16:] = wr >> 4
+    dots = ((q - 8).reshape(out, -1, 32) * xq.reshape(-1, 32).astype(np.int64)).sum(axis=2)
+    ref = (dots * (xs.astype(np.float64)[None, :] * ws.reshape(out, -1).astype(np.float64))).sum(axis=1)
+    assert np.max(np.abs(y - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("out,in_", [(16, 64), (1024, 640), (8, 32), (24, 128)])
+def test_x8_tile_matches_single_column(orc, out, in_):
+    # test/raster/quant/tile_test.clj:198-215 (exact int32 dots)
+    half, nb = in_ // 2, in_ // 32
+    wq = orc.jfill_bytes(out + in_, out * in_ // 2).view(np.uint8)
+    ws = np.ones(out * nb, np.float32)
+    xq = orc.jfill_bytes(7 * (out + in_), in_)
+    wqi, _ = orc.repack_x8(wq, ws, out, in_, True)
+    groups = range(out // 8) if out <= 64 else [0, 1, out // 8 - 1]
+    for gi in groups:
+        for b in range(nb):
+            out8 = orc.wi8_dot_x8(wqi, gi * nb * 128 + b * 128, xq, b * 32, True)
+            for L in range(8):
+                col = gi * 8 + L
+                assert out8[L] == orc.wi8_dot_q4(wq, col * half + b * 16, xq, b * 32)
+
+
+def test_x8_q8_tile_and_fold_match_row_major(orc):
+    rng = np.random.default_rng(21)
+    in_, out = 256, 32
+    w = rng.uniform(-0.5, 0.5, out * in_).astype(np.float32)
+    x = rng.uniform(-0.5, 0.5, in_).astype(np.float32)
+    wq, ws = orc.quantize_weight_q8u(w)  # unsigned, zero-point 128
+    wqi, wsi = orc.repack_x8(wq, ws, out, in_, False)
+    xq, xs, xsum = orc.quantize_act_i8(x, 1, in_)
+    y8 = orc.qmatmul_x8(xq, xs, xsum, wqi, wsi, in_, out, False)
+    codes = (wq.astype(np.int64) - 128).reshape(out, -1, 32)
+    dots = (codes * xq.reshape(-1, 32).astype(np.int64)).sum(axis=2)
+    ref = (dots * (xs.astype(np.float64)[None, :] * ws.reshape(out, -1))).sum(axis=1)
+    assert np.max(np.abs(y8 - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("in_,out", [(256, 64), (512, 128)])
+def test_x8_vs_composable(orc, in_, out):
+    # test/raster/quant/x8_simd_test.clj:24-33 (< 1e-3)
+    rng = np.random.default_rng(in_)
+    w = (rng.random(out * in_) - 0.5).astype(np.float32)
+    x = (rng.random(in_) - 0.5).astype(np.float32)
+    wq, ws = orc.quantize_weight_q4(w)
+    wqi, wsi = orc.repack_x8(wq, ws, out, in_, True)
+    xq, xs, xsum = orc.quantize_act_i8(x, 1, in_)
+    y8 = orc.qmatmul_x8(xq, xs, xsum, wqi, wsi, in_, out, True)
+    yc = orc.qmatmul_q4_composable(xq, xs, xsum, wq, ws, in_, out)
+    assert np.max(np.abs(y8 - yc)) < 1e-3
+
+
+# ---------------------------------------------------------------- signed q8_0 prefill
+def test_quantize_one_q8_roundtrip(orc):
+    # test/raster/quant/pack_test.clj:136-156
+    out, in_ = 4, 64
+    nb = in_ // 32
+    W = orc.jfill_uniform_centered(7, out * in_)
+    wp, ws = orc.quantize_one_q8(W, in_, out)
+    assert wp.size == out * in_ // 4 and ws.size == out * nb
+    q = wp.view(np.int8).astype(np.int64).reshape(out, in_)
+    d = np.repeat(ws.reshape(out, nb).astype(np.float64), 32, axis=1)
+    assert q.min() >= -127 and q.max() <= 127
+    assert np.all(np.abs(q * d - W.reshape(out, in_)) < 0.5 * d + 1e-7)
+    with pytest.raises(AssertionError):
+        orc.quantize_one_q8(np.zeros(30, np.float32), 30, 1)
+
+
+def test_quantize_one_q8_agrees_with_q8_quantize(orc):
+    # both are per-32-block d = max|w|/127 with Java rounding; only the packing differs
+    W = orc.jfill_gauss(5, 0.3, 8 * 128)
+    wp, ws = orc.quantize_one_q8(W, 128, 8)
+    codes, scales = orc.q8_quantize(W, 8, 128)
+    assert np.array_equal(wp.view(np.int8), codes)
+    assert np.array_equal(ws, scales)
+
+
+def test_quant_act_rows_matches_blockwise_quantizer(orc):
+    rng = np.random.default_rng(17)
+    T, in_ = 5, 128
+    x = rng.standard_normal(T * in_).astype(np.float32)
+    xp, xs = orc.quant_act_i8_rows(x, in_, T)
+    xq, xs2, _ = orc.quantize_act_i8(x, T, in_)
+    assert np.array_equal(xs, xs2)
+    assert np.array_equal(xp.view(np.int8), xq)
+
+
+def test_qmatmul_i8_gemm_exact_int_dots(orc):
+    rng = np.random.default_rng(19)
+    T, in_, out = 3, 128, 10
+    W = rng.standard_normal(out * in_).astype(np.float32)
+    x = rng.standard_normal(T * in_).astype(np.float32)
+    wp, ws = orc.quantize_one_q8(W, in_, out)
+    xp, xs = orc.quant_act_i8_rows(x, in_, T)
+    y = orc.qmatmul_i8_gemm(xp, xs, wp, ws, in_, out, T).reshape(T, out)
+    wq = wp.view(np.int8).astype(np.int64).reshape(out, -1, 32)
+    xq = xp.view(np.int8).astype(np.int64).reshape(T, -1, 32)
+    dots = np.einsum("obk,tbk->tob", wq, xq)
+    sc = ws.reshape(out, -1).astype(np.float64)[None] * xs.reshape(T, -1).astype(np.float64)[:, None]
+    ref = (dots * sc).sum(axis=2)
+    assert np.max(np.abs(y - ref)) <= 1e-6 * np.max(np.abs(ref))
+    # the dp4a GEMV is the same int core without scales
+    yi = orc.i8gemv_dp4a(wp, xp[: in_ // 4], in_ // 4, out)
+    assert np.array_equal(yi, wq.reshape(out, in_) @ xq[0].reshape(in_).astype(np.float64))
+
+
+def test_staged_equals_flat_with_power_of_two_scales(orc):
+    # staged_contract_device_test.clj:1-20: with power-of-two scales the per-block
+    # (staged) sum and the dequantized (flat) sum are the same exact number
+    rng = np.random.default_rng(23)
+    m, in_, out = 2, 128, 8
+    codes = rng.integers(-127, 128, out * in_).astype(np.int8)
+    scales = (2.0 ** rng.integers(-8, -2, out * in_ // 32)).astype(np.float32)
+    x = (rng.integers(-64, 64, m * in_) / 64.0).astype(np.float32)
+    y = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    Wd = orc.dequant_q8_dense(codes, scales, in_, out)
+    flat = orc.dense_matmul_nt_f64(x, Wd, m, in_, out)
+    assert np.array_equal(y.astype(np.float64), flat)
