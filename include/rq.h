@@ -1,0 +1,137 @@
+/*
+ * rq.h — C ABI of librq, the MI355X (gfx950) block-quantized matmul library.
+ *
+ * Plain C: scalars, pointers and sizes only. A JVM caller binds these symbols
+ * with Panama FFM downcalls (the reference reaches every native library that
+ * way: raster/linalg/blas.clj:162-186, raster/gpu/ze_runtime.clj:40-64); a
+ * Python caller uses ctypes. Reference paths below are inside replikativ/raster.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (RQ_OK == 0). On failure,
+ *    rq_last_error() gives a message for the calling thread
+ *    (mirrors ze-call! mapping non-zero driver status to ex-info,
+ *    raster/gpu/ze_runtime.clj:281-291).
+ *  - Weight layout is Raster's row-major [out x in] ("y = x . W^T"), one scale
+ *    per 32 consecutive `in` elements, scales row-major [out x in/32]
+ *    (raster/quant/train.clj:13-16, raster/compiler/backend/cpu/quant.clj:27-39).
+ *  - "Device pointer" arguments are HIP device allocations (from rq_buf_alloc
+ *    or any hipMalloc). "stream" is a hipStream_t passed as void*; NULL means
+ *    the null stream. Compute entry points are asynchronous on that stream and
+ *    never retain host pointers after they return.
+ *  - bf16 and fp16 travel as raw uint16 bits (Raster's :half convention,
+ *    raster/types/float16.clj:8). bf16 outputs are rounded to nearest even.
+ *  - y is fully overwritten, never accumulated into (the :overwrite buffer
+ *    write mode of raster/quant/op.clj:75-79).
+ */
+#ifndef RQ_H
+#define RQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RQ_VERSION 1
+
+/* status codes */
+enum {
+  RQ_OK = 0,
+  RQ_ERR_SHAPE = 1,   /* in % 32 != 0, out % 8 != 0 for x8 layouts, non-positive dims */
+  RQ_ERR_DTYPE = 2,   /* dtype/format not supported by this entry point */
+  RQ_ERR_NULL = 3,    /* required pointer is NULL */
+  RQ_ERR_OOM = 4,     /* device allocation failed */
+  RQ_ERR_HIP = 5,     /* a HIP runtime call failed (message has the HIP error) */
+  RQ_ERR_HANDLE = 6,  /* unknown, destroyed or foreign context / weight handle */
+  RQ_ERR_DEVICE = 7   /* no gfx950 device with that id */
+};
+
+/* element types */
+enum { RQ_F32 = 0, RQ_BF16 = 1, RQ_F16 = 2 };
+
+/* weight formats */
+enum {
+  RQ_Q8_0 = 0, /* signed int8 codes, W = scale * code (raster/quant/train.clj:13-16) */
+  RQ_Q4_0 = 1  /* unsigned nibbles, zero-point 8, lo = elem k, hi = elem k+16 of each
+                  32-block (raster/compiler/backend/cpu/quant.clj:27-31) */
+};
+
+typedef struct rq_ctx_s* rq_ctx;
+typedef struct rq_weight_s* rq_weight;
+
+/* ---- library / context ------------------------------------------------- */
+int rq_version(void);
+const char* rq_status_string(int status);
+const char* rq_last_error(void);
+/* Binds a context to a HIP device (raster/gpu/core.clj:243-257 make-session). */
+int rq_ctx_create(int device, rq_ctx* out);
+/* Idempotent per handle; destroys weights still owned by the context
+ * (raster/gpu/core.clj:259-293 close-session!). */
+int rq_ctx_destroy(rq_ctx ctx);
+/* Number of compute units and the wavefront size of the context's device. */
+int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz);
+
+/* ---- device memory and streams (raster/gpu/ze_runtime.clj:765-787 DeviceBuffer) */
+int rq_buf_alloc(rq_ctx ctx, size_t bytes, void** dptr);
+int rq_buf_free(rq_ctx ctx, void* dptr);
+int rq_upload(rq_ctx ctx, void* dst_dev, const void* src_host, size_t bytes, void* stream);
+int rq_download(rq_ctx ctx, void* dst_host, const void* src_dev, size_t bytes, void* stream);
+int rq_stream_create(rq_ctx ctx, void** stream);
+int rq_stream_destroy(rq_ctx ctx, void* stream);
+int rq_sync(rq_ctx ctx, void* stream);
+
+/* ---- resident quantized weights ------------------------------------------
+ * Created once from Raster's host arrays and kept in HBM (the :constant role of
+ * resident weights, raster/gpu/core.clj:889-940). */
+
+/* Q8_0 from qlinear-q8's arrays: codes int8[out*in], scales f32[out*in/32]
+ * (raster/quant/train.clj:88-89). */
+int rq_weight_create_q8(rq_ctx ctx, const int8_t* codes, const float* scales, int64_t out, int64_t in,
+                        rq_weight* w);
+/* Q8_0 from quantize-one-q8's packed words: wp int32[out*in/4] (4 little-endian
+ * int8 lanes each), ws f32[out*in/32] (raster/quant/pack.clj:210-236). */
+int rq_weight_create_q8_packed(rq_ctx ctx, const int32_t* wp, const float* ws, int64_t out, int64_t in,
+                               rq_weight* w);
+/* Q4_0 row-major: packed u8[out*in/2]; scales are f32 (Raster's Q4_0 ws,
+ * raster/compiler/backend/cpu/quant.clj:42-70) or fp16 bits (scale_dtype RQ_F16). */
+int rq_weight_create_q4(rq_ctx ctx, const uint8_t* packed, const void* scales, int scale_dtype, int64_t out,
+                        int64_t in, rq_weight* w);
+/* From the x8 column-interleaved repack-stream layout that raster.quant.op's
+ * qlinear-i8! / qlinear-i8-q8! take (raster/compiler/core/layout.clj:246-286):
+ * nibble = 1 for Q4_0 (wqi u8[(out/8)*(in/32)*128]), 0 for the unsigned
+ * zero-point-128 Q8 (wqi u8[(out/8)*(in/32)*256]); wsi f32[(out/8)*(in/32)*8].
+ * out % 8 == 0. Stored on the device in the row-major form. */
+int rq_weight_create_x8(rq_ctx ctx, const uint8_t* wqi, const float* wsi, int nibble, int64_t out, int64_t in,
+                        rq_weight* w);
+int rq_weight_destroy(rq_weight w);
+int rq_weight_info(rq_weight w, int* format, int64_t* out, int64_t* in, int* scale_dtype, size_t* device_bytes);
+/* Device pointers to the resident codes/packed bytes and scales (read-only). */
+int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
+
+/* ---- compute ---------------------------------------------------------------- */
+
+/* y[m,o] = sum_i dequant(W)[o,i] * x[m,i] for a resident weight; x is
+ * [m x in] of x_dtype (RQ_F32 or RQ_BF16), y is [m x out] of y_dtype (RQ_F32 or
+ * RQ_BF16), both device pointers, row-major. Replaces qlinear-q8
+ * (raster/quant/train.clj:77-108) and, for Q4_0, the f32-activation dequant
+ * GEMV; m <= 16 runs the HBM-bound GEMV kernels, larger m the MFMA GEMM.
+ * m == 0 is a no-op. */
+int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+               void* stream);
+
+/* Writes the dequantized f32 weight W[out*in] (device pointer) using the same
+ * device-side decode as the matmul kernels. Replaces dequant-q8-dense
+ * (raster/quant/train.clj:60-71) and the Q4_0 dequant
+ * (test/raster/compiler/backend/cpu/quant_encode_test.clj:9-24). */
+int rq_dequant(rq_ctx ctx, rq_weight w, float* w_out, void* stream);
+
+/* Host-array convenience with qlinear-q8's exact argument list
+ * (raster/quant/train.clj:88-89): uploads, runs rq_qmatmul, downloads, syncs. */
+int rq_qlinear_q8(rq_ctx ctx, const float* x, const int8_t* codes, const float* scales, int64_t m, int64_t in,
+                  int64_t out, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,14 @@
+"""raster_amd — MI355X (gfx950) block-quantized matmul for Raster.
+
+The product is librq.so (HIP kernels + the C ABI of include/rq.h); this package
+holds its sources (csrc/), the build script and a Python mirror of Raster's
+quantized-matmul call surface (quant.py).
+"""
+from . import _lib
+from .quant import (RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, Context, QWeight, RqError, context,
+                    dequant_q8_dense, qlinear_q8)
+
+__all__ = [
+    "Context", "QWeight", "RqError", "context", "qlinear_q8", "dequant_q8_dense",
+    "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
+]

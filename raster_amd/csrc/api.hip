@@ -1,0 +1,463 @@
+// api.hip — the C ABI declared in include/rq.h.
+//
+// Handles (contexts, weights, buffers) live in process-wide registries guarded
+// by one mutex, so a destroyed, double-freed or foreign handle is reported as
+// RQ_ERR_HANDLE instead of being dereferenced. Errors carry a message in a
+// thread-local string (rq_last_error).
+#include <mutex>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "rq_internal.h"
+
+namespace rq {
+
+struct Ctx {
+  uint32_t magic;
+  int device;
+  int cu_count;
+  int wave_size;
+  int clock_khz;
+  std::unordered_set<Weight*> weights;
+  std::unordered_set<void*> buffers;
+};
+
+static constexpr uint32_t kCtxMagic = 0x52514358u;     // "RQCX"
+static constexpr uint32_t kWeightMagic = 0x52515754u;  // "RQWT"
+
+static std::mutex g_mu;
+static std::unordered_set<Ctx*> g_ctxs;
+static std::unordered_set<Weight*> g_weights;
+static thread_local std::string t_err;
+
+static int fail(int status, const std::string& msg) {
+  t_err = msg;
+  return status;
+}
+
+static int hip_fail(hipError_t e, const char* what) {
+  return fail(RQ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define RQ_HIP(call, what)                   \
+  do {                                       \
+    hipError_t e_ = (call);                  \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+static bool live_ctx(Ctx* c) { return c && g_ctxs.count(c) && c->magic == kCtxMagic; }
+static bool live_weight(Weight* w) { return w && g_weights.count(w) && w->magic == kWeightMagic; }
+
+static int check_ctx(Ctx* c) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_ctx(c)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_ctx");
+  return RQ_OK;
+}
+
+static int set_device(Ctx* c) {
+  RQ_HIP(hipSetDevice(c->device), "hipSetDevice");
+  return RQ_OK;
+}
+
+static int check_shape(int64_t out, int64_t in) {
+  if (out <= 0 || in <= 0) return fail(RQ_ERR_SHAPE, "out and in must be positive");
+  if (in % 32 != 0) return fail(RQ_ERR_SHAPE, "in=" + std::to_string(in) + " not a multiple of 32");
+  if (in > (int64_t)1 << 30 || out > (int64_t)1 << 30) return fail(RQ_ERR_SHAPE, "dimension too large");
+  return RQ_OK;
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Allocates the weight and uploads row-major codes/packed bytes and scales.
+static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t in, const void* qhost,
+                       const void* shost, rq_weight* wout) {
+  const size_t qbytes = format == RQ_Q8_0 ? (size_t)(out * in) : (size_t)(out * in / 2);
+  const size_t sbytes = (size_t)(out * (in / 32)) * (scale_dtype == RQ_F16 ? 2 : 4);
+  const size_t total = align256(qbytes) + align256(sbytes);
+  if (int s = set_device(c)) return s;
+  void* base = nullptr;
+  hipError_t e = hipMalloc(&base, total);
+  if (e != hipSuccess || !base) {
+    (void)hipGetLastError();
+    return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(total) + " bytes for weight failed");
+  }
+  Weight* w = new (std::nothrow) Weight();
+  if (!w) {
+    (void)hipFree(base);
+    return fail(RQ_ERR_OOM, "host allocation failed");
+  }
+  w->magic = kWeightMagic;
+  w->format = format;
+  w->scale_dtype = scale_dtype;
+  w->device = c->device;
+  w->out = out;
+  w->in = in;
+  w->base = base;
+  w->q = static_cast<uint8_t*>(base);
+  w->scales = static_cast<uint8_t*>(base) + align256(qbytes);
+  w->bytes = total;
+  w->ctx = c;
+  e = hipMemcpy(w->q, qhost, qbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(w->scales, shost, sbytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(base);
+    delete w;
+    return hip_fail(e, "weight upload");
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!live_ctx(c)) {
+      (void)hipFree(base);
+      delete w;
+      return fail(RQ_ERR_HANDLE, "rq_ctx destroyed during weight creation");
+    }
+    g_weights.insert(w);
+    c->weights.insert(w);
+  }
+  *wout = reinterpret_cast<rq_weight>(w);
+  return RQ_OK;
+}
+
+static void free_weight_locked(Weight* w) {
+  (void)hipSetDevice(w->device);
+  (void)hipFree(w->base);
+  w->magic = 0;
+  g_weights.erase(w);
+  delete w;
+}
+
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" {
+
+int rq_version(void) { return RQ_VERSION; }
+
+const char* rq_status_string(int s) {
+  switch (s) {
+    case RQ_OK: return "ok";
+    case RQ_ERR_SHAPE: return "bad shape";
+    case RQ_ERR_DTYPE: return "unsupported dtype or format";
+    case RQ_ERR_NULL: return "null pointer";
+    case RQ_ERR_OOM: return "out of device memory";
+    case RQ_ERR_HIP: return "HIP runtime error";
+    case RQ_ERR_HANDLE: return "invalid handle";
+    case RQ_ERR_DEVICE: return "no gfx950 device";
+    default: return "unknown status";
+  }
+}
+
+const char* rq_last_error(void) { return t_err.c_str(); }
+
+int rq_ctx_create(int device, rq_ctx* out) {
+  if (!out) return fail(RQ_ERR_NULL, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return fail(RQ_ERR_DEVICE, "no HIP device visible");
+  }
+  if (device < 0 || device >= n) return fail(RQ_ERR_DEVICE, "device id out of range");
+  hipDeviceProp_t p;
+  RQ_HIP(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
+  if (std::string(p.gcnArchName).rfind("gfx950", 0) != 0)
+    return fail(RQ_ERR_DEVICE, std::string("device is ") + p.gcnArchName + ", librq is built for gfx950");
+  Ctx* c = new (std::nothrow) Ctx();
+  if (!c) return fail(RQ_ERR_OOM, "host allocation failed");
+  c->magic = kCtxMagic;
+  c->device = device;
+  c->cu_count = p.multiProcessorCount;
+  c->wave_size = p.warpSize;
+  c->clock_khz = p.clockRate;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_ctxs.insert(c);
+  }
+  *out = reinterpret_cast<rq_ctx>(c);
+  return RQ_OK;
+}
+
+int rq_ctx_destroy(rq_ctx h) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_ctx(c)) return fail(RQ_ERR_HANDLE, "unknown or already destroyed rq_ctx");
+  (void)hipSetDevice(c->device);
+  for (Weight* w : c->weights) free_weight_locked(w);
+  for (void* b : c->buffers) (void)hipFree(b);
+  c->magic = 0;
+  g_ctxs.erase(c);
+  delete c;
+  return RQ_OK;
+}
+
+int rq_ctx_device_info(rq_ctx h, int* cu_count, int* wave_size, int* clock_khz) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (cu_count) *cu_count = c->cu_count;
+  if (wave_size) *wave_size = c->wave_size;
+  if (clock_khz) *clock_khz = c->clock_khz;
+  return RQ_OK;
+}
+
+int rq_buf_alloc(rq_ctx h, size_t bytes, void** dptr) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!dptr) return fail(RQ_ERR_NULL, "dptr is NULL");
+  *dptr = nullptr;
+  if (bytes == 0) return fail(RQ_ERR_SHAPE, "zero-byte buffer");
+  if (int s = set_device(c)) return s;
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  c->buffers.insert(p);
+  *dptr = p;
+  return RQ_OK;
+}
+
+int rq_buf_free(rq_ctx h, void* dptr) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_ctx(c)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_ctx");
+  if (!dptr || !c->buffers.count(dptr)) return fail(RQ_ERR_HANDLE, "pointer is not a live rq_buf of this context");
+  (void)hipSetDevice(c->device);
+  c->buffers.erase(dptr);
+  RQ_HIP(hipFree(dptr), "hipFree");
+  return RQ_OK;
+}
+
+int rq_upload(rq_ctx h, void* dst, const void* src, size_t bytes, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!dst || !src) return fail(RQ_ERR_NULL, "NULL pointer");
+  if (int s = set_device(c)) return s;
+  RQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream), "hipMemcpyAsync H2D");
+  RQ_HIP(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+  return RQ_OK;
+}
+
+int rq_download(rq_ctx h, void* dst, const void* src, size_t bytes, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!dst || !src) return fail(RQ_ERR_NULL, "NULL pointer");
+  if (int s = set_device(c)) return s;
+  RQ_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream), "hipMemcpyAsync D2H");
+  RQ_HIP(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+  return RQ_OK;
+}
+
+int rq_stream_create(rq_ctx h, void** stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!stream) return fail(RQ_ERR_NULL, "stream is NULL");
+  if (int s = set_device(c)) return s;
+  hipStream_t st;
+  RQ_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = (void*)st;
+  return RQ_OK;
+}
+
+int rq_stream_destroy(rq_ctx h, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!stream) return fail(RQ_ERR_NULL, "stream is NULL");
+  RQ_HIP(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+  return RQ_OK;
+}
+
+int rq_sync(rq_ctx h, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (int s = set_device(c)) return s;
+  RQ_HIP(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+  return RQ_OK;
+}
+
+int rq_weight_create_q8(rq_ctx h, const int8_t* codes, const float* scales, int64_t out, int64_t in,
+                        rq_weight* w) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!codes || !scales || !w) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  return make_weight(c, RQ_Q8_0, RQ_F32, out, in, codes, scales, w);
+}
+
+int rq_weight_create_q8_packed(rq_ctx h, const int32_t* wp, const float* ws, int64_t out, int64_t in,
+                               rq_weight* w) {
+  // four little-endian int8 lanes per word: the words' bytes are the codes in order
+  return rq_weight_create_q8(h, reinterpret_cast<const int8_t*>(wp), ws, out, in, w);
+}
+
+int rq_weight_create_q4(rq_ctx h, const uint8_t* packed, const void* scales, int scale_dtype, int64_t out,
+                        int64_t in, rq_weight* w) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!packed || !scales || !w) return fail(RQ_ERR_NULL, "NULL argument");
+  if (scale_dtype != RQ_F32 && scale_dtype != RQ_F16) return fail(RQ_ERR_DTYPE, "Q4 scales must be f32 or f16");
+  if (int s = check_shape(out, in)) return s;
+  return make_weight(c, RQ_Q4_0, scale_dtype, out, in, packed, scales, w);
+}
+
+int rq_weight_create_x8(rq_ctx h, const uint8_t* wqi, const float* wsi, int nibble, int64_t out, int64_t in,
+                        rq_weight* w) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!wqi || !wsi || !w) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  if (out % 8 != 0) return fail(RQ_ERR_SHAPE, "x8 layout needs out % 8 == 0");
+  // Invert the column interleave of raster/compiler/core/layout.clj:246-286
+  // (tile 8, k-group 4, 8 input groups per 32-block).
+  const int64_t nb = in / 32, ng = out / 8;
+  std::vector<float> ws((size_t)(out * nb));
+  for (int64_t g = 0; g < ng; g++)
+    for (int64_t b = 0; b < nb; b++)
+      for (int r = 0; r < 8; r++) ws[(size_t)((g * 8 + r) * nb + b)] = wsi[g * nb * 8 + b * 8 + r];
+  if (nibble) {
+    std::vector<uint8_t> packed((size_t)(out * in / 2));
+    for (int64_t g = 0; g < ng; g++)
+      for (int64_t b = 0; b < nb; b++)
+        for (int ig = 0; ig < 8; ig++)
+          for (int j = 0; j < 16; j++) {
+            const uint8_t byte = wqi[g * nb * 128 + b * 128 + ig * 16 + j];
+            const int e = ig * 4 + j % 4;           // element of the block
+            const int64_t col = g * 8 + j / 4;      // low nibble column; high = col + 4
+            const int64_t cols[2] = {col, col + 4};
+            const uint8_t nibs[2] = {(uint8_t)(byte & 0xF), (uint8_t)(byte >> 4)};
+            for (int t = 0; t < 2; t++) {
+              uint8_t& dst = packed[(size_t)(cols[t] * (in / 2) + b * 16 + (e < 16 ? e : e - 16))];
+              dst = e < 16 ? (uint8_t)((dst & 0xF0) | nibs[t]) : (uint8_t)((dst & 0x0F) | (nibs[t] << 4));
+            }
+          }
+    return make_weight(c, RQ_Q4_0, RQ_F32, out, in, packed.data(), ws.data(), w);
+  }
+  // byte-direct unsigned codes with zero-point 128 -> signed codes (u - 128)
+  std::vector<int8_t> codes((size_t)(out * in));
+  for (int64_t g = 0; g < ng; g++)
+    for (int64_t b = 0; b < nb; b++)
+      for (int ig = 0; ig < 8; ig++)
+        for (int j = 0; j < 32; j++) {
+          const uint8_t u = wqi[g * nb * 256 + b * 256 + ig * 32 + j];
+          const int64_t row = g * 8 + j / 4;
+          const int e = ig * 4 + j % 4;
+          codes[(size_t)(row * in + b * 32 + e)] = (int8_t)((int)u - 128);
+        }
+  return make_weight(c, RQ_Q8_0, RQ_F32, out, in, codes.data(), ws.data(), w);
+}
+
+int rq_weight_destroy(rq_weight h) {
+  Weight* w = reinterpret_cast<Weight*>(h);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_weight(w)) return fail(RQ_ERR_HANDLE, "unknown or already destroyed rq_weight");
+  if (live_ctx(w->ctx)) w->ctx->weights.erase(w);
+  free_weight_locked(w);
+  return RQ_OK;
+}
+
+int rq_weight_info(rq_weight h, int* format, int64_t* out, int64_t* in, int* scale_dtype, size_t* bytes) {
+  Weight* w = reinterpret_cast<Weight*>(h);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_weight(w)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_weight");
+  if (format) *format = w->format;
+  if (out) *out = w->out;
+  if (in) *in = w->in;
+  if (scale_dtype) *scale_dtype = w->scale_dtype;
+  if (bytes) *bytes = w->bytes;
+  return RQ_OK;
+}
+
+int rq_weight_device_ptrs(rq_weight h, const void** qdata, const void** scales) {
+  Weight* w = reinterpret_cast<Weight*>(h);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_weight(w)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_weight");
+  if (qdata) *qdata = w->q;
+  if (scales) *scales = w->scales;
+  return RQ_OK;
+}
+
+static int lookup(rq_ctx h, rq_weight wh, Ctx** c, Weight* copy) {
+  Ctx* cc = reinterpret_cast<Ctx*>(h);
+  Weight* w = reinterpret_cast<Weight*>(wh);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!live_ctx(cc)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_ctx");
+  if (!live_weight(w)) return fail(RQ_ERR_HANDLE, "unknown or destroyed rq_weight");
+  if (w->device != cc->device) return fail(RQ_ERR_HANDLE, "weight lives on another device");
+  *c = cc;
+  *copy = *w;
+  return RQ_OK;
+}
+
+int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m, void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
+  if (!x || !y) return fail(RQ_ERR_NULL, "x or y is NULL");
+  if (x_dtype != RQ_F32 && x_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "x must be f32 or bf16");
+  if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
+  if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
+  if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  if (int s = set_device(c)) return s;
+  MatmulArgs a;
+  a.q = w.q;
+  a.scales = w.scales;
+  a.scale_dtype = w.scale_dtype;
+  a.format = w.format;
+  a.x = x;
+  a.x_dtype = x_dtype;
+  a.y = y;
+  a.y_dtype = y_dtype;
+  a.m = m;
+  a.k = w.in;
+  a.n = w.out;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = m <= 16 ? launch_gemv(a) : launch_gemm(a, c->cu_count);
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return RQ_OK;
+}
+
+int rq_dequant(rq_ctx h, rq_weight wh, float* w_out, void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (!w_out) return fail(RQ_ERR_NULL, "w_out is NULL");
+  if (((uintptr_t)w_out & 15) != 0) return fail(RQ_ERR_SHAPE, "w_out must be 16-byte aligned");
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_dequant(w, w_out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dequant launch");
+  return RQ_OK;
+}
+
+int rq_qlinear_q8(rq_ctx h, const float* x, const int8_t* codes, const float* scales, int64_t m, int64_t in,
+                  int64_t out, float* y) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!x || !codes || !scales || !y) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  rq_weight w = nullptr;
+  if (int s = rq_weight_create_q8(h, codes, scales, out, in, &w)) return s;
+  void *dx = nullptr, *dy = nullptr;
+  int s = rq_buf_alloc(h, (size_t)(m * in) * 4, &dx);
+  if (!s) s = rq_buf_alloc(h, (size_t)(m * out) * 4, &dy);
+  if (!s) s = rq_upload(h, dx, x, (size_t)(m * in) * 4, nullptr);
+  if (!s) s = rq_qmatmul(h, w, dx, RQ_F32, dy, RQ_F32, m, nullptr);
+  if (!s) s = rq_download(h, y, dy, (size_t)(m * out) * 4, nullptr);
+  std::string keep = s ? t_err : std::string();
+  if (dx) rq_buf_free(h, dx);
+  if (dy) rq_buf_free(h, dy);
+  rq_weight_destroy(w);
+  if (s) t_err = keep;
+  return s;
+}
+
+}  // extern "C"

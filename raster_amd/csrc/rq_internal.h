@@ -1,0 +1,86 @@
+// rq_internal.h — shared definitions for librq's HIP translation units.
+// gfx950 (CDNA4) only: wave64, MFMA bf16/i8, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/rq.h"
+
+namespace rq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Resident weight, stored in HBM in Raster's row-major layout:
+//   Q8_0: codes int8[out*in] then scales f32[out*in/32]
+//   Q4_0: packed u8[out*in/2] (lo nibble = elem k, hi = elem k+16 per 32-block)
+//         then scales f32 or fp16 [out*in/32]
+// Both arrays live in one allocation, each 256-byte aligned.
+struct Weight {
+  uint32_t magic;
+  int format;       // RQ_Q8_0 / RQ_Q4_0
+  int scale_dtype;  // RQ_F32 / RQ_F16
+  int device;
+  int64_t out, in;
+  void* base;       // device allocation
+  uint8_t* q;       // codes / packed nibbles
+  void* scales;
+  size_t bytes;
+  struct Ctx* ctx;
+};
+
+// Launch descriptor for the matmul kernels.
+struct MatmulArgs {
+  const uint8_t* q;
+  const void* scales;
+  int scale_dtype;
+  int format;
+  const void* x;
+  int x_dtype;
+  void* y;
+  int y_dtype;
+  int64_t m, k, n;  // m activation rows, k = in, n = out
+  hipStream_t stream;
+};
+
+// Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
+hipError_t launch_gemv(const MatmulArgs& a);
+hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
+hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
+
+// ---- device helpers shared by every kernel that decodes weights -----------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even f32 -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <typename ST>
+__device__ __forceinline__ float load_scale(const ST* s, int64_t i);
+template <>
+__device__ __forceinline__ float load_scale<float>(const float* s, int64_t i) { return s[i]; }
+template <>
+__device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* s, int64_t i) {
+  return f16_bits_to_f32(s[i]);
+}
+
+// Signed Q8 code j (0..3) of a little-endian dword, as an exact float.
+__device__ __forceinline__ float q8_code(uint32_t d, int j) { return (float)(int8_t)(d >> (8 * j)); }
+// Q4 nibble value q (0..15) of byte j of a dword; hi selects the high nibble.
+__device__ __forceinline__ float q4_nib(uint32_t d, int j, bool hi) {
+  return (float)((d >> (8 * j + (hi ? 4 : 0))) & 0xFu);
+}
+
+}  // namespace rq

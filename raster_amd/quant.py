@@ -1,0 +1,224 @@
+"""Host-side mirror of Raster's quantized-matmul call surface over librq.
+
+Names, argument order and result shapes follow the reference functions
+(paths inside replikativ/raster):
+
+  qlinear_q8(x, codes, scales, m, in_, out) -> y[m*out]   raster/quant/train.clj:77-108
+  dequant_q8_dense(codes, scales, in_, out) -> W[out*in]  raster/quant/train.clj:60-71
+
+plus the resident-weight object the GPU path needs (`QWeight`, the :constant
+weights of raster/gpu/core.clj:889-940) and a per-device `Context`
+(make-session, raster/gpu/core.clj:243-257). Every compute call goes through the
+C ABI of include/rq.h; there is no CPU fallback. Device arrays are torch CUDA
+tensors (plumbing only: memory and streams), host arrays are numpy.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+
+import numpy as np
+
+from . import _lib
+from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, RqError, call, lib
+
+__all__ = [
+    "Context", "QWeight", "RqError", "context", "qlinear_q8", "dequant_q8_dense",
+    "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
+]
+
+
+def _np_ptr(a: np.ndarray):
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("host arrays must be C-contiguous")
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Context:
+    """A librq context bound to one HIP device (raster/gpu/core.clj:243-293)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        call("rq_ctx_create", device, C.byref(h))
+        self.handle = h
+        self.device = device
+
+    def device_info(self) -> dict:
+        cu, ws, clk = C.c_int(), C.c_int(), C.c_int()
+        call("rq_ctx_device_info", self.handle, C.byref(cu), C.byref(ws), C.byref(clk))
+        return {"cu_count": cu.value, "wave_size": ws.value, "clock_khz": clk.value}
+
+    def sync(self, stream=None) -> None:
+        call("rq_sync", self.handle, _stream_ptr(stream))
+
+    def close(self) -> None:
+        if self.handle:
+            call("rq_ctx_destroy", self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+_ctx_lock = threading.Lock()
+_contexts: dict[int, Context] = {}
+
+
+def context(device: int = 0) -> Context:
+    """Process-wide default context per device."""
+    with _ctx_lock:
+        c = _contexts.get(device)
+        if c is None or c.handle is None:
+            c = Context(device)
+            _contexts[device] = c
+        return c
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return C.c_void_p(stream)
+    return C.c_void_p(stream.cuda_stream)  # torch.cuda.Stream
+
+
+def _dtype_code(t) -> int:
+    import torch
+
+    if t.dtype == torch.float32:
+        return RQ_F32
+    if t.dtype == torch.bfloat16:
+        return RQ_BF16
+    raise TypeError(f"activations/outputs must be float32 or bfloat16, got {t.dtype}")
+
+
+class QWeight:
+    """A resident block-quantized weight [out x in] in HBM (one scale per 32 of `in`)."""
+
+    def __init__(self, ctx: Context, handle: C.c_void_p):
+        self.ctx = ctx
+        self.handle = handle
+        fmt, out, in_, sdt, nbytes = C.c_int(), C.c_int64(), C.c_int64(), C.c_int(), C.c_size_t()
+        call("rq_weight_info", handle, C.byref(fmt), C.byref(out), C.byref(in_), C.byref(sdt), C.byref(nbytes))
+        self.format, self.out, self.in_ = fmt.value, out.value, in_.value
+        self.scale_dtype, self.device_bytes = sdt.value, nbytes.value
+
+    # ---- constructors -------------------------------------------------------
+    @classmethod
+    def q8(cls, codes, scales, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """From qlinear-q8's arrays: int8 codes[out*in], f32 scales[out*in/32]."""
+        ctx = ctx or context()
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        _need(codes.size == out * in_ and scales.size == out * (in_ // 32), "array sizes do not match out x in")
+        h = C.c_void_p()
+        call("rq_weight_create_q8", ctx.handle, _np_ptr(codes), _np_ptr(scales), out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    @classmethod
+    def q8_packed(cls, wp, ws, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """From quantize-one-q8's int32-packed words (raster/quant/pack.clj:210-236)."""
+        ctx = ctx or context()
+        wp = np.ascontiguousarray(wp, np.int32)
+        ws = np.ascontiguousarray(ws, np.float32)
+        _need(wp.size == out * in_ // 4 and ws.size == out * (in_ // 32), "array sizes do not match out x in")
+        h = C.c_void_p()
+        call("rq_weight_create_q8_packed", ctx.handle, _np_ptr(wp), _np_ptr(ws), out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    @classmethod
+    def q4(cls, packed, scales, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """Row-major Q4_0: packed u8[out*in/2]; scales f32 or fp16 (np.float16 / uint16 bits)."""
+        ctx = ctx or context()
+        packed = np.ascontiguousarray(packed, np.uint8)
+        scales = np.asarray(scales)
+        if scales.dtype in (np.float16, np.uint16):
+            scales, sdt = np.ascontiguousarray(scales).view(np.uint16), RQ_F16
+        else:
+            scales, sdt = np.ascontiguousarray(scales, np.float32), RQ_F32
+        _need(packed.size == out * in_ // 2 and scales.size == out * (in_ // 32), "array sizes do not match out x in")
+        h = C.c_void_p()
+        call("rq_weight_create_q4", ctx.handle, _np_ptr(packed), _np_ptr(scales), sdt, out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    @classmethod
+    def x8(cls, wqi, wsi, nibble: bool, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """From the repack-stream x8 layout of raster/compiler/core/layout.clj:246-286."""
+        ctx = ctx or context()
+        wqi = np.ascontiguousarray(wqi).view(np.uint8)
+        wsi = np.ascontiguousarray(wsi, np.float32)
+        h = C.c_void_p()
+        call("rq_weight_create_x8", ctx.handle, _np_ptr(wqi), _np_ptr(wsi), int(bool(nibble)), out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    # ---- compute --------------------------------------------------------------
+    def matmul(self, x, y=None, out_dtype=None, stream=None):
+        """y[m, out] = x[m, in] . dequant(W)^T on the device (x: torch f32/bf16 CUDA tensor)."""
+        import torch
+
+        _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous CUDA tensor")
+        _need(x.numel() % self.in_ == 0, "x.numel() must be a multiple of in")
+        m = x.numel() // self.in_
+        if y is None:
+            y = torch.empty((m, self.out), dtype=out_dtype or torch.float32, device=x.device)
+        _need(y.is_cuda and y.is_contiguous() and y.numel() == m * self.out, "y must be a contiguous [m, out] CUDA tensor")
+        if stream is None:
+            stream = torch.cuda.current_stream(x.device)
+        call("rq_qmatmul", self.ctx.handle, self.handle, C.c_void_p(x.data_ptr()), _dtype_code(x),
+             C.c_void_p(y.data_ptr()), _dtype_code(y), m, _stream_ptr(stream))
+        return y
+
+    def dequant(self, stream=None):
+        """Dequantized f32 W[out, in] computed on the device."""
+        import torch
+
+        w = torch.empty((self.out, self.in_), dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        if stream is None:
+            stream = torch.cuda.current_stream(w.device)
+        call("rq_dequant", self.ctx.handle, self.handle, C.c_void_p(w.data_ptr()), _stream_ptr(stream))
+        return w
+
+    def device_ptrs(self):
+        q, s = C.c_void_p(), C.c_void_p()
+        call("rq_weight_device_ptrs", self.handle, C.byref(q), C.byref(s))
+        return q.value, s.value
+
+    def destroy(self) -> None:
+        if self.handle:
+            call("rq_weight_destroy", self.handle)
+            self.handle = None
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+# ---- Raster-named host-array entry points -------------------------------------
+
+def qlinear_q8(x, codes, scales, m: int, in_: int, out: int, ctx: Context | None = None) -> np.ndarray:
+    """raster.quant.train/qlinear-q8: y[m*out] = x[m*in] . dequant(codes, scales)^T, on the GPU."""
+    ctx = ctx or context()
+    x = np.ascontiguousarray(x, np.float32)
+    codes = np.ascontiguousarray(codes, np.int8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    if in_ % 32 != 0:
+        raise AssertionError(f"in={in_} not a multiple of 32")
+    _need(x.size == m * in_ and codes.size == out * in_ and scales.size == out * (in_ // 32), "array sizes")
+    y = np.empty(m * out, np.float32)
+    call("rq_qlinear_q8", ctx.handle, _np_ptr(x), _np_ptr(codes), _np_ptr(scales), m, in_, out, _np_ptr(y))
+    return y
+
+
+def dequant_q8_dense(codes, scales, in_: int, out: int, ctx: Context | None = None) -> np.ndarray:
+    """raster.quant.train/dequant-q8-dense, decoded on the GPU: f32 W[out*in]."""
+    w = QWeight.q8(codes, scales, out, in_, ctx)
+    try:
+        import torch
+
+        return w.dequant().cpu().numpy().ravel()
+    finally:
+        w.destroy()

@@ -1,0 +1,337 @@
+"""GPU parity: the gfx950 kernels behind librq against the C oracle.
+
+Bars (from the workload definition):
+  * dequantized weights: bit-exact (IEEE f32 of scale * code);
+  * outputs: normwise max|y - ref| / max|ref| < 1e-3 for f32 activations and
+    < 1e-2 for bf16 activations or bf16 outputs
+    (normwise as in test/raster/dl/decoder_layer_gpu_test.clj:17 of the reference).
+Full-size configurations are checked on a subset of output rows where the
+scalar oracle would otherwise take minutes; the subset always includes the
+first and last rows and a spread in between.
+"""
+import numpy as np
+import pytest
+
+from raster_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 1e-2
+
+
+def note(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    if not t.cuda.is_available():
+        pytest.skip("no GPU")
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import raster_amd
+
+    c = raster_amd.Context(0)
+    yield c
+    c.close()
+
+
+def rows_subset(n, count):
+    if n <= count:
+        return np.arange(n)
+    idx = np.unique(np.concatenate([[0, n - 1], np.linspace(0, n - 1, count - 2).astype(np.int64)]))
+    return idx
+
+
+def dev(torch, a, dtype="f32"):
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    return t.to(torch.bfloat16) if dtype == "bf16" else t
+
+
+def run(torch, w, x_np, m, xdt, ydt):
+    import raster_amd
+
+    x = dev(torch, x_np, xdt).reshape(m, w.in_)
+    y = w.matmul(x, out_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+# ---------------------------------------------------------------- dequant tiles
+@pytest.mark.parametrize("out,in_", [(4096, 4096), (37, 96)])
+def test_dequant_q8_bit_exact(torch, ctx, orc, out, in_):
+    import raster_amd
+
+    codes, scales = wl.q8_weights(out, in_, seed=0)
+    note(f"dequant q8 {out}x{in_}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    got = w.dequant().cpu().numpy().ravel()
+    w.destroy()
+    ref = orc.dequant_q8_dense(codes, scales, in_, out)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("scale_kind", ["f16", "f32"])
+@pytest.mark.parametrize("out,in_", [(14336, 4096), (13, 64)])
+def test_dequant_q4_bit_exact(torch, ctx, orc, out, in_, scale_kind):
+    import raster_amd
+
+    packed, sc16 = wl.q4_weights(out, in_, seed=0)
+    scales = sc16 if scale_kind == "f16" else sc16.view(np.float16).astype(np.float32)
+    note(f"dequant q4 {out}x{in_} {scale_kind}")
+    w = raster_amd.QWeight.q4(packed, scales if scale_kind == "f32" else sc16.view(np.float16), out, in_, ctx)
+    got = w.dequant().cpu().numpy().ravel()
+    w.destroy()
+    ref = orc.dequant_q4(packed, sc16 if scale_kind == "f16" else scales, in_, out)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_q8_extreme_codes(torch, ctx, orc):
+    import raster_amd
+
+    out, in_ = 8, 256
+    codes = np.tile(np.array([-128, 127, 0, -1, 1, -127, 64, -64], np.int8), out * in_ // 8)
+    scales = np.full(out * in_ // 32, 0.0173, np.float32)
+    scales[3] = 0.0
+    scales[5] = np.float32(3.4e38) / 128
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    got = w.dequant().cpu().numpy().ravel()
+    w.destroy()
+    ref = orc.dequant_q8_dense(codes, scales, in_, out)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMV (m <= 16)
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 16])
+def test_gemv_q8_f32(torch, ctx, orc, m):
+    import raster_amd
+
+    out, in_ = (4096, 4096) if m == 1 else (300, 1024)
+    codes, scales = wl.q8_weights(out, in_, seed=m)
+    x = wl.activations(m, in_, seed=10 + m)
+    note(f"gemv q8 f32 m={m} {out}x{in_}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    ref = orc.qlinear_q8(x, codes, scales, m, in_, out).reshape(m, out)
+    assert orc.normwise_relerr(y, ref) < TOL_F32
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_gemv_q4_f16_scales_c3(torch, ctx, orc, m):
+    import raster_amd
+
+    out, in_ = 14336, 4096
+    packed, sc16 = wl.q4_weights(out, in_, seed=3)
+    x = wl.activations(m, in_, seed=30 + m)
+    note(f"gemv q4 f32 m={m} {out}x{in_}")
+    w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    rows = rows_subset(out, 1024 if m > 1 else out)
+    pk = packed.reshape(out, in_ // 2)[rows].ravel()
+    sc = sc16.reshape(out, in_ // 32)[rows].ravel()
+    ref = orc.qlinear_q4(x, pk, sc, m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y[:, rows], ref) < TOL_F32
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("m", [1, 7])
+def test_gemv_bf16_in_bf16_out(torch, ctx, orc, fmt, m):
+    import raster_amd
+
+    out, in_ = 520, 8192
+    x = wl.activations(m, in_, seed=50 + m, dtype="bf16")
+    note(f"gemv {fmt} bf16 m={m} {out}x{in_}")
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=5)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        ref = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=5)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+        ref = orc.qlinear_q4(x, packed, sc16, m, in_, out)
+    y = run(torch, w, x, m, "bf16", "bf16")
+    y32 = run(torch, w, x, m, "bf16", "f32")
+    w.destroy()
+    ref = ref.reshape(m, out)
+    assert orc.normwise_relerr(y, ref) < TOL_BF16
+    assert orc.normwise_relerr(y32, ref) < TOL_F32
+    # the bf16 output is the RNE rounding of the kernel's own f32 result
+    assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y))
+
+
+# ---------------------------------------------------------------- GEMM (m > 16)
+def test_gemm_q8_bf16_c2(torch, ctx, orc):
+    import raster_amd
+
+    m, in_, out = 512, 4096, 11008
+    codes, scales = wl.q8_weights(out, in_, seed=2)
+    x = wl.activations(m, in_, seed=20, dtype="bf16")
+    note(f"gemm q8 bf16 m={m} {out}x{in_}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    y = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    rows = rows_subset(out, 192)
+    cs = codes.reshape(out, in_)[rows].ravel()
+    ss = scales.reshape(out, in_ // 32)[rows].ravel()
+    ref = orc.qlinear_q8(x, cs, ss, m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y[:, rows], ref) < TOL_BF16
+
+
+@pytest.mark.parametrize("m,in_,out", [(17, 32, 8), (129, 96, 100), (300, 256, 130), (64, 1024, 257)])
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_gemm_ragged_f32(torch, ctx, orc, m, in_, out, fmt):
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=m + out)
+    note(f"gemm {fmt} f32 m={m} {out}x{in_}")
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=out)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        ref = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=out)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+        ref = orc.qlinear_q4(x, packed, sc16, m, in_, out)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    assert orc.normwise_relerr(y, ref.reshape(m, out)) < TOL_F32
+
+
+def test_gemm_q4_bf16_m256(torch, ctx, orc):
+    import raster_amd
+
+    m, in_, out = 256, 8192, 1536
+    packed, sc16 = wl.q4_weights(out, in_, seed=7)
+    x = wl.activations(m, in_, seed=70, dtype="bf16")
+    note(f"gemm q4 bf16 m={m} {out}x{in_}")
+    w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+    y = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    rows = rows_subset(out, 128)
+    pk = packed.reshape(out, in_ // 2)[rows].ravel()
+    sc = sc16.reshape(out, in_ // 32)[rows].ravel()
+    ref = orc.qlinear_q4(x, pk, sc, m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y[:, rows], ref) < TOL_BF16
+
+
+def test_zero_scale_blocks_and_zero_rows(torch, ctx, orc):
+    import raster_amd
+
+    m, in_, out = 40, 128, 24
+    codes, scales = wl.q8_weights(out, in_, seed=9)
+    scales.reshape(out, -1)[5, :] = 0.0
+    scales.reshape(out, -1)[:, 2] = 0.0
+    x = wl.activations(m, in_, seed=90)
+    x.reshape(m, in_)[3] = 0.0
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    for mm in (m, 4):
+        note(f"zero-scale q8 m={mm}")
+        y = run(torch, w, x[: mm * in_], mm, "f32", "f32")
+        ref = orc.qlinear_q8(x[: mm * in_], codes, scales, mm, in_, out).reshape(mm, out)
+        assert orc.normwise_relerr(y, ref) < TOL_F32
+        assert np.all(y[:, 5] == 0.0)
+        if mm > 3:
+            assert np.all(y[3] == 0.0)
+    w.destroy()
+
+
+# ---------------------------------------------------------------- ingestion formats
+@pytest.mark.parametrize("nibble", [True, False])
+def test_x8_layout_ingestion(torch, ctx, orc, nibble):
+    import raster_amd
+
+    rng = np.random.default_rng(31)
+    out, in_, m = 64, 512, 3
+    wf = rng.uniform(-0.5, 0.5, out * in_).astype(np.float32)
+    if nibble:
+        wq, ws = orc.quantize_weight_q4(wf)
+    else:
+        wq, ws = orc.quantize_weight_q8u(wf)
+    wqi, wsi = orc.repack_x8(wq, ws, out, in_, nibble)
+    note(f"x8 ingest nibble={nibble}")
+    w = raster_amd.QWeight.x8(wqi, wsi, nibble, out, in_, ctx)
+    got = w.dequant().cpu().numpy().ravel()
+    zp = 8 if nibble else 128
+    ref = orc.dequant_weight(wq, ws, out * in_, zp, nibble)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    x = wl.activations(m, in_, seed=32)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    dense = orc.dense_matmul_nt_f64(x, ref, m, in_, out).reshape(m, out)
+    assert orc.normwise_relerr(y, dense) < TOL_F32
+
+
+def test_q8_packed_ingestion(torch, ctx, orc):
+    import raster_amd
+
+    rng = np.random.default_rng(33)
+    out, in_, m = 40, 256, 20
+    W = rng.standard_normal(out * in_).astype(np.float32)
+    wp, ws = orc.quantize_one_q8(W, in_, out)
+    note("q8 packed ingest")
+    w = raster_amd.QWeight.q8_packed(wp, ws, out, in_, ctx)
+    x = wl.activations(m, in_, seed=34)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    ref = orc.qlinear_q8(x, wp.view(np.int8), ws, m, in_, out).reshape(m, out)
+    assert orc.normwise_relerr(y, ref) < TOL_F32
+
+
+# ---------------------------------------------------------------- host surface + errors
+def test_qlinear_q8_host_surface(torch, ctx, orc):
+    # the shapes of test/raster/quant/train_test.clj:26-40
+    import raster_amd
+
+    out, in_, m = 4, 64, 2
+    W = orc.jfill_gauss(1, 0.3, out * in_)
+    X = orc.jfill_gauss(2, 0.3, m * in_)
+    codes, scales = orc.q8_quantize(W, out, in_)
+    note("qlinear_q8 host")
+    y = raster_amd.qlinear_q8(X, codes, scales, m, in_, out, ctx=ctx)
+    ref = orc.qlinear_q8(X, codes, scales, m, in_, out)
+    assert np.max(np.abs(y - ref)) < 1e-5
+    Wd = raster_amd.dequant_q8_dense(codes, scales, in_, out, ctx=ctx)
+    assert np.array_equal(Wd, orc.dequant_q8_dense(codes, scales, in_, out))
+    with pytest.raises(AssertionError):
+        raster_amd.qlinear_q8(np.zeros(30, np.float32), np.zeros(30, np.int8), np.zeros(1, np.float32), 1, 30, 1)
+
+
+def test_error_statuses_on_gpu(torch, ctx):
+    import ctypes as C
+
+    import raster_amd
+    from raster_amd import _lib
+
+    L = _lib.lib()
+    codes, scales = wl.q8_weights(8, 64, seed=1)
+    w = raster_amd.QWeight.q8(codes, scales, 8, 64, ctx)
+    x = torch.zeros((2, 64), device="cuda")
+    y = torch.zeros((2, 8), device="cuda")
+    xp, yp = C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr())
+    assert L.rq_qmatmul(ctx.handle, w.handle, xp, 7, yp, 0, 2, None) == _lib.RQ_ERR_DTYPE
+    assert L.rq_qmatmul(ctx.handle, w.handle, xp, 0, yp, 0, -1, None) == _lib.RQ_ERR_SHAPE
+    assert L.rq_qmatmul(ctx.handle, w.handle, None, 0, yp, 0, 2, None) == _lib.RQ_ERR_NULL
+    assert L.rq_qmatmul(ctx.handle, w.handle, C.c_void_p(x.data_ptr() + 4), 0, yp, 0, 1, None) == _lib.RQ_ERR_SHAPE
+    assert L.rq_qmatmul(ctx.handle, w.handle, xp, 0, yp, 0, 0, None) == _lib.RQ_OK
+    h = C.c_void_p()
+    assert L.rq_weight_create_q8(ctx.handle, codes.ctypes.data_as(C.c_void_p),
+                                 scales.ctypes.data_as(C.c_void_p), 8, 60, C.byref(h)) == _lib.RQ_ERR_SHAPE
+    assert b"multiple of 32" in L.rq_last_error()
+    big = C.c_void_p()
+    assert L.rq_buf_alloc(ctx.handle, 1 << 50, C.byref(big)) == _lib.RQ_ERR_OOM
+    handle = w.handle
+    w.destroy()
+    assert L.rq_weight_destroy(handle) == _lib.RQ_ERR_HANDLE
+    assert L.rq_qmatmul(ctx.handle, handle, xp, 0, yp, 0, 2, None) == _lib.RQ_ERR_HANDLE
+    buf = C.c_void_p()
+    assert L.rq_buf_alloc(ctx.handle, 1024, C.byref(buf)) == _lib.RQ_OK
+    assert L.rq_buf_free(ctx.handle, buf) == _lib.RQ_OK
+    assert L.rq_buf_free(ctx.handle, buf) == _lib.RQ_ERR_HANDLE
