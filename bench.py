@@ -1,0 +1,325 @@
+"""Benchmark of librq's block-quantized matmul on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite headline|all]
+
+Headline (the JSON `value`): the Q8 prefill GEMM of the second workload
+configuration, M=512 K=4096 N=11008, bf16 activations, bf16 output, f32
+accumulation, weights resident in HBM (`Q8 prefill GEMM, Llama-7B MLP up`).
+A step is one rq_qmatmul call over that batch; `value` is TFLOP/s
+(2*M*K*N flop per step) timed with HIP events on the stream the kernel runs on.
+
+Beside it, on the same JSON line:
+  gemv   - the M=1 Q8 decode GEMV (K=N=4096, f32 in/out) in GB/s of
+           algorithmic bytes (codes + scales + x + y). Timed over 100
+           back-to-back calls in one captured HIP graph, rotating through
+           enough weight copies (> 512 MB) that every call reads its weight
+           from HBM, not the 256 MB Infinity Cache ("cold"); warm = one copy.
+  sweep  - (--suite all) Q4 skinny M in {1,4,16} and the 70B-MLP shapes.
+  roofline      - the GEMM kernel against dense bf16 MFMA peak.
+  roofline_gemv - the GEMV kernel against HBM peak.
+  cpu_baseline  - the C restatement of Raster's qlinear-q8 loop
+                  (oracle/cpu_baseline.c) on a row sample of the same GEMM,
+                  all host threads; reported only.
+
+Multi-GPU runs are not part of this build: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "qmatmul GEMV GB/s (% of HBM peak) at M=1; GEMM TFLOPS (% MFMA) at M=512"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q8_bytes(m, k, n, xb, yb):
+    return n * k + n * (k // 32) * 4 + m * k * xb + m * n * yb
+
+
+def q4_bytes(m, k, n, xb, yb):
+    return n * k // 2 + n * (k // 32) * 2 + m * k * xb + m * n * yb
+
+
+class Case:
+    """One resident-weight workload: `copies` weight copies rotated per call."""
+
+    def __init__(self, torch, ctx, fmt, m, k, n, xdt, ydt, copies=1, seed=0):
+        import numpy as np
+
+        import raster_amd
+        from raster_amd import workloads as wl
+
+        self.torch, self.m, self.k, self.n, self.fmt = torch, m, k, n, fmt
+        if fmt == "q8":
+            codes, scales = wl.q8_weights(n, k, seed=seed)
+            self.weights = [raster_amd.QWeight.q8(codes, scales, n, k, ctx) for _ in range(copies)]
+            self.bytes = q8_bytes(m, k, n, 4 if xdt == "f32" else 2, 4 if ydt == "f32" else 2)
+        else:
+            packed, sc16 = wl.q4_weights(n, k, seed=seed)
+            self.weights = [raster_amd.QWeight.q4(packed, sc16.view(np.float16), n, k, ctx)
+                            for _ in range(copies)]
+            self.bytes = q4_bytes(m, k, n, 4 if xdt == "f32" else 2, 4 if ydt == "f32" else 2)
+        self.flops = 2.0 * m * k * n
+        x = torch.from_numpy(wl.activations(m, k, seed=seed + 1, dtype=xdt)).cuda().reshape(m, k)
+        self.x = x.to(torch.bfloat16) if xdt == "bf16" else x
+        ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
+        self.y = torch.empty((m, n), dtype=ydtype, device="cuda")
+        self.i = 0
+
+    def step(self):
+        w = self.weights[self.i % len(self.weights)]
+        self.i += 1
+        w.matmul(self.x, self.y)
+
+    def destroy(self):
+        for w in self.weights:
+            w.destroy()
+        self.weights = []
+
+
+def time_eager(torch, case, steps, warmup):
+    """Event-timed back-to-back calls on the current stream; ms per call."""
+    for _ in range(warmup):
+        case.step()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        case.step()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_graph(torch, case, calls=100, reps=5):
+    """`calls` launches captured in one HIP graph, replayed `reps` times after a
+    warm replay; returns (median ms per call, coefficient of variation)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            case.step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            case.step()
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    st = torch.cuda.current_stream()
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / calls)
+    del g
+    med = statistics.median(times)
+    cv = statistics.pstdev(times) / med if med > 0 else 0.0
+    return med, cv
+
+
+def copies_for_cold(nbytes):
+    return max(1, -(-2 * MALL_BYTES // nbytes))
+
+
+def hbm_line(torch, ctx, name, fmt, m, k, n, xdt, ydt):
+    """Cold (rotating copies) and warm GB/s for an HBM-bound shape."""
+    out = {"workload": name, "fmt": fmt, "m": m, "k": k, "n": n, "x": xdt, "y": ydt}
+    one = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=1)
+    wbytes = one.bytes
+    warm_ms, warm_cv = time_graph(torch, one)
+    one.destroy()
+    c = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=copies_for_cold(wbytes))
+    cold_ms, cold_cv = time_graph(torch, c)
+    out.update(copies=len(c.weights), bytes=wbytes, flop=c.flops)
+    c.destroy()
+    out.update(cold_us=round(cold_ms * 1e3, 3), cold_GBs=round(wbytes / cold_ms / 1e6, 1),
+               cold_cv=round(cold_cv, 4), cold_frac_hbm=round(wbytes / cold_ms / 1e6 / HBM_PEAK_GBS, 4),
+               warm_us=round(warm_ms * 1e3, 3), warm_GBs=round(wbytes / warm_ms / 1e6, 1),
+               warm_cv=round(warm_cv, 4))
+    return out
+
+
+def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
+    c = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=1)
+    ms = time_eager(torch, c, steps, warmup)
+    c.destroy()
+    tf = c.flops / ms / 1e9
+    return {"workload": name, "fmt": fmt, "m": m, "k": k, "n": n, "x": xdt, "y": ydt,
+            "us": round(ms * 1e3, 3), "TFLOPs": round(tf, 2), "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def read_traffic(kernel_tag):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary
+    (profiles/<kernel_tag>_pmc.txt, line `traffic_bytes_per_launch: N`)."""
+    path = os.path.join(PROFILES, f"{kernel_tag}_pmc.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(m, k, n, budget_s=10.0):
+    """Raster's qlinear-q8 loop restated in C (oracle/cpu_baseline.c), all host
+    threads, on a row sample of the GEMM; TFLOP/s scaled to the full shape."""
+    import ctypes as C
+
+    import numpy as np
+
+    from oracle import oracle
+    from raster_amd import workloads as wl
+
+    L = oracle.baseline_lib()
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    codes, scales = wl.q8_weights(n, k, seed=0)
+    x = wl.activations(m, k, seed=1, dtype="bf16")
+
+    def run(rows):
+        y = np.empty(rows * n, np.float32)
+        t0 = time.perf_counter()
+        L.rqb_qlinear_q8(x.ctypes.data_as(C.c_void_p), codes.ctypes.data_as(C.c_void_p),
+                         scales.ctypes.data_as(C.c_void_p), rows, k, n, y.ctypes.data_as(C.c_void_p), threads)
+        return time.perf_counter() - t0
+
+    t1 = run(1)
+    rows = int(max(1, min(m, budget_s / max(t1, 1e-6))))
+    dt = run(rows)
+    flop = 2.0 * rows * k * n
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"qlinear-q8 loop (f32 products, f64 accumulation) over {rows} of {m} activation rows "
+                      f"x K={k} x N={n}, {dt:.2f} s, {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--suite", choices=["headline", "all"], default="headline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import raster_amd
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (gfx950) GPU", file=sys.stderr)
+        sys.exit(1)
+    ctx = raster_amd.Context(0)
+    info = ctx.device_info()
+    clock_ghz = info["clock_khz"] / 1e6
+    # dense bf16 MFMA: 4 SIMDs per CU, 1024 flop per clock per SIMD on CDNA4
+    peak_props = info["cu_count"] * 4 * 1024 * clock_ghz / 1e3
+    log(f"device: {torch.cuda.get_device_name(0)} cu={info['cu_count']} clock={clock_ghz:.3f} GHz")
+
+    # ---- headline: Q8 GEMM M=512 K=4096 N=11008, bf16 in / bf16 out
+    M, K, N = 512, 4096, 11008
+    log(f"headline gemm q8 m={M} k={K} n={N} steps={args.steps} warmup={args.warmup}")
+    head = Case(torch, ctx, "q8", M, K, N, "bf16", "bf16")
+    for _ in range(args.warmup):
+        head.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        head.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    head.destroy()
+    tflops = head.flops / ms / 1e9
+    log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s (wall {wall:.3f} s)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: int8 codes U{-127..127}, f32 scales U(0.002,0.02), x N(0,1) rounded to bf16)",
+        "config": {"workload": "Q8 prefill GEMM, Llama-7B MLP up-projection: M=512 K=4096 N=11008, "
+                               "bf16 activations, f32 accumulation, bf16 output",
+                   "m": M, "k": K, "n": N, "weights": "q8_0 resident in HBM"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": read_traffic("gemm_q8_bf16_C2"),
+                     "peak_from_device_props": round(peak_props, 1),
+                     "kernel": "rq::gemm_kernel<0, float, 1>", "flop_per_launch": head.flops},
+    }
+
+    if not args.only_gemm:
+        # ---- decode GEMV: Q8 M=1 K=N=4096, f32 in / f32 out
+        log("gemv q8 m=1 k=4096 n=4096 (cold rotation + warm)")
+        gv = hbm_line(torch, ctx, "Q8 decode GEMV", "q8", 1, 4096, 4096, "f32", "f32")
+        result["gemv"] = gv
+        result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["cold_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": gv["cold_frac_hbm"], "traffic": read_traffic("gemv_q8_f32_C1"),
+                                   "kernel": "rq::gemv_kernel<0, float, 0, 1, 4, 4>",
+                                   "bytes_per_launch": gv["bytes"]}
+        log(f"gemv: cold {gv['cold_us']} us {gv['cold_GBs']} GB/s; warm {gv['warm_us']} us {gv['warm_GBs']} GB/s")
+
+    if args.suite == "all" and not args.only_gemm:
+        sweep = []
+        for m in (1, 4, 16):
+            log(f"q4 skinny m={m}")
+            sweep.append(hbm_line(torch, ctx, "Q4 decode skinny", "q4", m, 4096, 14336, "f32", "f32"))
+        for fmt in ("q8", "q4"):
+            for m in (1, 32):
+                log(f"70B MLP {fmt} m={m}")
+                sweep.append(hbm_line(torch, ctx, "70B MLP", fmt, m, 8192, 28672, "bf16", "bf16"))
+            log(f"70B MLP {fmt} m=256")
+            sweep.append(mfma_line(torch, ctx, "70B MLP", fmt, 256, 8192, 28672, "bf16", "bf16"))
+        result["sweep"] = sweep
+
+    if not args.no_cpu and not args.only_gemm:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(M, K, N)
+        log(f"cpu baseline: {result['cpu_baseline']['value']} TFLOP/s")
+    else:
+        result["cpu_baseline"] = None
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
