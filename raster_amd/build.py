@@ -5,7 +5,7 @@
 One hipcc invocation over every .hip file in raster_amd/csrc. Packed-FP32
 instruction selection is switched off (-packed-fp32-ops) for every device
 compile; hipcc's host pass warns that it does not know that feature, which is
-harmless.
+harmless. MFMA accumulators are kept in VGPRs (-amdgpu-mfma-vgpr-form).
 """
 from __future__ import annotations
 
@@ -37,6 +37,9 @@ def build(verbose: bool = False) -> str:
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: without it the register allocator copies
+        # accumulator tiles between AGPRs around every MFMA
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-Wall", "-Wno-unused-function",
         "-o", tmp, *sources(),
     ]

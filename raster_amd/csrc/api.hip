@@ -71,11 +71,16 @@ static int check_shape(int64_t out, int64_t in) {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Allocates the weight and uploads row-major codes/packed bytes and scales.
+// Allocates the weight, uploads Raster's row-major codes/packed bytes and
+// scales to a staging buffer and converts them to the chunked device layout.
 static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t in, const void* qhost,
                        const void* shost, rq_weight* wout) {
-  const size_t qbytes = format == RQ_Q8_0 ? (size_t)(out * in) : (size_t)(out * in / 2);
-  const size_t sbytes = (size_t)(out * (in / 32)) * (scale_dtype == RQ_F16 ? 2 : 4);
+  const int64_t npad = (out + 15) / 16 * 16;
+  const size_t ssz = scale_dtype == RQ_F16 ? 2 : 4;
+  const size_t qbytes_rm = (size_t)out * (size_t)(in / 32) * code_bytes(format);
+  const size_t sbytes_rm = (size_t)out * (size_t)(in / 32) * ssz;
+  const size_t qbytes = (size_t)npad * (size_t)(in / 32) * code_bytes(format);
+  const size_t sbytes = (size_t)npad * (size_t)(in / 32) * ssz;
   const size_t total = align256(qbytes) + align256(sbytes);
   if (int s = set_device(c)) return s;
   void* base = nullptr;
@@ -84,8 +89,16 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
     (void)hipGetLastError();
     return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(total) + " bytes for weight failed");
   }
+  void* stage = nullptr;
+  e = hipMalloc(&stage, align256(qbytes_rm) + sbytes_rm);
+  if (e != hipSuccess || !stage) {
+    (void)hipGetLastError();
+    (void)hipFree(base);
+    return fail(RQ_ERR_OOM, "hipMalloc of the weight staging buffer failed");
+  }
   Weight* w = new (std::nothrow) Weight();
   if (!w) {
+    (void)hipFree(stage);
     (void)hipFree(base);
     return fail(RQ_ERR_OOM, "host allocation failed");
   }
@@ -95,13 +108,19 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   w->device = c->device;
   w->out = out;
   w->in = in;
+  w->npad = npad;
   w->base = base;
   w->q = static_cast<uint8_t*>(base);
   w->scales = static_cast<uint8_t*>(base) + align256(qbytes);
   w->bytes = total;
   w->ctx = c;
-  e = hipMemcpy(w->q, qhost, qbytes, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(w->scales, shost, sbytes, hipMemcpyHostToDevice);
+  uint8_t* q_rm = static_cast<uint8_t*>(stage);
+  uint8_t* s_rm = q_rm + align256(qbytes_rm);
+  e = hipMemcpy(q_rm, qhost, qbytes_rm, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(s_rm, shost, sbytes_rm, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_chunk_weight(format, scale_dtype, q_rm, s_rm, out, in, npad, w->q, w->scales, nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  (void)hipFree(stage);
   if (e != hipSuccess) {
     (void)hipFree(base);
     delete w;
@@ -418,8 +437,11 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   a.m = m;
   a.k = w.in;
   a.n = w.out;
+  a.npad = w.npad;
   a.stream = (hipStream_t)stream;
-  hipError_t e = m <= 16 ? launch_gemv(a) : launch_gemm(a, c->cu_count);
+  hipError_t e = m <= 16                ? launch_gemv(a)
+                 : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
+                                      : launch_gemm(a, c->cu_count);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return RQ_OK;
 }

@@ -1,5 +1,5 @@
-// dequant.hip — writes the dequantized f32 weight W[out x in] from a resident
-// weight, with the same decode helpers (q8_code / q4_nib / load_scale) the
+// dequant.hip — writes the dequantized f32 weight W[out x in] (row-major, as
+// Raster returns it) from a resident chunked weight, with the same decode helpers (q8_code / q4_nib / load_scale) the
 // matmul kernels use. W[o, i] = scale[o, i/32] * code[o, i] is one IEEE f32
 // multiply of two exactly-represented operands, the value dequant-q8-dense
 // produces (raster/quant/train.clj:60-71: (float)(double scale * double code)
@@ -17,17 +17,19 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= nchunk) return;
   const int64_t row = c / (rowbytes / 16), cc = c % (rowbytes / 16);
-  const uint4 raw = *reinterpret_cast<const uint4*>(q + row * rowbytes + cc * 16);
-  const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
   const int64_t nb = in / 32;
+  // 16-byte piece cc of the row: Q8 half cc % 2 of block cc / 2, Q4 block cc
+  const int64_t src = FMT == RQ_Q8_0 ? code_off<FMT>(row, cc / 2, nb) + 16 * (cc % 2) : code_off<FMT>(row, cc, nb);
+  const uint4 raw = *reinterpret_cast<const uint4*>(q + src);
+  const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
   if (FMT == RQ_Q8_0) {
-    const float s = load_scale<ST>(sc, row * nb + cc / 2);
+    const float s = load_scale<ST>(sc, scale_off(row, cc / 2, nb));
     float4* dst = reinterpret_cast<float4*>(w + row * in + cc * 16);
 #pragma unroll
     for (int i = 0; i < 4; i++)
       dst[i] = make_float4(s * q8_code(d[i], 0), s * q8_code(d[i], 1), s * q8_code(d[i], 2), s * q8_code(d[i], 3));
   } else {
-    const float s = load_scale<ST>(sc, row * nb + cc);
+    const float s = load_scale<ST>(sc, scale_off(row, cc, nb));
     float4* dst = reinterpret_cast<float4*>(w + row * in + cc * 32);
 #pragma unroll
     for (int i = 0; i < 4; i++) {

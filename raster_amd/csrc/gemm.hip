@@ -50,7 +50,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ q
   const int wm = wave & 1, wn = wave >> 1;
   const int nkb = K / 32;
   const int lrow = tid >> 1, lhalf = tid & 1;
-  const int64_t qrow = FMT == RQ_Q8_0 ? (int64_t)K : (int64_t)K / 2;
 
   // staging registers
   uint4 a_raw[XT == RQ_F32 ? 4 : 2];
@@ -77,10 +76,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ q
     }
     const int bn = n0 + lrow;
     if (bn < N) {
-      const int64_t off = FMT == RQ_Q8_0 ? (int64_t)bn * qrow + (int64_t)kb * 32 + 16 * lhalf
-                                         : (int64_t)bn * qrow + (int64_t)kb * 16;
+      const int64_t off = code_off<FMT>(bn, kb, nkb) + (FMT == RQ_Q8_0 ? 16 * lhalf : 0);
       b_raw = *reinterpret_cast<const uint4*>(q + off);
-      s_raw = load_scale<ST>(sc, (int64_t)bn * nkb + kb);
+      s_raw = load_scale<ST>(sc, scale_off(bn, kb, nkb));
     } else {
       b_raw = make_uint4(0, 0, 0, 0);
       s_raw = 0.0f;

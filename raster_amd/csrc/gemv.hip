@@ -79,8 +79,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ q
       for (int r = 0; r < ROWS; r++) {
         const int row = row0 + r;
         if (c < nchunks && row < N) {
-          raw[g][r] = *reinterpret_cast<const uint4*>(q + (int64_t)row * rowbytes + (int64_t)c * 16);
-          s[g][r] = load_scale<ST>(sc, (int64_t)row * nb + (FMT == RQ_Q8_0 ? c / 2 : c));
+          const int64_t off = FMT == RQ_Q8_0 ? code_off<FMT>(row, c / 2, nb) + 16 * (c % 2) : code_off<FMT>(row, c, nb);
+          raw[g][r] = *reinterpret_cast<const uint4*>(q + off);
+          s[g][r] = load_scale<ST>(sc, scale_off(row, FMT == RQ_Q8_0 ? c / 2 : c, nb));
         } else {
           raw[g][r] = make_uint4(0, 0, 0, 0);
           s[g][r] = 0.0f;

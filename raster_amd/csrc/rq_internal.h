@@ -15,23 +15,42 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
-// Resident weight, stored in HBM in Raster's row-major layout:
-//   Q8_0: codes int8[out*in] then scales f32[out*in/32]
-//   Q4_0: packed u8[out*in/2] (lo nibble = elem k, hi = elem k+16 per 32-block)
-//         then scales f32 or fp16 [out*in/32]
+// Resident weight in HBM, "chunked" layout. Rows are padded with zeros to
+// npad = 16 * ceil(out / 16). Chunk (g, b) holds the 16 rows [16g, 16g+16) of
+// the 32-element block b (nb = in / 32 blocks per row), chunks ordered g-major:
+//   codes  : CB bytes per row and block, CB = 32 (Q8_0: int8 codes) or
+//            16 (Q4_0: Raster's packing, byte j = lo nibble elem j | hi nibble
+//            elem j+16); chunk (g, b) at byte (g*nb + b) * 16*CB, row r of the
+//            chunk at + r*CB.
+//   scales : 16 per chunk (f32, or fp16 bits), element (g*nb + b)*16 + r.
+// A 16-row x 64-element window is then 1 KB (Q8) or 512 B (Q4) of contiguous
+// codes and every weight load a kernel issues covers whole cache lines.
 // Both arrays live in one allocation, each 256-byte aligned.
 struct Weight {
   uint32_t magic;
   int format;       // RQ_Q8_0 / RQ_Q4_0
   int scale_dtype;  // RQ_F32 / RQ_F16
   int device;
-  int64_t out, in;
+  int64_t out, in, npad;
   void* base;       // device allocation
-  uint8_t* q;       // codes / packed nibbles
-  void* scales;
+  uint8_t* q;       // chunked codes / packed nibbles
+  void* scales;     // chunked scales
   size_t bytes;
   struct Ctx* ctx;
 };
+
+// bytes of codes per row and 32-element block
+__host__ __device__ constexpr int code_bytes(int fmt) { return fmt == RQ_Q8_0 ? 32 : 16; }
+__host__ __device__ __forceinline__ int64_t chunk_of(int64_t row, int64_t b, int64_t nb) { return (row >> 4) * nb + b; }
+// byte offset of (row, block b) in the chunked codes
+template <int FMT>
+__host__ __device__ __forceinline__ int64_t code_off(int64_t row, int64_t b, int64_t nb) {
+  return chunk_of(row, b, nb) * (16 * code_bytes(FMT)) + (row & 15) * code_bytes(FMT);
+}
+// element offset of (row, block b) in the chunked scales
+__host__ __device__ __forceinline__ int64_t scale_off(int64_t row, int64_t b, int64_t nb) {
+  return chunk_of(row, b, nb) * 16 + (row & 15);
+}
 
 // Launch descriptor for the matmul kernels.
 struct MatmulArgs {
@@ -44,13 +63,18 @@ struct MatmulArgs {
   void* y;
   int y_dtype;
   int64_t m, k, n;  // m activation rows, k = in, n = out
+  int64_t npad;     // n padded to a multiple of 16 (rows present in the chunked layout)
   hipStream_t stream;
 };
 
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
 hipError_t launch_gemv(const MatmulArgs& a);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
+hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
+// Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
+hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
+                               int64_t in, int64_t npad, uint8_t* q, void* s, hipStream_t stream);
 
 // ---- device helpers shared by every kernel that decodes weights -----------
 

@@ -205,6 +205,34 @@ def test_gemm_ragged_f32(torch, ctx, orc, m, in_, out, fmt):
     assert orc.normwise_relerr(y, ref.reshape(m, out)) < TOL_F32
 
 
+@pytest.mark.parametrize("m,in_,out", [(17, 32, 8), (100, 64, 100), (129, 96, 130), (300, 160, 257),
+                                       (257, 224, 96), (64, 416, 200), (520, 1024, 190)])
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
+    # bf16 activations take the dequantize-to-LDS MFMA kernel: K-block counts
+    # 1, 2, 3, 5, 7, 13 and 32 exercise every tail of its 6-step unrolled
+    # pipeline; M and N are ragged against the 64/128/256 x 64/96/128 tiles.
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=3 * m + out, dtype="bf16")
+    note(f"gemm {fmt} bf16 m={m} {out}x{in_}")
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=out + 1)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        ref = orc.qlinear_q8(x, codes, scales, m, in_, out)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=out + 1)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+        ref = orc.qlinear_q4(x, packed, sc16, m, in_, out)
+    y32 = run(torch, w, x, m, "bf16", "f32")
+    y16 = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    ref = ref.reshape(m, out)
+    assert orc.normwise_relerr(y32, ref) < TOL_BF16
+    assert orc.normwise_relerr(y16, ref) < TOL_BF16
+    assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
+
+
 def test_gemm_q4_bf16_m256(torch, ctx, orc):
     import raster_amd
 
