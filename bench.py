@@ -109,16 +109,17 @@ def time_eager(torch, case, steps, warmup):
 
 def time_graph(torch, case, calls=100, reps=5):
     """`calls` launches captured in one HIP graph, replayed `reps` times after a
-    warm replay; returns (median ms per call, coefficient of variation)."""
+    warm replay; returns (median ms per call, coefficient of variation). The
+    warm-up runs on the capture stream itself, so per-stream scratch (the
+    prefill GEMM's packed activations) exists before capture begins."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for _ in range(3):
             case.step()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
+    s.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for _ in range(calls):
             case.step()
     g.replay()

@@ -23,6 +23,10 @@ struct Ctx {
   int clock_khz;
   std::unordered_set<Weight*> weights;
   std::unordered_set<void*> buffers;
+  // Per-stream scratch for the packed activations of the bf16 GEMM; grow-only,
+  // freed with the context. Calls on one stream run in order, so a stream's
+  // buffer is never used by two kernels at once.
+  std::unordered_map<hipStream_t, std::pair<void*, size_t>> scratch;
 };
 
 static constexpr uint32_t kCtxMagic = 0x52514358u;     // "RQCX"
@@ -140,6 +144,35 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   return RQ_OK;
 }
 
+// Scratch of at least `bytes` for `stream` (grow-only, one buffer per stream).
+static int stream_scratch(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto& e = c->scratch[stream];
+  if (e.second < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(RQ_ERR_SHAPE,
+                  "this stream is being captured and has no scratch for m=" + std::to_string(bytes) +
+                      " bytes yet: run the same (or a larger) call on the stream once before capturing");
+    if (e.first) {
+      // the old buffer may still be read by kernels queued on this stream
+      const hipError_t se = hipStreamSynchronize(stream);
+      if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
+      (void)hipFree(e.first);
+      e = {nullptr, 0};
+    }
+    const size_t want = bytes + bytes / 4;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(want) + " bytes of scratch failed");
+    }
+    e = {p, want};
+  }
+  *out = e.first;
+  return RQ_OK;
+}
+
 static void free_weight_locked(Weight* w) {
   (void)hipSetDevice(w->device);
   (void)hipFree(w->base);
@@ -208,6 +241,7 @@ int rq_ctx_destroy(rq_ctx h) {
   (void)hipSetDevice(c->device);
   for (Weight* w : c->weights) free_weight_locked(w);
   for (void* b : c->buffers) (void)hipFree(b);
+  for (auto& kv : c->scratch) (void)hipFree(kv.second.first);
   c->magic = 0;
   g_ctxs.erase(c);
   delete c;
@@ -439,6 +473,12 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   a.n = w.out;
   a.npad = w.npad;
   a.stream = (hipStream_t)stream;
+  a.scratch = nullptr;
+  if (m > 16 && x_dtype == RQ_BF16) {
+    // fragment-major copy of the activations: ceil(m/16)*16 rows
+    const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
+    if (int s = stream_scratch(c, a.stream, bytes, &a.scratch)) return s;
+  }
   hipError_t e = m <= 16                ? launch_gemv(a)
                  : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
                                       : launch_gemm(a, c->cu_count);

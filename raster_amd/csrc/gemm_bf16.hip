@@ -2,7 +2,7 @@
 //
 // y[m, o] = sum_k x[m, k] * W[o, k],  W[o, k] = scale[o, k/32] * code[o, k]
 //
-// The weight tile is dequantized once per workgroup into LDS: the f32 product
+// Each weight element is dequantized once per workgroup: the f32 product
 // scale * code is formed exactly as Raster's dequant (one IEEE f32 rounding of
 // the exact product, raster/quant/train.clj:60-71) and rounded to bf16 (RNE)
 // for the MFMA operand; accumulation is f32 over the whole K. With the scale
@@ -11,123 +11,114 @@
 // gemm.hip keeps integer codes as operands and applies the scale per block,
 // which is exact but costs one FMA per output per 32-block.)
 //
-// Mapping: 256 threads = 4 waves stacked along M, each wave WM x 16 rows and
-// the whole BN-column tile (BN/16 MFMA column tiles). Activations are not
-// shared between waves, so each wave loads its A fragments straight from global
-// memory into registers (2 k-steps ahead); only the dequantized weight tile,
-// which all four waves read, goes through LDS (three buffers, one barrier per
-// 32-wide k-step): while step s runs its MFMAs, step s+1's fragments are read
-// from LDS and step s+2's codes are dequantized into the third buffer.
+// Data flow per workgroup (4 waves side by side along N; tile BM x BN with
+// BM = 16*MT rows, BN = 4 * 16*NTW columns):
+//  * activations: a pack kernel first writes x in fragment-major order (every
+//    16-row x 32-k MFMA operand is one contiguous kilobyte, see pack_x_kernel).
+//    All four waves need the same activation rows, so each k-step's BM x 32
+//    tile is loaded once (coalesced), written to LDS in that same order and
+//    read back linearly by every wave (no bank conflicts).
+//  * weights: each wave owns its BN/4 columns. In the chunked device layout a
+//    16-row x 32-k weight fragment is one 512-byte (Q8) / 256-byte (Q4)
+//    chunk, so a wave loads its fragments straight into registers with one
+//    coalesced instruction each and dequantizes them there; weights never
+//    touch LDS and no element is dequantized twice.
+// MFMA operands are swapped (weights = A, activations = B) so each lane's
+// accumulator holds 4 consecutive outputs of one row (8/16-byte stores).
+// The k-loop is software-pipelined and unrolled by 6 (see RQ_STEP).
 #include "rq_internal.h"
 
 namespace rq {
 
 namespace {
 
-constexpr int LDB = 40;  // bf16 per LDS weight row: 32 + 8 pad (80-byte stride)
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  bf16x2_t v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round to nearest even
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// One loader thread's share of a 32-wide k-step of the weight tile: 16 elements
-// of one row. Q8: bytes [16h, 16h+16) of the row's block. Q4: bytes [8h, 8h+8)
-// of the 16-byte block, i.e. elements [8h, 8h+8) (low nibbles) and
-// [16+8h, 16+8h+8) (high nibbles).
-template <int FMT>
-struct BChunk {
-  uint4 v;
+// A lane's share of one 16-row x 32-k weight fragment: the 8 codes of row fr,
+// elements [8 fg, 8 fg + 8) of the block, plus the row's block scale.
+//  Q8: bytes [8 fg, 8 fg + 8) of the row's 32 codes.
+//  Q4: bytes [8 (fg & 1), +8) of the row's 16 packed bytes; low nibbles are
+//      elements 0..15 of the block, high nibbles 16..31 (Raster's packing),
+//      so fg < 2 takes low nibbles and fg >= 2 high nibbles.
+struct WCodes {
+  u32x2 v;
   float s;
 };
 
-// Loads are unconditional: out-of-range rows and k-steps are clamped to valid
-// addresses so the pipelined loop has no branches (the compiler can then wait
-// for exactly the load it needs instead of every outstanding one). A clamped
-// weight row only feeds output columns that are never stored. In the chunked
-// layout the 2*BN loader threads of a k-step read whole 512-byte (Q8) or
-// 256-byte (Q4) chunks: one wave instruction covers two chunks.
 template <int FMT, typename ST>
-__device__ __forceinline__ void load_bchunk(BChunk<FMT>& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                            int row, int half, int kb, int nkb) {
-  if (FMT == RQ_Q8_0) {
-    c.v = *reinterpret_cast<const uint4*>(q + code_off<FMT>(row, kb, nkb) + 16 * half);
-  } else {
-    const uint2 t = *reinterpret_cast<const uint2*>(q + code_off<FMT>(row, kb, nkb) + 8 * half);
-    c.v = make_uint4(t.x, t.y, 0u, 0u);
-  }
-  c.s = load_scale<ST>(sc, scale_off(row, kb, nkb));
+__device__ __forceinline__ void load_wcodes(WCodes& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
+                                            int64_t chunk, int fr, int fg) {
+  if (FMT == RQ_Q8_0)
+    c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
+  else
+    c.v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + fr * 16 + 8 * (fg & 1));
+  c.s = load_scale<ST>(sc, chunk * 16 + fr);
 }
 
-// Dequantize a chunk (exact f32 scale*code, then bf16 RNE) into an LDS row.
+// Dequantized fragment (8 bf16): exact f32 scale * code, one RNE rounding to bf16.
 template <int FMT>
-__device__ __forceinline__ void store_bchunk(const BChunk<FMT>& c, uint16_t* __restrict__ brow, int half) {
+__device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
   const float s = c.s;
+  uint32_t d[2];
+  float off;
   if (FMT == RQ_Q8_0) {
-    // signed code c = u - 128 with u = byte ^ 0x80; fma(u, s, -128 s) = s * c exactly rounded once
-    const float off = -128.0f * s;
-    const uint32_t d[4] = {c.v.x ^ 0x80808080u, c.v.y ^ 0x80808080u, c.v.z ^ 0x80808080u, c.v.w ^ 0x80808080u};
-    uint32_t o[8];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float w0 = fmaf((float)(d[i] & 0xFFu), s, off);
-      const float w1 = fmaf((float)((d[i] >> 8) & 0xFFu), s, off);
-      const float w2 = fmaf((float)((d[i] >> 16) & 0xFFu), s, off);
-      const float w3 = fmaf((float)(d[i] >> 24), s, off);
-      o[2 * i] = pack2_bf16(w0, w1);
-      o[2 * i + 1] = pack2_bf16(w2, w3);
-    }
-    uint4* dst = reinterpret_cast<uint4*>(brow + 16 * half);
-    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    // signed code = u - 128 with u = byte ^ 0x80: fma(u, s, -128 s) = s * code, rounded once
+    d[0] = c.v[0] ^ 0x80808080u;
+    d[1] = c.v[1] ^ 0x80808080u;
+    off = -128.0f * s;
   } else {
-    // nibble q, zero-point 8: fma(q, s, -8 s) = s * (q - 8) exactly rounded once
-    const float off = -8.0f * s;
-    const uint32_t lo[2] = {c.v.x & 0x0F0F0F0Fu, c.v.y & 0x0F0F0F0Fu};
-    const uint32_t hi[2] = {(c.v.x >> 4) & 0x0F0F0F0Fu, (c.v.y >> 4) & 0x0F0F0F0Fu};
-    uint32_t ol[4], oh[4];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      ol[2 * i] = pack2_bf16(fmaf((float)(lo[i] & 0xFFu), s, off), fmaf((float)((lo[i] >> 8) & 0xFFu), s, off));
-      ol[2 * i + 1] =
-          pack2_bf16(fmaf((float)((lo[i] >> 16) & 0xFFu), s, off), fmaf((float)(lo[i] >> 24), s, off));
-      oh[2 * i] = pack2_bf16(fmaf((float)(hi[i] & 0xFFu), s, off), fmaf((float)((hi[i] >> 8) & 0xFFu), s, off));
-      oh[2 * i + 1] =
-          pack2_bf16(fmaf((float)((hi[i] >> 16) & 0xFFu), s, off), fmaf((float)(hi[i] >> 24), s, off));
-    }
-    *reinterpret_cast<uint4*>(brow + 8 * half) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
-    *reinterpret_cast<uint4*>(brow + 16 + 8 * half) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+    // nibble q, zero-point 8: fma(q, s, -8 s) = s * (q - 8), rounded once
+    const int sh = fg >= 2 ? 4 : 0;
+    d[0] = (c.v[0] >> sh) & 0x0F0F0F0Fu;
+    d[1] = (c.v[1] >> sh) & 0x0F0F0F0Fu;
+    off = -8.0f * s;
   }
-}
-
-// Instruction order inside one k-step: global loads first, then the LDS
-// fragment reads, then each MFMA followed by two VALU instructions (the
-// dequant of a later step hides under the MFMA pipeline), LDS writes last.
-template <int NVMEM, int NDSR, int NMFMA>
-__device__ __forceinline__ void rq_step_schedule() {
-  __builtin_amdgcn_sched_group_barrier(0x020, NVMEM, 0);  // VMEM reads
-  __builtin_amdgcn_sched_group_barrier(0x100, NDSR, 0);   // DS reads
+  uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < NMFMA; i++) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+  for (int i = 0; i < 2; i++) {
+    o[2 * i] = pack2_bf16(fmaf((float)(d[i] & 0xFFu), s, off), fmaf((float)((d[i] >> 8) & 0xFFu), s, off));
+    o[2 * i + 1] = pack2_bf16(fmaf((float)((d[i] >> 16) & 0xFFu), s, off), fmaf((float)(d[i] >> 24), s, off));
   }
-  __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS writes
+  return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
 }  // namespace
 
-template <int FMT, typename ST, int WM, int BN>
+// Fragment-major copy of the activations: x[m][k] (bf16, row-major) to
+// xf[m/16][k/32][lane][8] with lane = 16 * ((k % 32) / 8) + m % 16, i.e. the
+// 16 bytes lane l of an MFMA operand fragment needs. Rows up to the next
+// multiple of 16 are zero. Row-major fragment loads hit 16 rows one row
+// stride apart (K*2 bytes, which aliases in L1) and use half of each cache
+// line; from xf every fragment is one contiguous kilobyte.
+// One workgroup moves a 16-row x 128-element region (4 k-blocks): it reads
+// 256 contiguous bytes per row (whole cache lines), transposes through LDS
+// (rows padded to 17 pieces against bank conflicts) and writes 4 KB
+// contiguously.
+__global__ __launch_bounds__(256) void pack_x_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xf, int M,
+                                                    int K) {
+  __shared__ uint4 t[16 * 17];
+  const int nb = K / 32, nq = (nb + 3) / 4;
+  const int tile = blockIdx.x / nq, b0 = (blockIdx.x % nq) * 4;
+  const int i = threadIdx.x;
+  {
+    const int r = i >> 4, pp = i & 15;  // row, 16-byte piece of the row's 256 bytes
+    const int m = tile * 16 + r, b = b0 + (pp >> 2);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (m < M && b < nb) v = *reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * b0 + 8 * pp);
+    t[r * 17 + pp] = v;
+  }
+  __syncthreads();
+  const int b = b0 + (i >> 6), l = i & 63, r = l & 15, fg = l >> 4;
+  if (b < nb) *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = t[r * 17 + (i >> 6) * 4 + fg];
+}
+
+template <int FMT, typename ST, int MT, int NTW>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                       const uint16_t* __restrict__ x, void* __restrict__ y, int M,
+                                                       const uint16_t* __restrict__ xf, void* __restrict__ y, int M,
                                                        int K, int N, int npad, int y_dtype, int tiles_m) {
-  constexpr int BM = 4 * WM * 16;
-  constexpr int NT = BN / 16;
-  // Three weight-tile buffers of 128 rows whatever BN is: threads beyond 2*BN
-  // dequantize a clamped duplicate row into rows BN..127, which no wave reads.
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[3][128 * LDB];
+  constexpr int BM = 16 * MT, BN = 64 * NTW;
+  constexpr int AP = MT / 4;  // 16-byte activation pieces each thread stages per k-step
+  static_assert(MT % 4 == 0, "MT must be a multiple of 4");
+  // three k-steps of activation fragments, fragment-major (1 KB per 16 rows)
+  __shared__ __attribute__((aligned(16))) uint16_t As[3][MT * 512];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous
   // run of tiles, m-tiles of one weight tile adjacent (one L2 fill per XCD).
@@ -141,72 +132,103 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   const int fr = lane & 15, fg = lane >> 4;
   const int nkb = K / 32;
 
-  // A fragment rows of this lane (rows past M are clamped: they only feed
-  // output rows that are never stored)
-  const uint16_t* arow[WM];
+  // activation staging: piece p = tid + 256 i (i < AP) of the BM x 32 step
+  // tile is fragment p / 64, lane position p % 64. Fragments past the padded
+  // rows are clamped (they only feed output rows that are never stored).
+  const int mt_last = (M + 15) / 16 - 1;
+  const uint16_t* asrc[AP];
+  int adst[AP];
 #pragma unroll
-  for (int i = 0; i < WM; i++) {
-    const int m = min(m0 + wave * WM * 16 + i * 16 + fr, M - 1);
-    arow[i] = x + (int64_t)m * K + 8 * fg;
+  for (int i = 0; i < AP; i++) {
+    const int p = tid + 256 * i;
+    const int mt = min(m0 / 16 + p / 64, mt_last);
+    asrc[i] = xf + (int64_t)mt * nkb * 512 + (p % 64) * 8;
+    adst[i] = p * 8;
   }
-  // weight loader role: 2 threads per tile row
-  const int brow_l = tid >> 1, bhalf = tid & 1;
-  const int brow_g = min(n0 + min(brow_l, BN - 1), npad - 1);
-  const int bst = brow_l * LDB;            // this thread's LDS row
-  const int bfo = fr * LDB + 8 * fg;       // this lane's fragment offset in a tile
-
-  f32x4 acc[WM][NT];
+  // this wave's weight chunks (16-row groups, clamped to the padded rows)
+  const int g_last = npad / 16 - 1;
+  int64_t wchunk[NTW];
 #pragma unroll
-  for (int i = 0; i < WM; i++)
-#pragma unroll
-    for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < NTW; j++) wchunk[j] = (int64_t)min(n0 / 16 + wave * NTW + j, g_last) * nkb;
 
-  bf16x8 ar[3][WM];   // A fragments of steps s, s+1, s+2
-  bf16x8 bf[2][NT];   // weight fragments of steps s, s+1
-  BChunk<FMT> bc[2];  // weight codes of steps s+2, s+3
+  f32x4 acc[MT][NTW];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < NTW; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Register rings (indices are compile-time inside the 6-step unrolled body):
+  //   areg: staged activation pieces of steps s+2 (written to LDS at step s)
+  //         and s+3 (loaded at step s)
+  //   afr:  activation fragments of steps s, s+1 (read from LDS one step ahead)
+  //   wc:   weight codes of steps s+1 .. s+3 (loaded 3 steps ahead)
+  //   wf:   dequantized weight fragments of steps s, s+1
+  u32x4 areg[2][AP];
+  bf16x8 afr[2][MT];
+  WCodes wc[3][NTW];
+  bf16x8 wf[2][NTW];
+
 #define RQ_LOAD_A(slot, kb_)                                                              \
   do {                                                                                    \
-    const int64_t ko_ = (int64_t)min((kb_), nkb - 1) * 32;                                \
-    _Pragma("unroll") for (int i = 0; i < WM; i++) ar[slot][i] =                          \
-        *reinterpret_cast<const bf16x8*>(arow[i] + ko_);                                  \
+    const int64_t ko_ = (int64_t)min((kb_), nkb - 1) * 512;                               \
+    _Pragma("unroll") for (int i = 0; i < AP; i++) areg[slot][i] =                        \
+        *reinterpret_cast<const u32x4*>(asrc[i] + ko_);                                   \
   } while (0)
-#define RQ_LOAD_B(slot, kb_) load_bchunk<FMT, ST>(bc[slot], q, sc, brow_g, bhalf, min((kb_), nkb - 1), nkb)
-#define RQ_READ_F(slot, buf)                                                              \
+#define RQ_STORE_A(slot, buf)                                                             \
   do {                                                                                    \
-    _Pragma("unroll") for (int j = 0; j < NT; j++) bf[slot][j] =                          \
-        *reinterpret_cast<const bf16x8*>(&Bs[buf][bfo + j * 16 * LDB]);                   \
+    _Pragma("unroll") for (int i = 0; i < AP; i++)                                        \
+        *reinterpret_cast<u32x4*>(&As[buf][adst[i]]) = areg[slot][i];                     \
+  } while (0)
+#define RQ_READ_A(slot, buf)                                                              \
+  do {                                                                                    \
+    _Pragma("unroll") for (int i = 0; i < MT; i++) afr[slot][i] =                         \
+        *reinterpret_cast<const bf16x8*>(&As[buf][i * 512 + lane * 8]);                   \
+  } while (0)
+#define RQ_LOAD_W(slot, kb_)                                                              \
+  do {                                                                                    \
+    const int kk_ = min((kb_), nkb - 1);                                                  \
+    _Pragma("unroll") for (int j = 0; j < NTW; j++)                                       \
+        load_wcodes<FMT, ST>(wc[slot][j], q, sc, wchunk[j] + kk_, fr, fg);                \
   } while (0)
 
+  // prologue: LDS buffers 0, 1 hold steps 0, 1; areg[0] holds step 2;
+  // afr[0] and wf[0] hold step 0; wc[1], wc[2] hold steps 1, 2.
   RQ_LOAD_A(0, 0);
   RQ_LOAD_A(1, 1);
-  RQ_LOAD_B(0, 0);
-  RQ_LOAD_B(1, 1);
-  store_bchunk<FMT>(bc[0], &Bs[0][bst], bhalf);
-  RQ_LOAD_B(0, 2);
-  store_bchunk<FMT>(bc[1], &Bs[1][bst], bhalf);
-  RQ_LOAD_B(1, 3);
+  RQ_LOAD_W(0, 0);
+  RQ_LOAD_W(1, 1);
+  RQ_LOAD_W(2, 2);
+  RQ_STORE_A(0, 0);
+  RQ_STORE_A(1, 1);
+  RQ_LOAD_A(0, 2);
+#pragma unroll
+  for (int j = 0; j < NTW; j++) wf[0][j] = dequant_frag<FMT>(wc[0][j], fg);
   __syncthreads();
-  RQ_READ_F(0, 0);
+  RQ_READ_A(0, 0);
 
-  // k-step s (32 wide), software-pipelined across steps:
-  //   A:      prefetch step s+2 from global into ar[(s+2) % 3]
-  //   weight: read step s+1's fragments from LDS buffer (s+1) % 3 into bf[(s+1) % 2]
-  //   MFMA:   ar[s % 3] x bf[s % 2]
-  //   dequant the codes of step s+2 (bc[s % 2]) into LDS buffer (s+2) % 3 and
-  //   refill bc[s % 2] with the codes of step s+4.
-  // One barrier per step; a buffer is rewritten two steps after its fragments
-  // were read. The scheduling barrier stops the compiler from hoisting the
-  // dequant of a just-issued load into the step that issued it.
+  // k-step s (u = s % 6), software-pipelined:
+  //   global: activation pieces of step s+3 -> areg[(u+1) % 2];
+  //           weight codes of step s+3 -> wc[u % 3]
+  //   LDS:    write areg[u % 2] (step s+2) into buffer (u+2) % 3;
+  //           read step s+1's activation fragments from buffer (u+1) % 3
+  //   MFMA:   wf[u % 2] (A operand, weights) x afr[u % 2] (B operand, activations)
+  //   VALU:   dequantize wc[(u+1) % 3] (step s+1) into wf[(u+1) % 2],
+  //           interleaved with the MFMAs.
+  // One barrier per step: a buffer is rewritten two steps after its last read.
 #define RQ_STEP(kb_, u_)                                                                  \
   do {                                                                                    \
-    RQ_LOAD_A(((u_) + 2) % 3, (kb_) + 2);                                                 \
-    RQ_READ_F(((u_) + 1) % 2, ((u_) + 1) % 3);                                            \
-    _Pragma("unroll") for (int i = 0; i < WM; i++)                                        \
-    _Pragma("unroll") for (int j = 0; j < NT; j++) acc[i][j] =                            \
-        __builtin_amdgcn_mfma_f32_16x16x32_bf16(ar[(u_) % 3][i], bf[(u_) % 2][j], acc[i][j], 0, 0, 0); \
-    store_bchunk<FMT>(bc[(u_) % 2], &Bs[((u_) + 2) % 3][bst], bhalf);                     \
-    RQ_LOAD_B((u_) % 2, (kb_) + 4);                                                       \
-    rq_step_schedule<WM + 2, NT, WM * NT>();                                                          \
+    RQ_LOAD_A(((u_) + 1) % 2, (kb_) + 3);                                                 \
+    RQ_LOAD_W((u_) % 3, (kb_) + 3);                                                       \
+    RQ_STORE_A((u_) % 2, ((u_) + 2) % 3);                                                 \
+    RQ_READ_A(((u_) + 1) % 2, ((u_) + 1) % 3);                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                    \
+    _Pragma("unroll") for (int j = 0; j < NTW; j++) {                                     \
+      _Pragma("unroll") for (int i = 0; i < MT; i++)                                      \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[(u_) % 2][j], afr[(u_) % 2][i], \
+                                                            acc[i][j], 0, 0, 0);          \
+      wf[((u_) + 1) % 2][j] = dequant_frag<FMT>(wc[((u_) + 1) % 3][j], fg);               \
+      __builtin_amdgcn_sched_barrier(0);                                                  \
+    }                                                                                     \
     __syncthreads();                                                                      \
     __builtin_amdgcn_sched_barrier(0);                                                    \
   } while (0)
@@ -227,77 +249,77 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   if (kb + 4 < nkb) RQ_STEP(kb + 4, 4);
 #undef RQ_STEP
 #undef RQ_LOAD_A
-#undef RQ_LOAD_B
-#undef RQ_READ_F
+#undef RQ_STORE_A
+#undef RQ_READ_A
+#undef RQ_LOAD_W
 
-  // epilogue: lane holds column fr of each 16x16 tile, rows 4*fg + r
+  // epilogue: acc[i][j] holds y[m][n .. n+3] with m = row fr of activation
+  // tile i, n = 4 fg of this wave's weight tile j: one 8-byte (bf16) or
+  // 16-byte (f32) store per lane and tile when rows are 16-byte aligned.
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
 #pragma unroll
-  for (int i = 0; i < WM; i++)
+  for (int i = 0; i < MT; i++) {
+    const int m = m0 + i * 16 + fr;
+    if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < NT; j++) {
-      const int n = n0 + j * 16 + fr;
-      if (n >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wave * WM * 16 + i * 16 + 4 * fg + r;
-        if (m >= M) continue;
+    for (int j = 0; j < NTW; j++) {
+      const int n = n0 + (wave * NTW + j) * 16 + 4 * fg;
+      const f32x4 v = acc[i][j];
+      if (vec && n + 3 < N) {
         if (y_dtype == RQ_F32)
-          static_cast<float*>(y)[(int64_t)m * N + n] = acc[i][j][r];
+          *reinterpret_cast<float4*>(static_cast<float*>(y) + (int64_t)m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
         else
-          static_cast<uint16_t*>(y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][r]);
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + (int64_t)m * N + n) =
+              make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (n + r >= N) break;
+          if (y_dtype == RQ_F32)
+            static_cast<float*>(y)[(int64_t)m * N + n + r] = v[r];
+          else
+            static_cast<uint16_t*>(y)[(int64_t)m * N + n + r] = (uint16_t)f32_to_bf16_bits(v[r]);
+        }
       }
     }
+  }
 }
 
-// Tile choice: BM = 256 (4 waves x 64 rows) for M > 128, else 64 or 128;
-// BN from {64, 96, 128} (two loader threads per weight row) minimising
-// rounds(tiles / CUs) * (BN + 32), i.e. wave quantisation across the chip
-// plus a fixed per-tile overhead.
-template <int FMT, typename ST, int WM, int BN>
-static hipError_t launch_t(const MatmulArgs& a) {
-  constexpr int BM = 4 * WM * 16;
-  const int tiles_m = (int)((a.m + BM - 1) / BM), tiles_n = (int)((a.n + BN - 1) / BN);
-  dim3 grid((unsigned)(tiles_m * tiles_n));
-  hipLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, WM, BN>), grid, dim3(256), 0, a.stream, a.q,
-                     static_cast<const ST*>(a.scales), static_cast<const uint16_t*>(a.x), a.y, (int)a.m, (int)a.k,
-                     (int)a.n, (int)a.npad, a.y_dtype, tiles_m);
+hipError_t launch_pack_x(const MatmulArgs& a) {
+  const int64_t pack_blocks = (a.m + 15) / 16 * ((a.k / 32 + 3) / 4);
+  hipLaunchKernelGGL(pack_x_kernel, dim3((unsigned)pack_blocks), dim3(256), 0, a.stream,
+                     static_cast<const uint16_t*>(a.x), static_cast<uint16_t*>(a.scratch), (int)a.m, (int)a.k);
   return hipGetLastError();
 }
 
-template <int FMT, typename ST, int WM>
-static hipError_t launch_bn(const MatmulArgs& a, int cu_count) {
-  constexpr int BM = 4 * WM * 16;
-  const int64_t tiles_m = (a.m + BM - 1) / BM;
-  const int cands[3] = {64, 96, 128};
-  int best = 128;
-  int64_t best_cost = -1;
-  for (int bn : cands) {
-    const int64_t tiles = tiles_m * ((a.n + bn - 1) / bn);
-    const int64_t rounds = (tiles + cu_count - 1) / cu_count;
-    const int64_t cost = rounds * (bn + 32);
-    if (best_cost < 0 || cost < best_cost) {
-      best_cost = cost;
-      best = bn;
-    }
-  }
-  switch (best) {
-    case 64: return launch_t<FMT, ST, WM, 64>(a);
-    case 96: return launch_t<FMT, ST, WM, 96>(a);
-    default: return launch_t<FMT, ST, WM, 128>(a);
-  }
+template <int FMT, typename ST, int MT, int NTW>
+static hipError_t launch_t(const MatmulArgs& a) {
+  constexpr int BM = 16 * MT, BN = 64 * NTW;
+  const int tiles_m = (int)((a.m + BM - 1) / BM), tiles_n = (int)((a.n + BN - 1) / BN);
+  if (hipError_t e = launch_pack_x(a)) return e;
+  dim3 grid((unsigned)(tiles_m * tiles_n));
+  hipLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, MT, NTW>), grid, dim3(256), 0, a.stream, a.q,
+                     static_cast<const ST*>(a.scales), static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m,
+                     (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, tiles_m);
+  return hipGetLastError();
 }
 
+// Tile: BM = 128 rows (64 when M <= 64) x BN = 128 columns. Measured with
+// random data at M = 512 (K 4096, N 11008) and M = 256 (K 8192, N 28672)
+// against 64 x 128, 128 x 192 and a variant that dequantizes each weight tile
+// once into LDS for 256-row tiles: 128 x 128 was fastest or within 1% at both
+// shapes, on par with hipBLASLt's dense bf16 GEMM there.
 template <int FMT, typename ST>
-static hipError_t launch_wm(const MatmulArgs& a, int cu_count) {
-  if (a.m <= 64) return launch_bn<FMT, ST, 1>(a, cu_count);
-  if (a.m <= 128) return launch_bn<FMT, ST, 2>(a, cu_count);
-  return launch_bn<FMT, ST, 4>(a, cu_count);
+static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
+  (void)cu_count;
+  if (a.m <= 64) return launch_t<FMT, ST, 4, 2>(a);
+  return launch_t<FMT, ST, 8, 2>(a);
 }
 
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count) {
-  if (a.format == RQ_Q8_0) return launch_wm<RQ_Q8_0, float>(a, cu_count);
-  if (a.scale_dtype == RQ_F16) return launch_wm<RQ_Q4_0, uint16_t>(a, cu_count);
-  return launch_wm<RQ_Q4_0, float>(a, cu_count);
+  if (a.format == RQ_Q8_0) return launch_mt<RQ_Q8_0, float>(a, cu_count);
+  if (a.scale_dtype == RQ_F16) return launch_mt<RQ_Q4_0, uint16_t>(a, cu_count);
+  return launch_mt<RQ_Q4_0, float>(a, cu_count);
 }
 
 }  // namespace rq

@@ -10,8 +10,13 @@
 namespace rq {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+// Register arrays use native vector types: HIP's uint2/uint4 are union-backed
+// structs, and arrays of them can end up in scratch memory.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
@@ -65,12 +70,15 @@ struct MatmulArgs {
   int64_t m, k, n;  // m activation rows, k = in, n = out
   int64_t npad;     // n padded to a multiple of 16 (rows present in the chunked layout)
   hipStream_t stream;
+  void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
 };
 
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
 hipError_t launch_gemv(const MatmulArgs& a);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
+// Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).
+hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
 // Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
@@ -79,6 +87,12 @@ hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm,
 // ---- device helpers shared by every kernel that decodes weights -----------
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // Round-to-nearest-even f32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
