@@ -224,6 +224,8 @@ def main():
     ap.add_argument("--suite", choices=["headline", "all"], default="headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="time the decode shapes only (C1 GEMV, Q4 skinny, 70B M=1) for profiling")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -244,6 +246,19 @@ def main():
     # dense bf16 MFMA: 4 SIMDs per CU, 1024 flop per clock per SIMD on CDNA4
     peak_props = info["cu_count"] * 4 * 1024 * clock_ghz / 1e3
     log(f"device: {torch.cuda.get_device_name(0)} cu={info['cu_count']} clock={clock_ghz:.3f} GHz")
+
+    if args.only_decode:
+        lines = [hbm_line(torch, ctx, "Q8 decode GEMV", "q8", 1, 4096, 4096, "f32", "f32")]
+        for m in (1, 4, 16):
+            lines.append(hbm_line(torch, ctx, "Q4 decode skinny", "q4", m, 4096, 14336, "f32", "f32"))
+        for fmt in ("q8", "q4"):
+            lines.append(hbm_line(torch, ctx, "70B MLP", fmt, 1, 8192, 28672, "bf16", "bf16"))
+        for ln in lines:
+            log(f"{ln['workload']} {ln['fmt']} m={ln['m']}: cold {ln['cold_us']} us {ln['cold_GBs']} GB/s, "
+                f"warm {ln['warm_us']} us {ln['warm_GBs']} GB/s")
+        ctx.close()
+        print(json.dumps({"decode": lines}), flush=True)
+        return
 
     # ---- headline: Q8 GEMM M=512 K=4096 N=11008, bf16 in / bf16 out
     M, K, N = 512, 4096, 11008

@@ -474,12 +474,13 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   a.npad = w.npad;
   a.stream = (hipStream_t)stream;
   a.scratch = nullptr;
-  if (m > 16 && x_dtype == RQ_BF16) {
+  if (!(m <= 16 && w.in <= skinny_max_k(m)) && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
     if (int s = stream_scratch(c, a.stream, bytes, &a.scratch)) return s;
   }
-  hipError_t e = m <= 16                ? launch_gemv(a)
+  const bool skinny = m <= 16 && w.in <= skinny_max_k(m);
+  hipError_t e = skinny               ? launch_gemv(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
                                       : launch_gemm(a, c->cu_count);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");

@@ -1,185 +1,423 @@
-// gemv.hip — decode-regime (m <= 16) block-quantized GEMV for gfx950.
+// gemv.hip — decode-regime (m <= 16) block-quantized matmul on CDNA4 int8 MFMA.
 //
 // y[m, o] = sum_b scale[o, b] * sum_{k in block b} code[o, k] * x[m, k]
-// (the staged form of qlinear-q8, raster/quant/train.clj:77-108: the f32 scale
-// multiplies the f32 block partial instead of every element; the product of
-// an integer code and x is exact, so the per-element dequantized weight is the
-// same number, only the summation order differs).
+// (qlinear-q8, raster/quant/train.clj:77-108, and its Q4_0 form: the f32 scale
+// multiplies the block partial instead of every element).
 //
-// HBM-bound. Mapping: one wave owns ROWS consecutive output rows; its 64 lanes
-// stride along K in 16-byte chunks (Q8: 16 codes = half a block, Q4: 16 bytes =
-// one 32-block). A group of G wave-steps issues every 128-bit load of codes and
-// scales before any arithmetic, so each lane keeps G*ROWS*16 bytes in flight.
-// x is read through L1/L2 (it is shared by every wave). Lane partials are
-// reduced across the wave at the end.
+// HBM-bound: the kernel must stream the weights at full bandwidth while doing
+// as little VALU work per byte as possible. Weights go into
+// v_mfma_i32_16x16x64_i8 as they are stored (Q8 codes as int8; Q4 nibbles
+// unmasked to bytes 0..15 with zero-point 8 applied per block), so no weight
+// is ever converted to floating point.
+//
+// Activations are made integer with a 16-bit block fixed point: per (row m,
+// block b), with e from frexp(max |x|) (max |x| < 2^e), raised by one when
+// max|x| * 2^(15-e) would round above 32639,
+//   X_k = rne(x_k * 2^(15-e)),  |X_k| <= 32639,   x_k = 2^(e-15) X_k + d_k,
+//   |d_k| <= 2^(e-16) <= 2^-15 max|x|  (2^-14 max|x| after the raise),
+// and X_k = 256 L0_k + L1_k with int8 levels L0, L1 in [-128, 127]. Then
+// sum_k code_k x_k = 2^(e-15) (256 C0 + C1) + sum_k code_k d_k with C0, C1
+// the exact int32 dot products of the codes with each level: the products
+// code_k * X_k are exact, so d_k is the only rounding beyond f32.
+//
+// MFMA shape: A (16 rows x 64 k) holds activation variants, B (64 k x 16
+// columns) the weights of 16 output rows o for one 64-element window
+// (two 32-blocks). Row r of A is (activation row 4 mg + r/4, level r & 1,
+// block (r >> 1) & 1 of the window); a variant is zero on the k-slots of the
+// other block. The int32 result lane (col o, quad q) then holds, for
+// activation row 4 mg + q, the four partials C0/C1 of both blocks, and
+//   acc += f32(256 C0_b + C1_b [- 8 XS_b for Q4]) * (scale[o, b] * 2^(e_b - 15))
+// per block: about two VALU ops per block partial.
+//
+// A block of x holding Inf or NaN gets a NaN factor, so every output of that
+// activation row is NaN (Raster's f32 loop gives +-Inf or NaN there).
+//
+// Mapping: a workgroup (8 or 16 waves) decomposes x into LDS once, then
+// takes 16-row groups of the weight in turn (stride over the grid); each wave
+// streams its share of a group's windows, 4 windows per batch with the next
+// batch's loads in flight; the waves' partial sums meet in LDS.
+#include <algorithm>
+
 #include "rq_internal.h"
 
 namespace rq {
 
-// Loads N consecutive activations starting at element `off` as f32.
-template <int XT, int N>
-__device__ __forceinline__ void load_x(const void* x, int64_t off, float* out) {
-  if (XT == RQ_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + off);
-#pragma unroll
-    for (int i = 0; i < N / 4; i++) {
-      float4 v = p[i];
-      out[4 * i + 0] = v.x;
-      out[4 * i + 1] = v.y;
-      out[4 * i + 2] = v.z;
-      out[4 * i + 3] = v.w;
-    }
+namespace {
+
+
+// LDS layout (dynamic shared memory), offsets in bytes
+struct SkinnyLds {
+  int kp;       // k padded to whole windows
+  int nbp;      // blocks, padded (= kp / 32)
+  int lev;      // int8 lev[mt][2][kp]
+  int xsf;      // f32 xsf[mt + 1][nbp]: 2^(e-15), NaN for non-finite blocks; row mt zero
+  int xs;       // i32 xs[mt + 1][nbp]: sum of X over the block (Q4 zero-point); row mt zero
+  int zero;     // 16 zero bytes
+  int red;      // f32 red[waves][mg][64]
+  int bytes;
+  __host__ __device__ SkinnyLds(int mt, int k, int waves) {
+    kp = (k + 63) / 64 * 64;
+    nbp = kp / 32;
+    lev = 0;
+    xsf = mt * 2 * kp;
+    xs = xsf + (mt + 1) * nbp * 4;
+    zero = xs + (mt + 1) * nbp * 4;
+    red = zero + 16;
+    bytes = red + waves * (mt / 4) * 64 * 4;
+  }
+};
+
+template <int XT>
+__device__ __forceinline__ void load_x4(const void* x, int64_t off, bool ok, float (&v)[4]) {
+  if (!ok) {
+    v[0] = v[1] = v[2] = v[3] = 0.0f;
+  } else if (XT == RQ_F32) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + off);
+    v[0] = t[0];
+    v[1] = t[1];
+    v[2] = t[2];
+    v[3] = t[3];
   } else {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + off);
-#pragma unroll
-    for (int i = 0; i < N / 8; i++) {
-      uint4 v = p[i];
-      uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        out[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
-        out[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-      }
-    }
+    const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(x) + off);
+    v[0] = __uint_as_float(t[0] << 16);
+    v[1] = __uint_as_float(t[0] & 0xFFFF0000u);
+    v[2] = __uint_as_float(t[1] << 16);
+    v[3] = __uint_as_float(t[1] & 0xFFFF0000u);
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Decomposition of one item: 4 activations (row mm, elements k..k+3 of block
+// b) of the 8 lanes sharing a block. Writes both int8 levels to LDS and, from
+// the block's first lane, the block factor and level sum.
+__device__ __forceinline__ void decompose_item(const float (&v)[4], int mm, int b, int part, int k, int kp, int nbp,
+                                               int8_t* __restrict__ lev, float* __restrict__ xsf,
+                                               int* __restrict__ xs) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  // fmaxf drops NaN operands, so non-finite values are flagged separately
+  int bad = !(fabsf(v[0]) <= 3.402823466e38f && fabsf(v[1]) <= 3.402823466e38f && fabsf(v[2]) <= 3.402823466e38f &&
+              fabsf(v[3]) <= 3.402823466e38f);
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  bad |= __shfl_xor(bad, 1, 64);
+  bad |= __shfl_xor(bad, 2, 64);
+  bad |= __shfl_xor(bad, 4, 64);
+  int e = 0;
+  const bool finite = !bad;
+  if (finite && amax > 0.0f) {
+    (void)frexpf(amax, &e);
+    if (ldexpf(amax, 15 - e) > 32639.0f) e += 1;  // keeps |X| <= 32639: both levels fit int8
+  }
+  uint32_t l0 = 0u, l1 = 0u;
+  int sum = 0;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  for (int i = 0; i < 4; i++) {
+    const int X = finite ? (int)rintf(ldexpf(v[i], 15 - e)) : 0;
+    const int a = (X + 128) >> 8, c = X - 256 * a;
+    l0 |= (uint32_t)(a & 0xFF) << (8 * i);
+    l1 |= (uint32_t)(c & 0xFF) << (8 * i);
+    sum += X;
+  }
+  *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 0) * kp + k) = l0;
+  *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 1) * kp + k) = l1;
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  sum += __shfl_xor(sum, 4, 64);
+  if (part == 0) {
+    xsf[mm * nbp + b] = finite ? ldexpf(1.0f, e - 15) : __builtin_nanf("");
+    xs[mm * nbp + b] = sum;
+  }
 }
 
-template <int FMT, typename ST, int XT, int MT, int ROWS, int G>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                  const void* __restrict__ x, void* __restrict__ y, int M,
-                                                  int K, int N, int y_dtype) {
-  constexpr int EPC = FMT == RQ_Q8_0 ? 16 : 32;  // weight elements per 16-byte chunk
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * ROWS;
-  if (row0 >= N) return;  // wave-uniform
-  const int nb = K / 32;
-  const int64_t rowbytes = FMT == RQ_Q8_0 ? (int64_t)K : (int64_t)K / 2;
-  const int nchunks = (int)(rowbytes / 16);
+}  // namespace
 
-  float acc[MT][ROWS];
-#pragma unroll
-  for (int m = 0; m < MT; m++)
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) acc[m][r] = 0.0f;
+template <int FMT, typename ST, int XT, int MT, int WAVES, int NB>
+__global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
+                                                           const void* __restrict__ x, void* __restrict__ y, int M,
+                                                           int K, int N, int npad, int y_dtype) {
+  constexpr int MG = MT / 4;                 // MFMAs per window (4 activation rows each)
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const SkinnyLds L(MT, K, WAVES);
+  int8_t* lev = reinterpret_cast<int8_t*>(smem + L.lev);
+  float* xsf = reinterpret_cast<float*>(smem + L.xsf);
+  int* xs = reinterpret_cast<int*>(smem + L.xs);
+  float* red = reinterpret_cast<float*>(smem + L.red);
 
-  for (int c0 = 0; c0 < nchunks; c0 += 64 * G) {
-    uint4 raw[G][ROWS];
-    float s[G][ROWS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g4 = lane >> 4;
+  const int nb = K / 32, nw = L.kp / 64;
+  const int ngroups = npad / 16;
+
+  // ---- per-lane A-fragment addressing. Lane (r, g4) supplies k-slots of
+  // window block g4 >> 1; variant r = (row 4 mg + r/4, level r & 1, block
+  // (r >> 1) & 1) is zero unless that block matches (and the row exists).
+  const int lvl = r & 1, sel = (r >> 1) & 1;
+  int aoff[MG];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      const int c = c0 + g * 64 + lane;
+  for (int mg = 0; mg < MG; mg++) {
+    const int mm = 4 * mg + (r >> 2);
+    const bool match = sel == (g4 >> 1) && mm < M;
+    const int kin = FMT == RQ_Q8_0 ? 16 * g4 : 32 * (g4 >> 1) + 8 * (g4 & 1);
+    aoff[mg] = match ? (mm * 2 + lvl) * L.kp + kin : -1;
+  }
+  // this lane's activation row per MFMA (for xsf / xs), quad q = g4; rows
+  // past M read the zero row
+  int xrow[MG];
 #pragma unroll
-      for (int r = 0; r < ROWS; r++) {
-        const int row = row0 + r;
-        if (c < nchunks && row < N) {
-          const int64_t off = FMT == RQ_Q8_0 ? code_off<FMT>(row, c / 2, nb) + 16 * (c % 2) : code_off<FMT>(row, c, nb);
-          raw[g][r] = *reinterpret_cast<const uint4*>(q + off);
-          s[g][r] = load_scale<ST>(sc, scale_off(row, FMT == RQ_Q8_0 ? c / 2 : c, nb));
+  for (int mg = 0; mg < MG; mg++) xrow[mg] = (4 * mg + g4 < M ? 4 * mg + g4 : MT) * L.nbp;
+
+  // ---- wave's window range of each group
+  const int per = (nw + WAVES - 1) / WAVES;
+  const int wbeg = wave * per, wend = min(nw, wbeg + per);
+
+  // weight bytes per 16-row chunk, and this lane's offset inside a window
+  constexpr int CB = FMT == RQ_Q8_0 ? 32 : 16;
+  const int wlo = (g4 >> 1) * CB * 16 + r * CB + (FMT == RQ_Q8_0 ? 16 : 8) * (g4 & 1);
+  // last window this lane's block exists in (an odd block count leaves the
+  // second block of the last window empty: its lanes reread a valid block,
+  // which the zero A variants cancel)
+  const int wmax = (nb - 1 - (g4 >> 1)) / 2;
+
+  u32x4 wq[2][NB];
+  float s0[2][NB], s1[2][NB];
+  // weight window w of group g: this lane's 16 (Q8) / 8 (Q4) code bytes and
+  // the row's two block scales; all loads unconditional at clamped addresses
+  auto load_batch = [&](int slot, int wb, int g) {
+    const uint8_t* qg = q + (int64_t)g * nb * CB * 16;  // the group's chunks
+    const ST* sg = sc + (int64_t)g * nb * 16;           // and scales
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      const int w = min(wb + i, nw - 1);
+      const int off = wlo + min(w, wmax) * 2 * CB * 16;
+      if (FMT == RQ_Q8_0) {
+        wq[slot][i] = *reinterpret_cast<const u32x4*>(qg + off);
+      } else {
+        const u32x2 t = *reinterpret_cast<const u32x2*>(qg + off);
+        wq[slot][i] = u32x4{t[0], t[1], 0u, 0u};
+      }
+      s0[slot][i] = load_scale<ST>(sg, 32 * w + r);
+      const float t1 = load_scale<ST>(sg, 16 * min(2 * w + 1, nb - 1) + r);
+      s1[slot][i] = 2 * w + 1 < nb ? t1 : 0.0f;
+    }
+  };
+
+  // ---- activation decomposition into LDS. A wave only ever reads the
+  // activations of its own k-slice (windows wbeg..wend of every group), so
+  // each wave decomposes just that slice into its own part of the LDS
+  // arrays: no workgroup barrier. The first XJ items' activation loads go
+  // out before the first weight batch, so the decomposition waits only for
+  // them (loads complete in issue order).
+  const int nblk_w = 2 * max(wend - wbeg, 0);  // blocks of this wave's slice
+  const int witems = M * nblk_w * 8;            // 4-element items of the slice
+  constexpr int XJ = 4;
+  float xv[XJ][4];
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int it = min(lane + 64 * j, max(witems - 1, 0));
+    const int mm = it / max(nblk_w * 8, 1), k = 32 * (2 * wbeg + (it >> 3) % max(nblk_w, 1)) + 4 * (it & 7);
+    load_x4<XT>(x, (int64_t)mm * K + min(k, K - 4), true, xv[j]);
+    if (k >= K) xv[j][0] = xv[j][1] = xv[j][2] = xv[j][3] = 0.0f;
+  }
+  if (blockIdx.x < ngroups) load_batch(0, wbeg, blockIdx.x);
+  if (lane < 4) reinterpret_cast<uint32_t*>(smem + L.zero)[lane] = 0u;
+  if (lane < nblk_w) {
+    xsf[MT * L.nbp + 2 * wbeg + lane] = 0.0f;
+    xs[MT * L.nbp + 2 * wbeg + lane] = 0;
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const int it = lane + 64 * j;
+    if (it < witems) {
+      const int mm = it / (nblk_w * 8), b = 2 * wbeg + (it >> 3) % nblk_w, part = it & 7;
+      decompose_item(xv[j], mm, b, part, 32 * b + 4 * part, L.kp, L.nbp, lev, xsf, xs);
+    }
+  }
+  for (int it = lane + 64 * XJ; it < witems; it += 64) {
+    const int mm = it / (nblk_w * 8), b = 2 * wbeg + (it >> 3) % nblk_w, part = it & 7;
+    const int k = 32 * b + 4 * part;
+    float v[4];
+    load_x4<XT>(x, (int64_t)mm * K + k, k < K, v);
+    decompose_item(v, mm, b, part, k, L.kp, L.nbp, lev, xsf, xs);
+  }
+  // the wave reads back what its own lanes wrote
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  float acc[MG];
+#pragma unroll
+  for (int mg = 0; mg < MG; mg++) acc[mg] = 0.0f;
+
+  // Phases: every LDS read of the batch, then every MFMA, then every
+  // epilogue, so LDS latency and MFMA latency overlap across windows.
+  auto compute_batch = [&](int slot, int wb) {
+    i32x4 af[NB][MG];
+    float f0[NB][MG], f1[NB][MG];
+    int x0[NB][MG], x1[NB][MG];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      const int w = wb + i;
+      const bool live = w < wend;  // wave-uniform
+      const int wblk = 2 * min(w, nw - 1);
+#pragma unroll
+      for (int mg = 0; mg < MG; mg++) {
+        const int ao = live && aoff[mg] >= 0 ? aoff[mg] + 64 * w : L.zero - L.lev;
+        if (FMT == RQ_Q8_0) {
+          af[i][mg] = *reinterpret_cast<const i32x4*>(lev + ao);
         } else {
-          raw[g][r] = make_uint4(0, 0, 0, 0);
-          s[g][r] = 0.0f;
+          // the zero slot is 16 bytes: both 8-byte halves read zeros there
+          const int ao2 = live && aoff[mg] >= 0 ? ao + 16 : ao + 8;
+          const u32x2 h0 = *reinterpret_cast<const u32x2*>(lev + ao);
+          const u32x2 h1 = *reinterpret_cast<const u32x2*>(lev + ao2);
+          af[i][mg] = i32x4{(int)h0[0], (int)h0[1], (int)h1[0], (int)h1[1]};
         }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      const int c = c0 + g * 64 + lane;
-      if (c >= nchunks) continue;
-      const int64_t k0 = (int64_t)c * EPC;
-      // decode the chunk of every row once; reused for all m
-      float w[ROWS][EPC];
-#pragma unroll
-      for (int r = 0; r < ROWS; r++) {
-        const uint32_t d[4] = {raw[g][r].x, raw[g][r].y, raw[g][r].z, raw[g][r].w};
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            if (FMT == RQ_Q8_0) {
-              w[r][4 * i + j] = q8_code(d[i], j);
-            } else {
-              w[r][4 * i + j] = q4_nib(d[i], j, false);
-              w[r][16 + 4 * i + j] = q4_nib(d[i], j, true);
-            }
-          }
-      }
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < M) {
-        float xv[EPC];
-        load_x<XT, EPC>(x, (int64_t)m * K + k0, xv);
-        float xs = 0.0f;
+        const f32x2 fv = *reinterpret_cast<const f32x2*>(xsf + xrow[mg] + wblk);
+        f0[i][mg] = live ? fv[0] : 0.0f;
+        f1[i][mg] = live ? fv[1] : 0.0f;
         if (FMT == RQ_Q4_0) {
-#pragma unroll
-          for (int e = 0; e < EPC; e++) xs += xv[e];
-        }
-#pragma unroll
-        for (int r = 0; r < ROWS; r++) {
-          float p = 0.0f;
-#pragma unroll
-          for (int e = 0; e < EPC; e++) p = fmaf(w[r][e], xv[e], p);
-          if (FMT == RQ_Q4_0) p = fmaf(-8.0f, xs, p);  // zero-point 8
-          acc[m][r] = fmaf(s[g][r], p, acc[m][r]);
-        }
+          const i32x2 xv = *reinterpret_cast<const i32x2*>(xs + xrow[mg] + wblk);
+          x0[i][mg] = xv[0];
+          x1[i][mg] = xv[1];
         }
       }
     }
-  }
+    i32x4 c[NB][MG];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      i32x4 bfrag;
+      if (FMT == RQ_Q8_0) {
+        bfrag = __builtin_bit_cast(i32x4, wq[slot][i]);
+      } else {
+        const uint32_t d0 = wq[slot][i][0], d1 = wq[slot][i][1];
+        bfrag = i32x4{(int)(d0 & 0x0F0F0F0Fu), (int)(d1 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
+                      (int)((d1 >> 4) & 0x0F0F0F0Fu)};
+      }
+#pragma unroll
+      for (int mg = 0; mg < MG; mg++)
+        c[i][mg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][mg], bfrag, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+      for (int mg = 0; mg < MG; mg++) {
+        int t0 = (c[i][mg][0] << 8) + c[i][mg][1], t1 = (c[i][mg][2] << 8) + c[i][mg][3];
+        if (FMT == RQ_Q4_0) {
+          t0 -= 8 * x0[i][mg];
+          t1 -= 8 * x1[i][mg];
+        }
+        acc[mg] = fmaf((float)t0, s0[slot][i] * f0[i][mg], acc[mg]);
+        acc[mg] = fmaf((float)t1, s1[slot][i] * f1[i][mg], acc[mg]);
+      }
+  };
 
+  // ---- task stream: batch j of the wave's windows in group round i is task
+  // t = i * nbg + j. The next task's loads (possibly the next group's) are in
+  // flight while the current task computes and a finished group's partial
+  // sums are combined.
+  const int nbg = (per + NB - 1) / NB;  // batches per group
+  const int rounds = (int)blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int ntask = rounds * nbg;
+  auto task_load = [&](int slot, int t) {
+    const int g = (int)blockIdx.x + (t / nbg) * (int)gridDim.x;
+    load_batch(slot, wbeg + (t % nbg) * NB, min(g, ngroups - 1));
+  };
+  // combine the waves' partial sums of the group in wave order; lane (r, g4)
+  // of wave 0 writes y[4 mg + g4][16 g + r]
+  auto finish_group = [&](int t) {
+    const int g = (int)blockIdx.x + (t / nbg) * (int)gridDim.x;
 #pragma unroll
-  for (int m = 0; m < MT; m++) {
-    if (m < M) {
+    for (int mg = 0; mg < MG; mg++) {
+      red[(wave * MG + mg) * 64 + lane] = acc[mg];
+      acc[mg] = 0.0f;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int o = 16 * g + r;
 #pragma unroll
-      for (int r = 0; r < ROWS; r++) {
-        const float v = wave_sum(acc[m][r]);
-        const int row = row0 + r;
-        if (lane == 0 && row < N) {
+      for (int mg = 0; mg < MG; mg++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < WAVES; wv++) v += red[(wv * MG + mg) * 64 + lane];
+        const int m = 4 * mg + g4;
+        if (m < M && o < N) {
           if (y_dtype == RQ_F32)
-            static_cast<float*>(y)[(int64_t)m * N + row] = v;
+            static_cast<float*>(y)[(int64_t)m * N + o] = v;
           else
-            static_cast<uint16_t*>(y)[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(v);
+            static_cast<uint16_t*>(y)[(int64_t)m * N + o] = (uint16_t)f32_to_bf16_bits(v);
         }
       }
     }
+    __syncthreads();
+  };
+  // task 0's batch went out with the prologue (slot 0)
+  for (int t = 0; t < ntask; t += 2) {
+    task_load(1, t + 1);
+    compute_batch(0, wbeg + (t % nbg) * NB);
+    if (t % nbg == nbg - 1) finish_group(t);
+    if (t + 1 >= ntask) break;
+    task_load(0, t + 2);
+    compute_batch(1, wbeg + ((t + 1) % nbg) * NB);
+    if ((t + 1) % nbg == nbg - 1) finish_group(t + 1);
   }
 }
+
+// Waves per workgroup: a group's 64-element windows are split across the
+// waves, and short per-wave runs with many waves in flight stream small
+// weights fastest (the weight-load ramp dominates a few-microsecond call).
+template <int MT>
+struct SkinnyShape {
+  static constexpr int waves = MT == 4 ? 16 : 8;
+  static constexpr int nb = 4;  // windows per batch
+};
 
 template <int FMT, typename ST, int XT, int MT>
-static hipError_t launch_t(const MatmulArgs& a) {
-  constexpr int ROWS = FMT == RQ_Q8_0 ? 4 : 2;
-  constexpr int G = FMT == RQ_Q8_0 ? 4 : 4;
-  const int rows_per_block = 4 * ROWS;
-  dim3 grid((unsigned)((a.n + rows_per_block - 1) / rows_per_block));
-  hipLaunchKernelGGL((gemv_kernel<FMT, ST, XT, MT, ROWS, G>), grid, dim3(256), 0, a.stream, a.q,
-                     static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, a.y_dtype);
+static hipError_t launch_t(const MatmulArgs& a, int cu_count) {
+  constexpr int WAVES = SkinnyShape<MT>::waves, NB = SkinnyShape<MT>::nb;
+  const SkinnyLds L(MT, (int)a.k, WAVES);
+  const int ngroups = (int)(a.npad / 16);
+  // persistent grid: the workgroups that fit on the chip at once (LDS per CU
+  // 160 KB; 16 waves per CU at this kernel's register use)
+  const int per_cu = std::max(1, std::min(163840 / L.bytes, 16 / WAVES));
+  const int grid = std::min(ngroups, per_cu * cu_count);
+  static bool attr = false;  // dynamic LDS above 64 KB must be allowed once per kernel
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<FMT, ST, XT, MT, WAVES, NB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((skinny_kernel<FMT, ST, XT, MT, WAVES, NB>), dim3((unsigned)grid), dim3(64 * WAVES),
+                     (unsigned)L.bytes, a.stream,
+                     a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                     a.y_dtype);
   return hipGetLastError();
 }
 
 template <int FMT, typename ST, int XT>
-static hipError_t launch_m(const MatmulArgs& a) {
-  if (a.m <= 1) return launch_t<FMT, ST, XT, 1>(a);
-  if (a.m <= 2) return launch_t<FMT, ST, XT, 2>(a);
-  if (a.m <= 4) return launch_t<FMT, ST, XT, 4>(a);
-  if (a.m <= 8) return launch_t<FMT, ST, XT, 8>(a);
-  return launch_t<FMT, ST, XT, 16>(a);
+static hipError_t launch_m(const MatmulArgs& a, int cu_count) {
+  if (a.m <= 4) return launch_t<FMT, ST, XT, 4>(a, cu_count);
+  if (a.m <= 8) return launch_t<FMT, ST, XT, 8>(a, cu_count);
+  return launch_t<FMT, ST, XT, 16>(a, cu_count);
 }
 
 template <int FMT, typename ST>
-static hipError_t launch_x(const MatmulArgs& a) {
-  return a.x_dtype == RQ_F32 ? launch_m<FMT, ST, RQ_F32>(a) : launch_m<FMT, ST, RQ_BF16>(a);
+static hipError_t launch_x(const MatmulArgs& a, int cu_count) {
+  return a.x_dtype == RQ_F32 ? launch_m<FMT, ST, RQ_F32>(a, cu_count) : launch_m<FMT, ST, RQ_BF16>(a, cu_count);
 }
 
-hipError_t launch_gemv(const MatmulArgs& a) {
-  if (a.format == RQ_Q8_0) return launch_x<RQ_Q8_0, float>(a);
-  if (a.scale_dtype == RQ_F16) return launch_x<RQ_Q4_0, uint16_t>(a);
-  return launch_x<RQ_Q4_0, float>(a);
+// Largest k the skinny kernel's LDS holds for m activation rows (rows are
+// processed in groups of 4, 8 or 16).
+int64_t skinny_max_k(int64_t m) {
+  const int mt = m <= 4 ? 4 : m <= 8 ? 8 : 16;
+  const int waves = mt == 4 ? SkinnyShape<4>::waves : SkinnyShape<8>::waves;
+  int64_t k = 64;
+  while (SkinnyLds(mt, (int)(k + 64), waves).bytes <= 163840) k += 64;
+  return k;
+}
+
+hipError_t launch_gemv(const MatmulArgs& a, int cu_count) {
+  if (a.format == RQ_Q8_0) return launch_x<RQ_Q8_0, float>(a, cu_count);
+  if (a.scale_dtype == RQ_F16) return launch_x<RQ_Q4_0, uint16_t>(a, cu_count);
+  return launch_x<RQ_Q4_0, float>(a, cu_count);
 }
 
 }  // namespace rq

@@ -12,6 +12,8 @@ namespace rq {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 // Register arrays use native vector types: HIP's uint2/uint4 are union-backed
 // structs, and arrays of them can end up in scratch memory.
@@ -74,7 +76,9 @@ struct MatmulArgs {
 };
 
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
-hipError_t launch_gemv(const MatmulArgs& a);
+hipError_t launch_gemv(const MatmulArgs& a, int cu_count);
+// Largest k the decode kernel (launch_gemv) supports for m activation rows.
+int64_t skinny_max_k(int64_t m);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).

@@ -233,6 +233,84 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
     assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
 
 
+# ---------------------------------------------------------------- decode kernel edges
+@pytest.mark.parametrize("m,in_,out", [(1, 32, 16), (3, 96, 40), (16, 160, 33), (5, 4096, 48), (16, 4096, 64)])
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_decode_shapes_and_error_bound(torch, ctx, orc, m, in_, out, fmt, xdt):
+    # odd block counts (1, 3, 5 blocks: a half window at the end), ragged
+    # output rows, every m-group size; error inside the derived bound
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=11 * m + in_, dtype=xdt)
+    note(f"decode {fmt} {xdt} m={m} {out}x{in_}")
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=out + in_)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        ref = orc.qlinear_q8(x, codes, scales, m, in_, out)
+        dense = orc.dequant_q8_dense(codes, scales, in_, out)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=out + in_)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+        ref = orc.qlinear_q4(x, packed, sc16, m, in_, out)
+        dense = orc.dequant_q4(packed, sc16, in_, out)
+    y = run(torch, w, x, m, xdt, "f32")
+    w.destroy()
+    ref = ref.reshape(m, out)
+    assert orc.normwise_relerr(y, ref) < TOL_F32
+    assert np.all(np.abs(y - ref) <= decomposition_bound(x, dense, m, in_, out))
+
+
+def test_decode_special_activations(torch, ctx, orc):
+    # per-block exponents: a block with 1e30 next to 1e-30, a zero row, an
+    # inf row and a NaN row; finite rows stay inside the bound, the zero row
+    # is exactly zero, and rows with a non-finite activation are non-finite
+    # (the kernel writes NaN; Raster's f32 loop gives +-inf or NaN)
+    import raster_amd
+
+    m, in_, out = 6, 128, 24
+    codes, scales = wl.q8_weights(out, in_, seed=5)
+    x = wl.activations(m, in_, seed=6).reshape(m, in_)
+    x[1, 0], x[1, 1] = 1e30, 1e-30
+    x[1, 40:64] *= 1e-20
+    x[2] = 0.0
+    x[3, 70] = np.inf
+    x[4, 5] = np.nan
+    x[5] *= 1e-35                       # subnormal-range block maxima
+    x = np.ascontiguousarray(x.ravel())
+    note("decode special activations")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    y = run(torch, w, x, m, "f32", "f32")
+    w.destroy()
+    ref = orc.qlinear_q8(x, codes, scales, m, in_, out).reshape(m, out)
+    dense = orc.dequant_q8_dense(codes, scales, in_, out)
+    fin = [0, 1, 2, 5]
+    xf = x.reshape(m, in_)[fin].ravel()
+    bound = decomposition_bound(xf, dense, len(fin), in_, out)
+    assert np.all(np.abs(y[fin] - ref[fin]) <= bound)
+    assert np.all(y[2] == 0.0)
+    assert not np.any(np.isfinite(y[3])) and not np.any(np.isfinite(y[4]))
+    assert not np.any(np.isfinite(ref[3])) and not np.any(np.isfinite(ref[4]))
+
+
+def test_decode_falls_back_above_lds_limit(torch, ctx, orc):
+    # k beyond the decode kernel's LDS capacity goes to the GEMM kernels
+    import raster_amd
+
+    m, in_, out = 2, 20480, 16
+    codes, scales = wl.q8_weights(out, in_, seed=8)
+    x = wl.activations(m, in_, seed=9)
+    note("decode fallback k=20480")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    y = run(torch, w, x, m, "f32", "f32")
+    yb = run(torch, w, x, m, "bf16", "f32")
+    w.destroy()
+    ref = orc.qlinear_q8(x, codes, scales, m, in_, out).reshape(m, out)
+    assert orc.normwise_relerr(y, ref) < TOL_F32
+    refb = orc.qlinear_q8(wl.bf16_round(x), codes, scales, m, in_, out).reshape(m, out)
+    assert orc.normwise_relerr(yb, refb) < TOL_BF16
+
+
 def test_gemm_q4_bf16_m256(torch, ctx, orc):
     import raster_amd
 
@@ -314,6 +392,24 @@ def test_q8_packed_ingestion(torch, ctx, orc):
 
 
 # ---------------------------------------------------------------- host surface + errors
+def decomposition_bound(x, wdense, m, in_, out):
+    """Per-output bound on |decode kernel - exact| for f32/bf16 activations:
+    the kernel rounds each activation to a 16-bit block fixed point with
+    |error| <= 2^(e-16) (e from frexp of the block max, raised by one where
+    max * 2^(15-e) > 32639), so |dy[m,o]| <= sum_b 2^(e_mb-16) sum_k |W[o,k]|,
+    plus f32 accumulation slack."""
+    xb = np.abs(np.asarray(x, np.float64).reshape(m, in_ // 32, 32))
+    amax = xb.max(axis=2)
+    _, e = np.frexp(amax)
+    e = np.where(amax > 0, e, 0)
+    e = np.where(np.ldexp(amax, 15 - e) > 32639.0, e + 1, e)
+    step = np.ldexp(1.0, e - 16)                                 # [m, nb]
+    wabs = np.abs(np.asarray(wdense, np.float64).reshape(out, in_ // 32, 32)).sum(axis=2)  # [out, nb]
+    bound = step @ wabs.T                                        # [m, out]
+    mag = np.abs(np.asarray(x, np.float64).reshape(m, in_)) @ np.abs(np.asarray(wdense, np.float64).reshape(out, in_)).T
+    return bound + 1e-6 * mag + 1e-30
+
+
 def test_qlinear_q8_host_surface(torch, ctx, orc):
     # the shapes of test/raster/quant/train_test.clj:26-40
     import raster_amd
@@ -325,7 +421,10 @@ def test_qlinear_q8_host_surface(torch, ctx, orc):
     note("qlinear_q8 host")
     y = raster_amd.qlinear_q8(X, codes, scales, m, in_, out, ctx=ctx)
     ref = orc.qlinear_q8(X, codes, scales, m, in_, out)
-    assert np.max(np.abs(y - ref)) < 1e-5
+    assert orc.normwise_relerr(y, ref) < TOL_F32
+    dense = orc.dequant_q8_dense(codes, scales, in_, out)
+    bound = decomposition_bound(X, dense, m, in_, out)
+    assert np.all(np.abs(y.reshape(m, out) - ref.reshape(m, out)) <= bound)
     Wd = raster_amd.dequant_q8_dense(codes, scales, in_, out, ctx=ctx)
     assert np.array_equal(Wd, orc.dequant_q8_dense(codes, scales, in_, out))
     with pytest.raises(AssertionError):
