@@ -15,8 +15,17 @@ Beside it, on the same JSON line:
            enough weight copies (> 512 MB) that every call reads its weight
            from HBM, not the 256 MB Infinity Cache ("cold"); warm = one copy.
   sweep  - (--suite all) Q4 skinny M in {1,4,16} and the 70B-MLP shapes.
-  roofline      - the GEMM kernel against dense bf16 MFMA peak.
-  roofline_gemv - the GEMV kernel against HBM peak.
+  roofline      - the GEMM kernel against dense bf16 MFMA peak: 2*M*K*N flop
+                  per launch over the kernel's average duration, from the start
+                  and end timestamps of its own dispatch, which librq captures in
+                  HIP events on the call's stream (rq_ctx_set_kernel_timing)
+                  during the timed steps. A step also runs the small
+                  activation-packing kernel, so `value` is lower.
+  roofline_gemv - the decode kernel against HBM peak: algorithmic bytes per
+                  launch over its cold per-call time (the graph replays above:
+                  one kernel per call, launch gaps included).
+  traffic       - HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and
+                  WRITE_SIZE runs, committed under profiles/ (null if absent).
   cpu_baseline  - the C restatement of Raster's qlinear-q8 loop
                   (oracle/cpu_baseline.c) on a row sample of the same GEMM,
                   all host threads; reported only.
@@ -170,6 +179,36 @@ def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
             "us": round(ms * 1e3, 3), "TFLOPs": round(tf, 2), "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
+COPY_ELEMS = 64 << 20  # f32 elements of the calibration copy: 256 MiB read + 256 MiB written
+
+
+def traffic_run(torch, ctx, launches=5):
+    """Kernels for the HBM-traffic counter passes, `launches` of each:
+    torch.neg over COPY_ELEMS f32 (a plain elementwise copy reading and writing
+    exactly 256 MiB, the calibration of the counters), the headline GEMM step
+    (activation pack + GEMM kernel) and the C1 decode kernel on its cold weight
+    rotation."""
+    src = torch.randn(COPY_ELEMS, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(launches):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    head = Case(torch, ctx, "q8", 512, 4096, 11008, "bf16", "bf16")
+    for _ in range(launches):
+        head.step()
+    torch.cuda.synchronize()
+    head.destroy()
+    one = q8_bytes(1, 4096, 4096, 4, 4)
+    dec = Case(torch, ctx, "q8", 1, 4096, 4096, "f32", "f32", copies=copies_for_cold(one))
+    for _ in range(len(dec.weights)):
+        dec.step()
+    torch.cuda.synchronize()
+    dec.destroy()
+    log(f"traffic run: {launches} x neg({COPY_ELEMS} f32), {launches} x C2 GEMM step, "
+        f"{copies_for_cold(one)} x C1 decode (cold rotation)")
+
+
 def read_traffic(kernel_tag):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary
     (profiles/<kernel_tag>_pmc.txt, line `traffic_bytes_per_launch: N`)."""
@@ -209,11 +248,15 @@ def cpu_baseline(m, k, n, budget_s=10.0):
 
     t1 = run(1)
     rows = int(max(1, min(m, budget_s / max(t1, 1e-6))))
-    dt = run(rows)
-    flop = 2.0 * rows * k * n
+    # whole passes over `rows` rows until about budget_s of wall time is spent
+    reps, dt = 0, 0.0
+    while reps == 0 or dt < budget_s:
+        dt += run(rows)
+        reps += 1
+    flop = 2.0 * rows * k * n * reps
     return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"qlinear-q8 loop (f32 products, f64 accumulation) over {rows} of {m} activation rows "
-                      f"x K={k} x N={n}, {dt:.2f} s, {threads} threads"}
+            "sample": f"qlinear-q8 loop (f32 products, f64 accumulation), {reps} pass(es) over {rows} of {m} "
+                      f"activation rows x K={k} x N={n}, {dt:.2f} s, {threads} threads"}
 
 
 def main():
@@ -226,6 +269,9 @@ def main():
     ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
     ap.add_argument("--only-decode", action="store_true",
                     help="time the decode shapes only (C1 GEMV, Q4 skinny, 70B M=1) for profiling")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="a short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: a copy kernel of "
+                         "known size (calibration), then the headline GEMM and the cold C1 decode kernel")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -260,6 +306,11 @@ def main():
         print(json.dumps({"decode": lines}), flush=True)
         return
 
+    if args.traffic_run:
+        traffic_run(torch, ctx)
+        ctx.close()
+        return
+
     # ---- headline: Q8 GEMM M=512 K=4096 N=11008, bf16 in / bf16 out
     M, K, N = 512, 4096, 11008
     log(f"headline gemm q8 m={M} k={K} n={N} steps={args.steps} warmup={args.warmup}")
@@ -269,6 +320,11 @@ def main():
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ctx.kernel_time()
+    # librq captures the GEMM dispatch's own start/end timestamps in HIP
+    # events on the call's stream (torch's current stream here), which
+    # separates the kernel from the activation-packing pass for the roofline
+    ctx.set_kernel_timing(True)
     t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(args.steps):
@@ -276,10 +332,15 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    kern_total, kern_n = ctx.kernel_time()
+    ctx.set_kernel_timing(False)
     ms = e0.elapsed_time(e1) / args.steps
+    kern_ms = kern_total / max(kern_n, 1)
     head.destroy()
     tflops = head.flops / ms / 1e9
-    log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s (wall {wall:.3f} s)")
+    kern_tflops = head.flops / kern_ms / 1e9
+    log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s (wall {wall:.3f} s); "
+        f"GEMM kernel {kern_ms * 1e3:.2f} us avg over {kern_n} launches, {kern_tflops:.1f} TFLOP/s")
 
     result = {
         "metric": METRIC,
@@ -297,10 +358,12 @@ def main():
         "config": {"workload": "Q8 prefill GEMM, Llama-7B MLP up-projection: M=512 K=4096 N=11008, "
                                "bf16 activations, f32 accumulation, bf16 output",
                    "m": M, "k": K, "n": N, "weights": "q8_0 resident in HBM"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": read_traffic("gemm_q8_bf16_C2"),
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 3), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(kern_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": read_traffic("gemm_bf16_q8_C2"),
                      "peak_from_device_props": round(peak_props, 1),
-                     "kernel": "rq::gemm_kernel<0, float, 1>", "flop_per_launch": head.flops},
+                     "kernel": "rq::gemm_bf16_kernel<0, float, 8, 2>", "flop_per_launch": head.flops,
+                     "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
 
     if not args.only_gemm:
@@ -308,10 +371,15 @@ def main():
         log("gemv q8 m=1 k=4096 n=4096 (cold rotation + warm)")
         gv = hbm_line(torch, ctx, "Q8 decode GEMV", "q8", 1, 4096, 4096, "f32", "f32")
         result["gemv"] = gv
-        result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["cold_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                   "frac": gv["cold_frac_hbm"], "traffic": read_traffic("gemv_q8_f32_C1"),
-                                   "kernel": "rq::gemv_kernel<0, float, 0, 1, 4, 4>",
-                                   "bytes_per_launch": gv["bytes"]}
+        # a decode step is this one kernel: its average duration is the cold
+        # graph's time per call (100 launches back to back, HIP events around
+        # each replay on the replaying stream; the ~0.7 us gaps between
+        # launches are included, so the rate is a lower bound)
+        result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["cold_GBs"], "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "frac": gv["cold_frac_hbm"],
+                                   "traffic": read_traffic("skinny_q8_f32_C1"),
+                                   "kernel": "rq::skinny_kernel<0, float, 0, 4, 16, 4>",
+                                   "bytes_per_launch": gv["bytes"], "kernel_avg_us": gv["cold_us"]}
         log(f"gemv: cold {gv['cold_us']} us {gv['cold_GBs']} GB/s; warm {gv['warm_us']} us {gv['warm_GBs']} GB/s")
 
     if args.suite == "all" and not args.only_gemm:

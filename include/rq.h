@@ -72,6 +72,18 @@ int rq_ctx_destroy(rq_ctx ctx);
 /* Number of compute units and the wavefront size of the context's device. */
 int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz);
 
+/* Kernel timing for measurement harnesses. No counterpart in the reference,
+ * whose microbench (raster/runtime/microbench.clj:20-60) times whole calls;
+ * this one separates the main kernel of a call (the MFMA GEMM or the decode
+ * kernel) from the small activation-packing pass of the bf16 GEMM.
+ * While enabled, every rq_qmatmul on this context launches its main kernel
+ * with a pair of HIP events that take that dispatch's own start and end
+ * timestamps (hipExtLaunchKernel; not on a stream that is being captured).
+ * rq_ctx_kernel_time waits for the pending pairs, returns their summed
+ * duration and count, and clears them. Disabling frees the events. */
+int rq_ctx_set_kernel_timing(rq_ctx ctx, int enable);
+int rq_ctx_kernel_time(rq_ctx ctx, double* total_ms, int64_t* launches);
+
 /* ---- device memory and streams (raster/gpu/ze_runtime.clj:765-787 DeviceBuffer) */
 int rq_buf_alloc(rq_ctx ctx, size_t bytes, void** dptr);
 int rq_buf_free(rq_ctx ctx, void* dptr);
@@ -90,7 +102,7 @@ int rq_sync(rq_ctx ctx, void* stream);
 int rq_weight_create_q8(rq_ctx ctx, const int8_t* codes, const float* scales, int64_t out, int64_t in,
                         rq_weight* w);
 /* Q8_0 from quantize-one-q8's packed words: wp int32[out*in/4] (4 little-endian
- * int8 lanes each), ws f32[out*in/32] (raster/quant/pack.clj:210-236). */
+ * int8 lanes each), ws f32[out*in/32] (raster/quant/pack.clj:55-81). */
 int rq_weight_create_q8_packed(rq_ctx ctx, const int32_t* wp, const float* ws, int64_t out, int64_t in,
                                rq_weight* w);
 /* Q4_0 row-major: packed u8[out*in/2]; scales are f32 (Raster's Q4_0 ws,
@@ -106,7 +118,13 @@ int rq_weight_create_x8(rq_ctx ctx, const uint8_t* wqi, const float* wsi, int ni
                         rq_weight* w);
 int rq_weight_destroy(rq_weight w);
 int rq_weight_info(rq_weight w, int* format, int64_t* out, int64_t* in, int* scale_dtype, size_t* device_bytes);
-/* Device pointers to the resident codes/packed bytes and scales (read-only). */
+/* Device pointers to the resident codes/packed bytes and scales (read-only).
+ * The resident form is NOT Raster's row-major layout: rows are padded to
+ * npad = ceil(out/16)*16 and stored in 16-row x 32-element chunks, chunk
+ * (r/16, b) at index (r/16)*(in/32) + b. A chunk holds the 16 rows' code blocks
+ * back to back (16 x 32 B for Q8_0, 16 x 16 B for Q4_0, each block in Raster's
+ * byte order) and the scales chunk holds the 16 rows' scales of block b.
+ * Padded rows are zero codes with zero scales. */
 int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
 
 /* ---- compute ---------------------------------------------------------------- */
@@ -116,7 +134,29 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * RQ_BF16), both device pointers, row-major. Replaces qlinear-q8
  * (raster/quant/train.clj:77-108) and, for Q4_0, the f32-activation dequant
  * GEMV; m <= 16 runs the HBM-bound GEMV kernels, larger m the MFMA GEMM.
- * m == 0 is a no-op. */
+ * m == 0 is a no-op.
+ *
+ * Numerics (all accumulation in f32):
+ *  - m <= 16 (and in small enough for the activation slice to fit in LDS:
+ *    in <= 17216 at m <= 4, 8704 at m <= 8, 4288 at m <= 16): int8 MFMA on the
+ *    raw weight codes. Each 32-block of each activation row is held as a 16-bit
+ *    block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
+ *    exponent, |X| < 2^15, so the per-element error is <= 2^(e-16) (below
+ *    1.6e-5 relative to the block maximum). An inf or NaN activation makes its
+ *    row's outputs NaN.
+ *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
+ *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA.
+ *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
+ *    split into two bf16 terms (about 16 mantissa bits).
+ *  - m <= 16 with a larger in: the f32-activation GEMM path above.
+ *
+ * bf16 x with m > 16 uses a per-stream scratch buffer (the packed activation
+ * tile, ceil(m/16)*16*in*2 bytes) that the context allocates on first use and
+ * grows on demand; it is freed by rq_ctx_destroy. Calls on one stream are
+ * ordered, calls on different streams do not share scratch. Under HIP graph
+ * capture no allocation can happen: run the same (or a larger) shape once on
+ * the capturing stream before capturing, otherwise the call fails with
+ * RQ_ERR_HIP and a message saying so. */
 int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                void* stream);
 

@@ -76,14 +76,14 @@ void rqo_jfill_gauss(int64_t seed, double mult, float* out, int64_t n) {
   for (int64_t i = 0; i < n; i++) out[i] = (float)(mult * rqo_jrandom_next_gaussian(&r));
 }
 
-/* pack_test.clj:125-128: (float (- (.nextDouble r) 0.5)) */
+/* pack_test.clj:9-12: (float (- (.nextDouble r) 0.5)) */
 void rqo_jfill_uniform_centered(int64_t seed, float* out, int64_t n) {
   rqo_jrandom r;
   rqo_jrandom_init(&r, seed);
   for (int64_t i = 0; i < n; i++) out[i] = (float)(rqo_jrandom_next_double(&r) - 0.5);
 }
 
-/* tile_test.clj:195-196: (.nextBytes (java.util.Random. seed) a) */
+/* tile_test.clj:10-11: (.nextBytes (java.util.Random. seed) a) */
 void rqo_jfill_bytes(int64_t seed, int8_t* out, int64_t n) {
   rqo_jrandom r;
   rqo_jrandom_init(&r, seed);

@@ -23,8 +23,8 @@ extern "C" {
 #endif
 
 /* ---- java.util.Random (JDK LCG) — used to regenerate the reference tests'
- *      inputs (e.g. test/raster/quant/train_test.clj:14-16, pack_test.clj:125-128,
- *      tile_test.clj:195-196). nextGaussian uses the C library log/sqrt where
+ *      inputs (e.g. test/raster/quant/train_test.clj:14-16, pack_test.clj:9-12,
+ *      tile_test.clj:10-11). nextGaussian uses the C library log/sqrt where
  *      the JDK uses StrictMath (fdlibm); the two can differ in the last bit on
  *      rare inputs, so Gaussian draws only feed tolerance-based checks. */
 typedef struct {
@@ -41,8 +41,8 @@ double rqo_jrandom_next_gaussian(rqo_jrandom* r);
 void rqo_jrandom_next_bytes(rqo_jrandom* r, int8_t* out, int64_t n);
 /* fill helpers matching the reference tests' generators */
 void rqo_jfill_gauss(int64_t seed, double mult, float* out, int64_t n);       /* train_test.clj:14-16 */
-void rqo_jfill_uniform_centered(int64_t seed, float* out, int64_t n);         /* pack_test.clj:125-128 */
-void rqo_jfill_bytes(int64_t seed, int8_t* out, int64_t n);                   /* tile_test.clj:195-196 */
+void rqo_jfill_uniform_centered(int64_t seed, float* out, int64_t n);         /* pack_test.clj:9-12 */
+void rqo_jfill_bytes(int64_t seed, int8_t* out, int64_t n);                   /* tile_test.clj:10-11 */
 
 /* Java Math.round(double): floor(x + 0.5) evaluated exactly; NaN -> 0. */
 int64_t rqo_java_round(double x);
@@ -119,7 +119,7 @@ void rqo_qmatmul_q8_x8(const int8_t* xq, const float* xs, const int32_t* xsum,
                        int64_t in, int64_t out, int64_t g_start, int64_t g_count);
 
 /* ---- signed q8_0 x q8_0 prefill path ---- */
-/* quantize-one-q8: raster/quant/pack.clj:210-236. Returns -1 if in % 32 != 0. */
+/* quantize-one-q8: raster/quant/pack.clj:55-81. Returns -1 if in % 32 != 0. */
 int rqo_quantize_one_q8(const float* W, int64_t in, int64_t out, int32_t* wp, float* ws);
 /* quant-act-i8-rows-gpu!: raster/quant/kernels_k.clj:309-342 (no clamp). */
 void rqo_quant_act_i8_rows(const float* x, int32_t* xp, float* xs, int64_t in, int64_t nrows);

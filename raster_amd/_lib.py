@@ -25,6 +25,8 @@ SIGNATURES = {
     "rq_ctx_create": ([_i, C.POINTER(_p)], _i),
     "rq_ctx_destroy": ([_p], _i),
     "rq_ctx_device_info": ([_p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)], _i),
+    "rq_ctx_set_kernel_timing": ([_p, _i], _i),
+    "rq_ctx_kernel_time": ([_p, C.POINTER(C.c_double), C.POINTER(_i64)], _i),
     "rq_buf_alloc": ([_p, _sz, C.POINTER(_p)], _i),
     "rq_buf_free": ([_p, _p], _i),
     "rq_upload": ([_p, _p, _p, _sz, _p], _i),

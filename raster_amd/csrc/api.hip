@@ -4,6 +4,7 @@
 // by one mutex, so a destroyed, double-freed or foreign handle is reported as
 // RQ_ERR_HANDLE instead of being dereferenced. Errors carry a message in a
 // thread-local string (rq_last_error).
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <string>
@@ -27,6 +28,12 @@ struct Ctx {
   // freed with the context. Calls on one stream run in order, so a stream's
   // buffer is never used by two kernels at once.
   std::unordered_map<hipStream_t, std::pair<void*, size_t>> scratch;
+  // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
+  // end timestamps of each rq_qmatmul's main kernel, waiting to be read, and a
+  // pool of spares.
+  std::atomic<bool> timing{false};
+  std::mutex timing_mu;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_pending, ev_pool;
 };
 
 static constexpr uint32_t kCtxMagic = 0x52514358u;     // "RQCX"
@@ -173,6 +180,46 @@ static int stream_scratch(Ctx* c, hipStream_t stream, size_t bytes, void** out) 
   return RQ_OK;
 }
 
+// An event pair for timing the main kernel of one call on `stream`, or
+// {nullptr, nullptr} when timing is off or the stream is being captured.
+static std::pair<hipEvent_t, hipEvent_t> timing_pair(Ctx* c, hipStream_t stream) {
+  if (!c->timing.load(std::memory_order_relaxed)) return {nullptr, nullptr};
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return {nullptr, nullptr};
+  std::lock_guard<std::mutex> lk(c->timing_mu);
+  if (!c->ev_pool.empty()) {
+    auto p = c->ev_pool.back();
+    c->ev_pool.pop_back();
+    return p;
+  }
+  // timing-only events (no system-scope fence: nothing is synchronised through them)
+  hipEvent_t a = nullptr, b = nullptr;
+  if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return {nullptr, nullptr};
+  if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return {nullptr, nullptr};
+  }
+  return {a, b};
+}
+
+static void timing_done(Ctx* c, std::pair<hipEvent_t, hipEvent_t> p, bool launched) {
+  if (!p.first) return;
+  std::lock_guard<std::mutex> lk(c->timing_mu);
+  (launched ? c->ev_pending : c->ev_pool).push_back(p);
+}
+
+static void timing_release(Ctx* c) {
+  std::lock_guard<std::mutex> lk(c->timing_mu);
+  for (auto* v : {&c->ev_pending, &c->ev_pool}) {
+    for (auto& p : *v) {
+      (void)hipEventSynchronize(p.second);
+      (void)hipEventDestroy(p.first);
+      (void)hipEventDestroy(p.second);
+    }
+    v->clear();
+  }
+}
+
 static void free_weight_locked(Weight* w) {
   (void)hipSetDevice(w->device);
   (void)hipFree(w->base);
@@ -242,6 +289,7 @@ int rq_ctx_destroy(rq_ctx h) {
   for (Weight* w : c->weights) free_weight_locked(w);
   for (void* b : c->buffers) (void)hipFree(b);
   for (auto& kv : c->scratch) (void)hipFree(kv.second.first);
+  timing_release(c);
   c->magic = 0;
   g_ctxs.erase(c);
   delete c;
@@ -254,6 +302,43 @@ int rq_ctx_device_info(rq_ctx h, int* cu_count, int* wave_size, int* clock_khz) 
   if (cu_count) *cu_count = c->cu_count;
   if (wave_size) *wave_size = c->wave_size;
   if (clock_khz) *clock_khz = c->clock_khz;
+  return RQ_OK;
+}
+
+int rq_ctx_set_kernel_timing(rq_ctx h, int enable) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (int s = set_device(c)) return s;
+  c->timing.store(enable != 0);
+  if (!enable) timing_release(c);
+  return RQ_OK;
+}
+
+int rq_ctx_kernel_time(rq_ctx h, double* total_ms, int64_t* launches) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!total_ms || !launches) return fail(RQ_ERR_NULL, "total_ms or launches is NULL");
+  if (int s = set_device(c)) return s;
+  std::lock_guard<std::mutex> lk(c->timing_mu);
+  double sum = 0.0;
+  int64_t n = 0;
+  hipError_t err = hipSuccess;
+  for (auto& p : c->ev_pending) {
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(p.second);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.first, p.second);
+    if (e == hipSuccess) {
+      sum += ms;
+      n++;
+    } else if (err == hipSuccess) {
+      err = e;
+    }
+    c->ev_pool.push_back(p);
+  }
+  c->ev_pending.clear();
+  *total_ms = sum;
+  *launches = n;
+  if (err != hipSuccess) return hip_fail(err, "reading kernel timing events");
   return RQ_OK;
 }
 
@@ -480,9 +565,13 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
     if (int s = stream_scratch(c, a.stream, bytes, &a.scratch)) return s;
   }
   const bool skinny = m <= 16 && w.in <= skinny_max_k(m);
+  const auto ev = timing_pair(c, a.stream);
+  a.ev_main[0] = ev.first;
+  a.ev_main[1] = ev.second;
   hipError_t e = skinny               ? launch_gemv(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
                                       : launch_gemm(a, c->cu_count);
+  timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return RQ_OK;
 }

@@ -10,7 +10,8 @@
 // multiplies the f32 partial (one FMA per output per block).
 //
 // f32 activations are split into bf16 hi + lo (x = hi + lo + O(2^-17 |x|)) and
-// take two MFMAs per tile; bf16 activations take one.
+// take two MFMAs per tile. This is the f32-activation path; bf16 activations
+// take gemm_bf16_kernel.
 //
 // Tiling: 256 threads = 4 waves (2 x 2), block tile 128 (m) x 128 (o), each wave
 // 64 x 64 = 4 x 4 MFMA tiles. Weights are the B operand so each lane's four
@@ -191,18 +192,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ q
     }
 }
 
+// f32 activations only: bf16 activations take gemm_bf16_kernel (gemm_bf16.hip).
 template <int FMT, typename ST>
 static hipError_t launch_x(const MatmulArgs& a) {
+  if (a.x_dtype != RQ_F32) return hipErrorInvalidValue;
   const int tiles_m = (int)((a.m + GBM - 1) / GBM), tiles_n = (int)((a.n + GBN - 1) / GBN);
   dim3 grid((unsigned)(tiles_m * tiles_n));
-  if (a.x_dtype == RQ_F32)
-    hipLaunchKernelGGL((gemm_kernel<FMT, ST, RQ_F32>), grid, dim3(256), 0, a.stream, a.q,
-                       static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, a.y_dtype,
-                       tiles_m);
-  else
-    hipLaunchKernelGGL((gemm_kernel<FMT, ST, RQ_BF16>), grid, dim3(256), 0, a.stream, a.q,
-                       static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, a.y_dtype,
-                       tiles_m);
+  hipExtLaunchKernelGGL((gemm_kernel<FMT, ST, RQ_F32>), grid, dim3(256), 0, a.stream, a.ev_main[0], a.ev_main[1],
+                        0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n,
+                        a.y_dtype, tiles_m);
   return hipGetLastError();
 }
 

@@ -298,9 +298,10 @@ static hipError_t launch_t(const MatmulArgs& a) {
   const int tiles_m = (int)((a.m + BM - 1) / BM), tiles_n = (int)((a.n + BN - 1) / BN);
   if (hipError_t e = launch_pack_x(a)) return e;
   dim3 grid((unsigned)(tiles_m * tiles_n));
-  hipLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, MT, NTW>), grid, dim3(256), 0, a.stream, a.q,
-                     static_cast<const ST*>(a.scales), static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m,
-                     (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, tiles_m);
+  hipExtLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, MT, NTW>), grid, dim3(256), 0, a.stream, a.ev_main[0],
+                        a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype, tiles_m);
   return hipGetLastError();
 }
 

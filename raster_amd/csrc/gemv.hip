@@ -37,6 +37,7 @@
 // streams its share of a group's windows, 4 windows per batch with the next
 // batch's loads in flight; the waves' partial sums meet in LDS.
 #include <algorithm>
+#include <atomic>
 
 #include "rq_internal.h"
 
@@ -378,17 +379,22 @@ static hipError_t launch_t(const MatmulArgs& a, int cu_count) {
   // 160 KB; 16 waves per CU at this kernel's register use)
   const int per_cu = std::max(1, std::min(163840 / L.bytes, 16 / WAVES));
   const int grid = std::min(ngroups, per_cu * cu_count);
-  static bool attr = false;  // dynamic LDS above 64 KB must be allowed once per kernel
-  if (!attr) {
+  // dynamic LDS above 64 KB must be allowed once per kernel and device (bit d
+  // of `attr_set`; setting it twice from racing threads is harmless)
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return e;
+  const uint64_t bit = uint64_t(1) << (dev & 63);
+  if (!(attr_set.load(std::memory_order_acquire) & bit)) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<FMT, ST, XT, MT, WAVES, NB>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
     if (e != hipSuccess) return e;
-    attr = true;
+    attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((skinny_kernel<FMT, ST, XT, MT, WAVES, NB>), dim3((unsigned)grid), dim3(64 * WAVES),
-                     (unsigned)L.bytes, a.stream,
-                     a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
-                     a.y_dtype);
+  hipExtLaunchKernelGGL((skinny_kernel<FMT, ST, XT, MT, WAVES, NB>), dim3((unsigned)grid), dim3(64 * WAVES),
+                        (unsigned)L.bytes, a.stream, a.ev_main[0], a.ev_main[1], 0, a.q,
+                        static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype);
   return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // gfx950 (CDNA4) only: wave64, MFMA bf16/i8, 160 KB LDS per CU.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -73,6 +74,9 @@ struct MatmulArgs {
   int64_t npad;     // n padded to a multiple of 16 (rows present in the chunked layout)
   hipStream_t stream;
   void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
+  // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
+  // and these events take that dispatch's own start and end timestamps
+  hipEvent_t ev_main[2] = {nullptr, nullptr};
 };
 
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).

@@ -51,6 +51,16 @@ class Context:
     def sync(self, stream=None) -> None:
         call("rq_sync", self.handle, _stream_ptr(stream))
 
+    def set_kernel_timing(self, enable: bool) -> None:
+        """Capture the dispatch timestamps of the main kernel of every matmul call."""
+        call("rq_ctx_set_kernel_timing", self.handle, 1 if enable else 0)
+
+    def kernel_time(self) -> tuple[float, int]:
+        """(summed main-kernel milliseconds, launches) since the last read."""
+        ms, n = C.c_double(), C.c_int64()
+        call("rq_ctx_kernel_time", self.handle, C.byref(ms), C.byref(n))
+        return ms.value, n.value
+
     def close(self) -> None:
         if self.handle:
             call("rq_ctx_destroy", self.handle)
@@ -120,7 +130,7 @@ class QWeight:
 
     @classmethod
     def q8_packed(cls, wp, ws, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
-        """From quantize-one-q8's int32-packed words (raster/quant/pack.clj:210-236)."""
+        """From quantize-one-q8's int32-packed words (raster/quant/pack.clj:55-81)."""
         ctx = ctx or context()
         wp = np.ascontiguousarray(wp, np.int32)
         ws = np.ascontiguousarray(ws, np.float32)

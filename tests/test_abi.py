@@ -46,6 +46,9 @@ def test_invalid_handles_are_reported_not_dereferenced():
     assert L.rq_dequant(None, None, None, None) == _lib.RQ_ERR_HANDLE
     info = C.c_int()
     assert L.rq_weight_info(bogus, C.byref(info), None, None, None, None) == _lib.RQ_ERR_HANDLE
+    assert L.rq_ctx_set_kernel_timing(bogus, 1) == _lib.RQ_ERR_HANDLE
+    ms, n = C.c_double(), C.c_int64()
+    assert L.rq_ctx_kernel_time(bogus, C.byref(ms), C.byref(n)) == _lib.RQ_ERR_HANDLE
 
 
 def test_ctx_create_null_out():

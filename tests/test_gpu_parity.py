@@ -462,3 +462,30 @@ def test_error_statuses_on_gpu(torch, ctx):
     assert L.rq_buf_alloc(ctx.handle, 1024, C.byref(buf)) == _lib.RQ_OK
     assert L.rq_buf_free(ctx.handle, buf) == _lib.RQ_OK
     assert L.rq_buf_free(ctx.handle, buf) == _lib.RQ_ERR_HANDLE
+
+
+def test_kernel_timing_counts_main_kernels(torch, ctx):
+    import raster_amd
+
+    codes, scales = wl.q8_weights(256, 1024, seed=3)
+    w = raster_amd.QWeight.q8(codes, scales, 256, 1024, ctx)
+    x1 = torch.randn((1, 1024), device="cuda")
+    x64 = torch.randn((64, 1024), device="cuda").to(torch.bfloat16)
+    ctx.kernel_time()
+    w.matmul(x1)  # timing off: not counted
+    torch.cuda.synchronize()
+    assert ctx.kernel_time() == (0.0, 0)
+    ctx.set_kernel_timing(True)
+    try:
+        for _ in range(3):
+            w.matmul(x1)  # decode kernel
+        w.matmul(x64, out_dtype=torch.bfloat16)  # pack + GEMM: one timed kernel
+        ms, n = ctx.kernel_time()
+        assert n == 4 and 0.0 < ms < 1000.0
+        assert ctx.kernel_time() == (0.0, 0)  # read clears
+    finally:
+        ctx.set_kernel_timing(False)
+    w.matmul(x1)
+    torch.cuda.synchronize()
+    assert ctx.kernel_time() == (0.0, 0)
+    w.destroy()

@@ -255,7 +255,7 @@ def test_q4_composable_equals_independent_int_dot(orc):
 
 @pytest.mark.parametrize("out,in_", [(16, 64), (1024, 640), (8, 32), (24, 128)])
 def test_x8_tile_matches_single_column(orc, out, in_):
-    # test/raster/quant/tile_test.clj:198-215 (exact int32 dots)
+    # test/raster/quant/tile_test.clj:13-30 (exact int32 dots)
     half, nb = in_ // 2, in_ // 32
     wq = orc.jfill_bytes(out + in_, out * in_ // 2).view(np.uint8)
     ws = np.ones(out * nb, np.float32)
@@ -301,7 +301,7 @@ def test_x8_vs_composable(orc, in_, out):
 
 # ---------------------------------------------------------------- signed q8_0 prefill
 def test_quantize_one_q8_roundtrip(orc):
-    # test/raster/quant/pack_test.clj:136-156
+    # test/raster/quant/pack_test.clj:20-40
     out, in_ = 4, 64
     nb = in_ // 32
     W = orc.jfill_uniform_centered(7, out * in_)
