@@ -137,10 +137,8 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * m == 0 is a no-op.
  *
  * Numerics (all accumulation in f32):
- *  - m <= 16 (and in small enough for the activation slice to fit in LDS:
- *    in <= 17216 at m <= 4, 8704 at m <= 8, 4288 at m <= 16): int8 MFMA on the
- *    raw weight codes. Each 32-block of each activation row is held as a 16-bit
- *    block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
+ *  - m <= 16: int8 MFMA on the raw weight codes. Each 32-block of each
+ *    activation row is held as a 16-bit block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
  *    exponent, |X| < 2^15, so the per-element error is <= 2^(e-16) (below
  *    1.6e-5 relative to the block maximum). An inf or NaN activation makes its
  *    row's outputs NaN.
@@ -148,15 +146,19 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
  *    split into two bf16 terms (about 16 mantissa bits).
- *  - m <= 16 with a larger in: the f32-activation GEMM path above.
  *
- * bf16 x with m > 16 uses a per-stream scratch buffer (the packed activation
- * tile, ceil(m/16)*16*in*2 bytes) that the context allocates on first use and
- * grows on demand; it is freed by rq_ctx_destroy. Calls on one stream are
- * ordered, calls on different streams do not share scratch. Under HIP graph
- * capture no allocation can happen: run the same (or a larger) shape once on
- * the capturing stream before capturing, otherwise the call fails with
- * RQ_ERR_HIP and a message saying so. */
+ * Scratch (per stream, allocated on first use, grown on demand, freed by
+ * rq_ctx_destroy; calls on one stream are ordered, calls on different streams
+ * do not share it):
+ *  - bf16 x with m > 16: the packed activation tile, ceil(m/16)*16*in*2 bytes;
+ *  - m <= 16 with activations too long for one workgroup's LDS (in above
+ *    17472 at m <= 4, 8704 at m <= 8, 4288 at m <= 16): per-group counters and
+ *    the K-slices' partial sums. The counters are zeroed when allocated and every
+ *    call leaves them at zero.
+ * Under HIP graph capture nothing can be allocated: run the same (or a
+ * larger) shape once on the capturing stream before capturing, otherwise the
+ * call fails with RQ_ERR_SHAPE and a message saying so.
+ */
 int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                void* stream);
 

@@ -24,10 +24,18 @@ struct Ctx {
   int clock_khz;
   std::unordered_set<Weight*> weights;
   std::unordered_set<void*> buffers;
-  // Per-stream scratch for the packed activations of the bf16 GEMM; grow-only,
-  // freed with the context. Calls on one stream run in order, so a stream's
-  // buffer is never used by two kernels at once.
-  std::unordered_map<hipStream_t, std::pair<void*, size_t>> scratch;
+  // Per-stream scratch, grow-only, freed with the context: the bf16 GEMM's
+  // packed activations, and the decode kernel's K-split counters (kept at zero
+  // between calls) and partial sums. Calls on one stream run in order, so a
+  // stream's buffers are never used by two kernels at once.
+  struct StreamScratch {
+    void* pack = nullptr;
+    size_t pack_bytes = 0;
+    void* red = nullptr;   // int counters[red_counters] (256-byte aligned), then partials
+    size_t red_bytes = 0;
+    int red_counters = 0;
+  };
+  std::unordered_map<hipStream_t, StreamScratch> scratch;
   // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
   // end timestamps of each rq_qmatmul's main kernel, waiting to be read, and a
   // pool of spares.
@@ -151,32 +159,68 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   return RQ_OK;
 }
 
-// Scratch of at least `bytes` for `stream` (grow-only, one buffer per stream).
-static int stream_scratch(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
+static bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+static const char* kCaptureScratch =
+    "this stream is being captured and its scratch is too small for this call: run the same (or a larger) "
+    "call on the stream once before capturing";
+
+// Replaces *buf (sized *have) by a fresh allocation of at least `bytes`
+// (+25%). The old buffer may still be read by kernels queued on the stream.
+static int regrow(hipStream_t stream, size_t bytes, void** buf, size_t* have) {
+  if (*buf) {
+    const hipError_t se = hipStreamSynchronize(stream);
+    if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+  }
+  const size_t want = bytes + bytes / 4;
+  void* p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(want) + " bytes of scratch failed");
+  }
+  *buf = p;
+  *have = want;
+  return RQ_OK;
+}
+
+// The bf16 GEMM's packed-activation buffer for `stream`, at least `bytes`.
+static int stream_pack(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto& e = c->scratch[stream];
-  if (e.second < bytes) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-      return fail(RQ_ERR_SHAPE,
-                  "this stream is being captured and has no scratch for m=" + std::to_string(bytes) +
-                      " bytes yet: run the same (or a larger) call on the stream once before capturing");
-    if (e.first) {
-      // the old buffer may still be read by kernels queued on this stream
-      const hipError_t se = hipStreamSynchronize(stream);
-      if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
-      (void)hipFree(e.first);
-      e = {nullptr, 0};
-    }
-    const size_t want = bytes + bytes / 4;
-    void* p = nullptr;
-    if (hipMalloc(&p, want) != hipSuccess || !p) {
-      (void)hipGetLastError();
-      return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(want) + " bytes of scratch failed");
-    }
-    e = {p, want};
+  if (e.pack_bytes < bytes) {
+    if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
+    if (int s = regrow(stream, bytes, &e.pack, &e.pack_bytes)) return s;
   }
-  *out = e.first;
+  *out = e.pack;
+  return RQ_OK;
+}
+
+// The decode kernel's K-split buffers for `stream`: `counters` zeroed ints
+// and `part_bytes` of partial sums. A new buffer's counters are zeroed on the
+// stream before first use; every call leaves them at zero again.
+static int stream_split(Ctx* c, hipStream_t stream, int counters, size_t part_bytes, int** cnt, float** part) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto& e = c->scratch[stream];
+  const size_t have_c = align256((size_t)e.red_counters * 4);
+  if (e.red_counters < counters || e.red_bytes < have_c + part_bytes) {
+    if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
+    const int nc = std::max(counters, e.red_counters);
+    const size_t ncb = align256((size_t)nc * 4);
+    if (int s = regrow(stream, ncb + std::max(part_bytes, e.red_bytes > have_c ? e.red_bytes - have_c : 0),
+                       &e.red, &e.red_bytes))
+      return s;
+    e.red_counters = nc;
+    const hipError_t me = hipMemsetAsync(e.red, 0, ncb, stream);
+    if (me != hipSuccess) return hip_fail(me, "zeroing the decode counters");
+  }
+  *cnt = static_cast<int*>(e.red);
+  *part = reinterpret_cast<float*>(static_cast<uint8_t*>(e.red) + align256((size_t)e.red_counters * 4));
   return RQ_OK;
 }
 
@@ -288,7 +332,10 @@ int rq_ctx_destroy(rq_ctx h) {
   (void)hipSetDevice(c->device);
   for (Weight* w : c->weights) free_weight_locked(w);
   for (void* b : c->buffers) (void)hipFree(b);
-  for (auto& kv : c->scratch) (void)hipFree(kv.second.first);
+  for (auto& kv : c->scratch) {
+    (void)hipFree(kv.second.pack);
+    (void)hipFree(kv.second.red);
+  }
   timing_release(c);
   c->magic = 0;
   g_ctxs.erase(c);
@@ -559,16 +606,20 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   a.npad = w.npad;
   a.stream = (hipStream_t)stream;
   a.scratch = nullptr;
-  if (!(m <= 16 && w.in <= skinny_max_k(m)) && x_dtype == RQ_BF16) {
+  a.part = nullptr;
+  a.cnt = nullptr;
+  const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
+  if (plan.ok && plan.ksplit > 1) {
+    if (int s = stream_split(c, a.stream, plan.counters, plan.part_bytes, &a.cnt, &a.part)) return s;
+  } else if (!plan.ok && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
-    if (int s = stream_scratch(c, a.stream, bytes, &a.scratch)) return s;
+    if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
   }
-  const bool skinny = m <= 16 && w.in <= skinny_max_k(m);
   const auto ev = timing_pair(c, a.stream);
   a.ev_main[0] = ev.first;
   a.ev_main[1] = ev.second;
-  hipError_t e = skinny               ? launch_gemv(a, c->cu_count)
+  hipError_t e = plan.ok              ? launch_gemv(a, plan)
                  : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);

@@ -32,10 +32,13 @@
 // A block of x holding Inf or NaN gets a NaN factor, so every output of that
 // activation row is NaN (Raster's f32 loop gives +-Inf or NaN there).
 //
-// Mapping: a workgroup (8 or 16 waves) decomposes x into LDS once, then
-// takes 16-row groups of the weight in turn (stride over the grid); each wave
+// Mapping: a workgroup (8 waves) decomposes x into LDS once, then takes
+// 16-row groups of the weight in turn (stride over the grid); each wave
 // streams its share of a group's windows, 4 windows per batch with the next
-// batch's loads in flight; the waves' partial sums meet in LDS.
+// batch's loads in flight; the waves' partial sums meet in LDS. When the
+// activations of all of K do not fit in LDS, K is cut into slices taken by
+// different workgroups, and the last one to finish a group adds the slices'
+// partial sums.
 #include <algorithm>
 #include <atomic>
 
@@ -50,19 +53,23 @@ namespace {
 struct SkinnyLds {
   int kp;       // k padded to whole windows
   int nbp;      // blocks, padded (= kp / 32)
-  int lev;      // int8 lev[mt][2][kp]
-  int xsf;      // f32 xsf[mt + 1][nbp]: 2^(e-15), NaN for non-finite blocks; row mt zero
-  int xs;       // i32 xs[mt + 1][nbp]: sum of X over the block (Q4 zero-point); row mt zero
+  int lstr;     // bytes per lev row: kp + 32, so the rows of one MFMA operand read fall in different banks
+  int xstr;     // elements per xsf / xs row: nbp + 2, for the same reason
+  int lev;      // int8 lev[mt][2][lstr]
+  int xsf;      // f32 xsf[mt + 1][xstr]: 2^(e-15), NaN for non-finite blocks; row mt zero
+  int xs;       // i32 xs[mt + 1][xstr]: sum of X over the block (Q4 zero-point); row mt zero
   int zero;     // 16 zero bytes
   int red;      // f32 red[waves][mg][64]
   int bytes;
   __host__ __device__ SkinnyLds(int mt, int k, int waves) {
     kp = (k + 63) / 64 * 64;
     nbp = kp / 32;
+    lstr = kp + 32;
+    xstr = nbp + 2;
     lev = 0;
-    xsf = mt * 2 * kp;
-    xs = xsf + (mt + 1) * nbp * 4;
-    zero = xs + (mt + 1) * nbp * 4;
+    xsf = mt * 2 * lstr;
+    xs = xsf + (mt + 1) * xstr * 4;
+    zero = xs + (mt + 1) * xstr * 4;
     red = zero + 16;
     bytes = red + waves * (mt / 4) * 64 * 4;
   }
@@ -87,28 +94,46 @@ __device__ __forceinline__ void load_x4(const void* x, int64_t off, bool ok, flo
   }
 }
 
+// Reductions over the 8 lanes that share a block (lanes 8j..8j+7): swap
+// neighbours, then pairs, then the two quads of the row half (DPP moves, no
+// LDS traffic).
+__device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_half_mirror(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
+  return fmaxf(v, __int_as_float(dpp_half_mirror(__float_as_int(v))));
+}
+__device__ __forceinline__ int or8(int v) {
+  v |= dpp_xor1(v);
+  v |= dpp_xor2(v);
+  return v | dpp_half_mirror(v);
+}
+__device__ __forceinline__ int sum8(int v) {
+  v += dpp_xor1(v);
+  v += dpp_xor2(v);
+  return v + dpp_half_mirror(v);
+}
+
 // Decomposition of one item: 4 activations (row mm, elements k..k+3 of block
 // b) of the 8 lanes sharing a block. Writes both int8 levels to LDS and, from
-// the block's first lane, the block factor and level sum.
-__device__ __forceinline__ void decompose_item(const float (&v)[4], int mm, int b, int part, int k, int kp, int nbp,
-                                               int8_t* __restrict__ lev, float* __restrict__ xsf,
+// the block's first lane, the block factor and level sum. All 8 lanes of a
+// block run it together (the reductions cross lanes); `valid` (the same for
+// the 8 lanes) only gates the LDS writes.
+__device__ __forceinline__ void decompose_item(const float (&v)[4], bool valid, int mm, int b, int part, int k, int lstr,
+                                               int xstr, int8_t* __restrict__ lev, float* __restrict__ xsf,
                                                int* __restrict__ xs) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   // fmaxf drops NaN operands, so non-finite values are flagged separately
   int bad = !(fabsf(v[0]) <= 3.402823466e38f && fabsf(v[1]) <= 3.402823466e38f && fabsf(v[2]) <= 3.402823466e38f &&
               fabsf(v[3]) <= 3.402823466e38f);
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-  bad |= __shfl_xor(bad, 1, 64);
-  bad |= __shfl_xor(bad, 2, 64);
-  bad |= __shfl_xor(bad, 4, 64);
-  int e = 0;
+  amax = max8(amax);
+  bad = or8(bad);
   const bool finite = !bad;
-  if (finite && amax > 0.0f) {
-    (void)frexpf(amax, &e);
-    if (ldexpf(amax, 15 - e) > 32639.0f) e += 1;  // keeps |X| <= 32639: both levels fit int8
-  }
+  int e = 0;
+  (void)frexpf(amax, &e);  // 0 for amax == 0
+  e = ldexpf(amax, 15 - e) > 32639.0f ? e + 1 : e;  // keeps |X| <= 32639: both levels fit int8
   uint32_t l0 = 0u, l1 = 0u;
   int sum = 0;
 #pragma unroll
@@ -119,14 +144,14 @@ __device__ __forceinline__ void decompose_item(const float (&v)[4], int mm, int 
     l1 |= (uint32_t)(c & 0xFF) << (8 * i);
     sum += X;
   }
-  *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 0) * kp + k) = l0;
-  *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 1) * kp + k) = l1;
-  sum += __shfl_xor(sum, 1, 64);
-  sum += __shfl_xor(sum, 2, 64);
-  sum += __shfl_xor(sum, 4, 64);
-  if (part == 0) {
-    xsf[mm * nbp + b] = finite ? ldexpf(1.0f, e - 15) : __builtin_nanf("");
-    xs[mm * nbp + b] = sum;
+  sum = sum8(sum);
+  if (valid) {
+    *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 0) * lstr + k) = l0;
+    *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 1) * lstr + k) = l1;
+    if (part == 0) {
+      xsf[mm * xstr + b] = finite ? ldexpf(1.0f, e - 15) : __builtin_nanf("");
+      xs[mm * xstr + b] = sum;
+    }
   }
 }
 
@@ -135,19 +160,26 @@ __device__ __forceinline__ void decompose_item(const float (&v)[4], int mm, int 
 template <int FMT, typename ST, int XT, int MT, int WAVES, int NB>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                            const void* __restrict__ x, void* __restrict__ y, int M,
-                                                           int K, int N, int npad, int y_dtype) {
+                                                           int K, int N, int npad, int y_dtype, int ksplit,
+                                                           float* __restrict__ part, int* __restrict__ cnt) {
   constexpr int MG = MT / 4;                 // MFMAs per window (4 activation rows each)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const SkinnyLds L(MT, K, WAVES);
+  const int nb = K / 32, nw = (K + 63) / 64;
+  const int ngroups = npad / 16;
+  // ---- this workgroup's K-slice: windows [s_beg, s_end), fixed for all its
+  // groups. LDS holds the activations of the slice only (slice-relative).
+  const int s = (int)blockIdx.x % ksplit;
+  const int sw = (nw + ksplit - 1) / ksplit;
+  const int s_beg = min(nw, s * sw), s_end = min(nw, s_beg + sw);
+  const SkinnyLds L(MT, 64 * sw, WAVES);
   int8_t* lev = reinterpret_cast<int8_t*>(smem + L.lev);
   float* xsf = reinterpret_cast<float*>(smem + L.xsf);
   int* xs = reinterpret_cast<int*>(smem + L.xs);
   float* red = reinterpret_cast<float*>(smem + L.red);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers and branches
   const int r = lane & 15, g4 = lane >> 4;
-  const int nb = K / 32, nw = L.kp / 64;
-  const int ngroups = npad / 16;
 
   // ---- per-lane A-fragment addressing. Lane (r, g4) supplies k-slots of
   // window block g4 >> 1; variant r = (row 4 mg + r/4, level r & 1, block
@@ -159,17 +191,17 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     const int mm = 4 * mg + (r >> 2);
     const bool match = sel == (g4 >> 1) && mm < M;
     const int kin = FMT == RQ_Q8_0 ? 16 * g4 : 32 * (g4 >> 1) + 8 * (g4 & 1);
-    aoff[mg] = match ? (mm * 2 + lvl) * L.kp + kin : -1;
+    aoff[mg] = match ? (mm * 2 + lvl) * L.lstr + kin : -1;
   }
   // this lane's activation row per MFMA (for xsf / xs), quad q = g4; rows
   // past M read the zero row
   int xrow[MG];
 #pragma unroll
-  for (int mg = 0; mg < MG; mg++) xrow[mg] = (4 * mg + g4 < M ? 4 * mg + g4 : MT) * L.nbp;
+  for (int mg = 0; mg < MG; mg++) xrow[mg] = (4 * mg + g4 < M ? 4 * mg + g4 : MT) * L.xstr;
 
-  // ---- wave's window range of each group
-  const int per = (nw + WAVES - 1) / WAVES;
-  const int wbeg = wave * per, wend = min(nw, wbeg + per);
+  // ---- wave's window range inside the slice (absolute window numbers)
+  const int per = (sw + WAVES - 1) / WAVES;
+  const int wbeg = min(s_end, s_beg + wave * per), wend = min(s_end, wbeg + per);
 
   // weight bytes per 16-row chunk, and this lane's offset inside a window
   constexpr int CB = FMT == RQ_Q8_0 ? 32 : 16;
@@ -182,7 +214,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   u32x4 wq[2][NB];
   float s0[2][NB], s1[2][NB];
   // weight window w of group g: this lane's 16 (Q8) / 8 (Q4) code bytes and
-  // the row's two block scales; all loads unconditional at clamped addresses
+  // the row's two block scales. All loads are unconditional at clamped
+  // addresses and nothing here uses the loaded values: any condition or
+  // select on them would make the compiler wait for the loads right here and
+  // lose the overlap with the work that follows.
   auto load_batch = [&](int slot, int wb, int g) {
     const uint8_t* qg = q + (int64_t)g * nb * CB * 16;  // the group's chunks
     const ST* sg = sc + (int64_t)g * nb * 16;           // and scales
@@ -197,48 +232,65 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
         wq[slot][i] = u32x4{t[0], t[1], 0u, 0u};
       }
       s0[slot][i] = load_scale<ST>(sg, 32 * w + r);
-      const float t1 = load_scale<ST>(sg, 16 * min(2 * w + 1, nb - 1) + r);
-      s1[slot][i] = 2 * w + 1 < nb ? t1 : 0.0f;
+      // a missing second block (odd block count) rereads the first block's
+      // scale; compute_batch zeroes it
+      s1[slot][i] = load_scale<ST>(sg, 16 * min(2 * w + 1, nb - 1) + r);
     }
   };
 
   // ---- activation decomposition into LDS. A wave only ever reads the
-  // activations of its own k-slice (windows wbeg..wend of every group), so
-  // each wave decomposes just that slice into its own part of the LDS
-  // arrays: no workgroup barrier. The first XJ items' activation loads go
-  // out before the first weight batch, so the decomposition waits only for
-  // them (loads complete in issue order).
-  const int nblk_w = 2 * max(wend - wbeg, 0);  // blocks of this wave's slice
-  const int witems = M * nblk_w * 8;            // 4-element items of the slice
-  constexpr int XJ = 4;
+  // activations of its own windows (wbeg..wend of every group), so each wave
+  // decomposes just those into its own part of the LDS arrays: no workgroup
+  // barrier. Items are 4 consecutive activations; a lane takes items lane,
+  // lane + 64, ... in chunks of XJ whose loads all go out before any is used.
+  // The first chunk's loads precede the first weight batch, so decomposing it
+  // waits only for them (loads complete in issue order). Lanes past the
+  // wave's last item reread it (same row) and do not write.
+  const int nblk_w = 2 * (wend - wbeg);          // blocks of this wave's windows
+  const int rb0 = 2 * (wbeg - s_beg);            // their first block, slice-relative
+  const int witems = M * nblk_w * 8;             // 4-element items
+  constexpr int XJ = 8;
   float xv[XJ][4];
+  // item slots j of a chunk that hold any item: a wave-uniform test, so the
+  // loads and decompositions of empty slots are skipped by scalar branches
+  auto load_chunk = [&](int base) {
 #pragma unroll
-  for (int j = 0; j < XJ; j++) {
-    const int it = min(lane + 64 * j, max(witems - 1, 0));
-    const int mm = it / max(nblk_w * 8, 1), k = 32 * (2 * wbeg + (it >> 3) % max(nblk_w, 1)) + 4 * (it & 7);
-    load_x4<XT>(x, (int64_t)mm * K + min(k, K - 4), true, xv[j]);
-    if (k >= K) xv[j][0] = xv[j][1] = xv[j][2] = xv[j][3] = 0.0f;
-  }
-  if (blockIdx.x < ngroups) load_batch(0, wbeg, blockIdx.x);
+    for (int j = 0; j < XJ; j++) {
+      if (base + 64 * j >= witems) break;
+      const int it = min(base + lane + 64 * j, witems - 1);
+      const int mm = it / (nblk_w * 8), rb = rb0 + (it >> 3) % nblk_w;
+      // columns past K (the missing half of a last window) reread in-row data
+      const int k = min(32 * (2 * s_beg + rb) + 4 * (it & 7), K - 4);
+      load_x4<XT>(x, (int64_t)mm * K + k, true, xv[j]);
+    }
+  };
+  auto decompose_chunk = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < XJ; j++) {
+      if (base + 64 * j >= witems) break;
+      const int it0 = base + lane + 64 * j;
+      const int it = min(it0, witems - 1);
+      const int mm = it / (nblk_w * 8), rb = rb0 + (it >> 3) % nblk_w, pt = it & 7;
+      decompose_item(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
+    }
+  };
+  const int gcols = (int)gridDim.x / ksplit;  // workgroups per slice
+  const int gfirst = (int)blockIdx.x / ksplit;
+  load_chunk(0);
+  // keep the scheduler from hoisting the weight loads above the activation
+  // loads: the decomposition below waits for the activations only
+  __builtin_amdgcn_sched_barrier(0);
+  load_batch(0, wbeg, min(gfirst, ngroups - 1));
+  __builtin_amdgcn_sched_barrier(0);
   if (lane < 4) reinterpret_cast<uint32_t*>(smem + L.zero)[lane] = 0u;
   if (lane < nblk_w) {
-    xsf[MT * L.nbp + 2 * wbeg + lane] = 0.0f;
-    xs[MT * L.nbp + 2 * wbeg + lane] = 0;
+    xsf[MT * L.xstr + rb0 + lane] = 0.0f;
+    xs[MT * L.xstr + rb0 + lane] = 0;
   }
-#pragma unroll
-  for (int j = 0; j < XJ; j++) {
-    const int it = lane + 64 * j;
-    if (it < witems) {
-      const int mm = it / (nblk_w * 8), b = 2 * wbeg + (it >> 3) % nblk_w, part = it & 7;
-      decompose_item(xv[j], mm, b, part, 32 * b + 4 * part, L.kp, L.nbp, lev, xsf, xs);
-    }
-  }
-  for (int it = lane + 64 * XJ; it < witems; it += 64) {
-    const int mm = it / (nblk_w * 8), b = 2 * wbeg + (it >> 3) % nblk_w, part = it & 7;
-    const int k = 32 * b + 4 * part;
-    float v[4];
-    load_x4<XT>(x, (int64_t)mm * K + k, k < K, v);
-    decompose_item(v, mm, b, part, k, L.kp, L.nbp, lev, xsf, xs);
+  decompose_chunk(0);
+  for (int base = 64 * XJ; base < witems; base += 64 * XJ) {
+    load_chunk(base);
+    decompose_chunk(base);
   }
   // the wave reads back what its own lanes wrote
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -258,10 +310,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     for (int i = 0; i < NB; i++) {
       const int w = wb + i;
       const bool live = w < wend;  // wave-uniform
-      const int wblk = 2 * min(w, nw - 1);
+      const int rw = max(0, min(w, s_end - 1) - s_beg);  // slice-relative window
 #pragma unroll
       for (int mg = 0; mg < MG; mg++) {
-        const int ao = live && aoff[mg] >= 0 ? aoff[mg] + 64 * w : L.zero - L.lev;
+        const int ao = live && aoff[mg] >= 0 ? aoff[mg] + 64 * rw : L.zero - L.lev;
         if (FMT == RQ_Q8_0) {
           af[i][mg] = *reinterpret_cast<const i32x4*>(lev + ao);
         } else {
@@ -271,13 +323,14 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
           const u32x2 h1 = *reinterpret_cast<const u32x2*>(lev + ao2);
           af[i][mg] = i32x4{(int)h0[0], (int)h0[1], (int)h1[0], (int)h1[1]};
         }
-        const f32x2 fv = *reinterpret_cast<const f32x2*>(xsf + xrow[mg] + wblk);
+        const f32x2 fv = *reinterpret_cast<const f32x2*>(xsf + xrow[mg] + 2 * rw);
         f0[i][mg] = live ? fv[0] : 0.0f;
-        f1[i][mg] = live ? fv[1] : 0.0f;
+        // a window's second block may not exist (odd block count)
+        f1[i][mg] = live && 2 * w + 1 < nb ? fv[1] : 0.0f;
         if (FMT == RQ_Q4_0) {
-          const i32x2 xv = *reinterpret_cast<const i32x2*>(xs + xrow[mg] + wblk);
-          x0[i][mg] = xv[0];
-          x1[i][mg] = xv[1];
+          const i32x2 xv2 = *reinterpret_cast<const i32x2*>(xs + xrow[mg] + 2 * rw);
+          x0[i][mg] = xv2[0];
+          x1[i][mg] = xv2[1];
         }
       }
     }
@@ -314,17 +367,21 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // t = i * nbg + j. The next task's loads (possibly the next group's) are in
   // flight while the current task computes and a finished group's partial
   // sums are combined.
-  const int nbg = (per + NB - 1) / NB;  // batches per group
-  const int rounds = (int)blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int nbg = max(1, (per + NB - 1) / NB);  // batches per group
+  const int rounds = gfirst < ngroups ? (ngroups - 1 - gfirst) / gcols + 1 : 0;
   const int ntask = rounds * nbg;
   auto task_load = [&](int slot, int t) {
-    const int g = (int)blockIdx.x + (t / nbg) * (int)gridDim.x;
+    const int g = gfirst + (t / nbg) * gcols;
     load_batch(slot, wbeg + (t % nbg) * NB, min(g, ngroups - 1));
   };
-  // combine the waves' partial sums of the group in wave order; lane (r, g4)
-  // of wave 0 writes y[4 mg + g4][16 g + r]
+  // Combine the waves' partial sums of the group in wave order; lane (r, g4)
+  // of wave 0 owns y[4 mg + g4][16 g + r]. With one slice it stores y. With
+  // several, it stores the slice's partial sums, and the workgroup that
+  // finishes the group's last slice adds all slices' partials in slice order
+  // (a deterministic sum) and stores y. The group's counter is back at zero
+  // when the kernel ends.
   auto finish_group = [&](int t) {
-    const int g = (int)blockIdx.x + (t / nbg) * (int)gridDim.x;
+    const int g = gfirst + (t / nbg) * gcols;
 #pragma unroll
     for (int mg = 0; mg < MG; mg++) {
       red[(wave * MG + mg) * 64 + lane] = acc[mg];
@@ -333,17 +390,43 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     __syncthreads();
     if (wave == 0) {
       const int o = 16 * g + r;
+      float v[MG];
 #pragma unroll
       for (int mg = 0; mg < MG; mg++) {
-        float v = 0.0f;
+        v[mg] = 0.0f;
 #pragma unroll
-        for (int wv = 0; wv < WAVES; wv++) v += red[(wv * MG + mg) * 64 + lane];
-        const int m = 4 * mg + g4;
-        if (m < M && o < N) {
-          if (y_dtype == RQ_F32)
-            static_cast<float*>(y)[(int64_t)m * N + o] = v;
-          else
-            static_cast<uint16_t*>(y)[(int64_t)m * N + o] = (uint16_t)f32_to_bf16_bits(v);
+        for (int wv = 0; wv < WAVES; wv++) v[mg] += red[(wv * MG + mg) * 64 + lane];
+      }
+      bool store = ksplit == 1;
+      if (!store) {
+#pragma unroll
+        for (int mg = 0; mg < MG; mg++) part[((int64_t)s * ngroups + g) * (MG * 64) + mg * 64 + lane] = v[mg];
+        __threadfence();  // release: the partials before the count
+        int old = 0;
+        if (lane == 0) old = atomicAdd(cnt + g, 1);
+        old = __shfl(old, 0, 64);
+        if (old == ksplit - 1) {
+          __threadfence();  // acquire: every slice's partials are visible
+#pragma unroll
+          for (int mg = 0; mg < MG; mg++) {
+            float sum = 0.0f;
+            for (int sl = 0; sl < ksplit; sl++) sum += part[((int64_t)sl * ngroups + g) * (MG * 64) + mg * 64 + lane];
+            v[mg] = sum;
+          }
+          if (lane == 0) __hip_atomic_store(cnt + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          store = true;
+        }
+      }
+      if (store) {
+#pragma unroll
+        for (int mg = 0; mg < MG; mg++) {
+          const int m = 4 * mg + g4;
+          if (m < M && o < N) {
+            if (y_dtype == RQ_F32)
+              static_cast<float*>(y)[(int64_t)m * N + o] = v[mg];
+            else
+              static_cast<uint16_t*>(y)[(int64_t)m * N + o] = (uint16_t)f32_to_bf16_bits(v[mg]);
+          }
         }
       }
     }
@@ -361,24 +444,48 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   }
 }
 
-// Waves per workgroup: a group's 64-element windows are split across the
-// waves, and short per-wave runs with many waves in flight stream small
-// weights fastest (the weight-load ramp dominates a few-microsecond call).
-template <int MT>
-struct SkinnyShape {
-  static constexpr int waves = MT == 4 ? 16 : 8;
-  static constexpr int nb = 4;  // windows per batch
-};
+constexpr int kBatch = 4;  // windows per batch
 
-template <int FMT, typename ST, int XT, int MT>
-static hipError_t launch_t(const MatmulArgs& a, int cu_count) {
-  constexpr int WAVES = SkinnyShape<MT>::waves, NB = SkinnyShape<MT>::nb;
-  const SkinnyLds L(MT, (int)a.k, WAVES);
-  const int ngroups = (int)(a.npad / 16);
-  // persistent grid: the workgroups that fit on the chip at once (LDS per CU
-  // 160 KB; 16 waves per CU at this kernel's register use)
-  const int per_cu = std::max(1, std::min(163840 / L.bytes, 16 / WAVES));
-  const int grid = std::min(ngroups, per_cu * cu_count);
+// Split and grid for the decode kernel.
+//  * waves per workgroup and workgroups per CU, measured with cold weights on
+//    the 4096 x 4096 Q8 and 14336 x 4096 Q4 shapes at m = 1..16: with more
+//    16-row groups than CUs, 16 waves (m <= 4); with at most one group per CU,
+//    8 waves for m <= 2 and 16 for m = 3, 4; 8 waves for m > 4, one workgroup per CU (their register use
+//    leaves room for no more, and a second workgroup would only repeat the
+//    activation decomposition).
+//  * A workgroup holds the activations of its K-range in LDS; when the whole
+//    K does not fit, each 16-row group is cut into ksplit K-slices handled by
+//    different workgroups, whose partial sums the last one to finish adds up.
+//    (Splitting only to create more workgroups does not pay: the
+//    cross-workgroup handoff costs more than it gains.)
+DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
+  DecodePlan p{};
+  if (m < 1 || m > 16) return p;
+  const int64_t nw = (k + 63) / 64, ngroups = npad / 16;
+  p.mt = m <= 4 ? 4 : m <= 8 ? 8 : 16;
+  p.waves = p.mt == 4 && (ngroups > cu_count || m > 2) ? 16 : 8;
+  const int per_cu_max = p.mt == 4 ? 16 / p.waves : 1;
+  int64_t ks = 1;
+  while (SkinnyLds(p.mt, (int)(64 * ((nw + ks - 1) / ks)), p.waves).bytes > 163840) {
+    if (ks >= nw) return p;
+    ks++;
+  }
+  const int lds = SkinnyLds(p.mt, (int)(64 * ((nw + ks - 1) / ks)), p.waves).bytes;
+  const int per_cu = std::max(1, std::min(163840 / lds, per_cu_max));
+  const int64_t gcols = std::min<int64_t>(ngroups, std::max<int64_t>(1, (int64_t)per_cu * cu_count / ks));
+  if (gcols * ks > INT32_MAX) return p;
+  p.ksplit = (int)ks;
+  p.grid = (int)(gcols * ks);
+  p.lds_bytes = lds;
+  p.part_bytes = ks > 1 ? (size_t)ks * (size_t)ngroups * (size_t)(p.mt * 16) * 4 : 0;
+  p.counters = ks > 1 ? (int)ngroups : 0;
+  p.ok = true;
+  return p;
+}
+
+template <int FMT, typename ST, int XT, int MT, int WAVES>
+static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
+  auto kernel = &skinny_kernel<FMT, ST, XT, MT, WAVES, kBatch>;
   // dynamic LDS above 64 KB must be allowed once per kernel and device (bit d
   // of `attr_set`; setting it twice from racing threads is harmless)
   static std::atomic<uint64_t> attr_set{0};
@@ -386,44 +493,34 @@ static hipError_t launch_t(const MatmulArgs& a, int cu_count) {
   if (hipError_t e = hipGetDevice(&dev)) return e;
   const uint64_t bit = uint64_t(1) << (dev & 63);
   if (!(attr_set.load(std::memory_order_acquire) & bit)) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&skinny_kernel<FMT, ST, XT, MT, WAVES, NB>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipExtLaunchKernelGGL((skinny_kernel<FMT, ST, XT, MT, WAVES, NB>), dim3((unsigned)grid), dim3(64 * WAVES),
-                        (unsigned)L.bytes, a.stream, a.ev_main[0], a.ev_main[1], 0, a.q,
-                        static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
-                        a.y_dtype);
+  hipExtLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(64 * WAVES), (unsigned)p.lds_bytes, a.stream,
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m,
+                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.cnt);
   return hipGetLastError();
 }
 
 template <int FMT, typename ST, int XT>
-static hipError_t launch_m(const MatmulArgs& a, int cu_count) {
-  if (a.m <= 4) return launch_t<FMT, ST, XT, 4>(a, cu_count);
-  if (a.m <= 8) return launch_t<FMT, ST, XT, 8>(a, cu_count);
-  return launch_t<FMT, ST, XT, 16>(a, cu_count);
+static hipError_t launch_m(const MatmulArgs& a, const DecodePlan& p) {
+  if (p.mt == 4) return p.waves == 16 ? launch_t<FMT, ST, XT, 4, 16>(a, p) : launch_t<FMT, ST, XT, 4, 8>(a, p);
+  if (p.mt == 8) return launch_t<FMT, ST, XT, 8, 8>(a, p);
+  return launch_t<FMT, ST, XT, 16, 8>(a, p);
 }
 
 template <int FMT, typename ST>
-static hipError_t launch_x(const MatmulArgs& a, int cu_count) {
-  return a.x_dtype == RQ_F32 ? launch_m<FMT, ST, RQ_F32>(a, cu_count) : launch_m<FMT, ST, RQ_BF16>(a, cu_count);
+static hipError_t launch_x(const MatmulArgs& a, const DecodePlan& p) {
+  return a.x_dtype == RQ_F32 ? launch_m<FMT, ST, RQ_F32>(a, p) : launch_m<FMT, ST, RQ_BF16>(a, p);
 }
 
-// Largest k the skinny kernel's LDS holds for m activation rows (rows are
-// processed in groups of 4, 8 or 16).
-int64_t skinny_max_k(int64_t m) {
-  const int mt = m <= 4 ? 4 : m <= 8 ? 8 : 16;
-  const int waves = mt == 4 ? SkinnyShape<4>::waves : SkinnyShape<8>::waves;
-  int64_t k = 64;
-  while (SkinnyLds(mt, (int)(k + 64), waves).bytes <= 163840) k += 64;
-  return k;
-}
-
-hipError_t launch_gemv(const MatmulArgs& a, int cu_count) {
-  if (a.format == RQ_Q8_0) return launch_x<RQ_Q8_0, float>(a, cu_count);
-  if (a.scale_dtype == RQ_F16) return launch_x<RQ_Q4_0, uint16_t>(a, cu_count);
-  return launch_x<RQ_Q4_0, float>(a, cu_count);
+hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p) {
+  if (!p.ok || (p.ksplit > 1 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
+  if (a.format == RQ_Q8_0) return launch_x<RQ_Q8_0, float>(a, p);
+  if (a.scale_dtype == RQ_F16) return launch_x<RQ_Q4_0, uint16_t>(a, p);
+  return launch_x<RQ_Q4_0, float>(a, p);
 }
 
 }  // namespace rq

@@ -74,15 +74,26 @@ struct MatmulArgs {
   int64_t npad;     // n padded to a multiple of 16 (rows present in the chunked layout)
   hipStream_t stream;
   void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
+  float* part;      // decode with K-split: partial sums, DecodePlan::part_bytes
+  int* cnt;         // decode with K-split: one zeroed counter per 16-row group
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
   // and these events take that dispatch's own start and end timestamps
   hipEvent_t ev_main[2] = {nullptr, nullptr};
 };
 
+// Decode kernel (m <= 16) launch plan: rows per MFMA group, waves per
+// workgroup, K-slices per 16-row group, grid and LDS; ok is false when the
+// decode kernel cannot take the shape (then the GEMM path runs).
+struct DecodePlan {
+  bool ok;
+  int mt, waves, ksplit, grid, lds_bytes;
+  size_t part_bytes;  // scratch for the slices' partial sums (ksplit > 1)
+  int counters;       // zero-initialised ints, one per 16-row group (ksplit > 1)
+};
+DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
+
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
-hipError_t launch_gemv(const MatmulArgs& a, int cu_count);
-// Largest k the decode kernel (launch_gemv) supports for m activation rows.
-int64_t skinny_max_k(int64_t m);
+hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).

@@ -293,22 +293,47 @@ def test_decode_special_activations(torch, ctx, orc):
     assert not np.any(np.isfinite(ref[3])) and not np.any(np.isfinite(ref[4]))
 
 
-def test_decode_falls_back_above_lds_limit(torch, ctx, orc):
-    # k beyond the decode kernel's LDS capacity goes to the GEMM kernels
+@pytest.mark.parametrize("m,in_,out", [(2, 20480, 16), (16, 8192, 48), (9, 4096, 4096)])
+def test_decode_k_split(torch, ctx, orc, m, in_, out):
+    # few 16-row groups, or activations too long for one workgroup's LDS: the
+    # decode kernel cuts K into slices whose partial sums one workgroup adds up
     import raster_amd
 
-    m, in_, out = 2, 20480, 16
     codes, scales = wl.q8_weights(out, in_, seed=8)
     x = wl.activations(m, in_, seed=9)
-    note("decode fallback k=20480")
+    note(f"decode k-split m={m} in={in_} out={out}")
     w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
     y = run(torch, w, x, m, "f32", "f32")
-    yb = run(torch, w, x, m, "bf16", "f32")
+    y2 = run(torch, w, x, m, "f32", "f32")
+    yb = run(torch, w, x, m, "bf16", "bf16")
     w.destroy()
-    ref = orc.qlinear_q8(x, codes, scales, m, in_, out).reshape(m, out)
-    assert orc.normwise_relerr(y, ref) < TOL_F32
-    refb = orc.qlinear_q8(wl.bf16_round(x), codes, scales, m, in_, out).reshape(m, out)
-    assert orc.normwise_relerr(yb, refb) < TOL_BF16
+    assert np.array_equal(y, y2), "split sums must be deterministic"
+    rows = rows_subset(out, 48)
+    ref = orc.qlinear_q8(x, codes.reshape(out, in_)[rows].ravel(), scales.reshape(out, -1)[rows].ravel(),
+                         m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y[:, rows], ref) < TOL_F32
+    dense = orc.dequant_q8_dense(codes.reshape(out, in_)[rows].ravel(), scales.reshape(out, -1)[rows].ravel(),
+                                 in_, len(rows))
+    bound = decomposition_bound(x.reshape(m, in_), dense, m, in_, len(rows))
+    assert np.all(np.abs(y[:, rows] - ref) <= bound)
+    refb = orc.qlinear_q8(wl.bf16_round(x), codes.reshape(out, in_)[rows].ravel(),
+                          scales.reshape(out, -1)[rows].ravel(), m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(yb[:, rows], refb) < TOL_BF16
+
+
+def test_decode_split_scratch_reuse_across_shapes(torch, ctx, orc):
+    # one stream, split calls of growing and shrinking group counts: every call
+    # must find its counters at zero (left there by the previous call)
+    import raster_amd
+
+    for out, in_, m in ((16, 4096, 1), (64, 8192, 3), (32, 2048, 4), (16, 4096, 1)):
+        codes, scales = wl.q8_weights(out, in_, seed=out + in_)
+        x = wl.activations(m, in_, seed=m)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        y = run(torch, w, x, m, "f32", "f32")
+        w.destroy()
+        ref = orc.qlinear_q8(x, codes, scales, m, in_, out).reshape(m, out)
+        assert orc.normwise_relerr(y, ref) < TOL_F32, (out, in_, m)
 
 
 def test_gemm_q4_bf16_m256(torch, ctx, orc):
