@@ -14,6 +14,8 @@ Beside it, on the same JSON line:
            back-to-back calls in one captured HIP graph, rotating through
            enough weight copies (> 512 MB) that every call reads its weight
            from HBM, not the 256 MB Infinity Cache ("cold"); warm = one copy.
+  decoder - the two-layer decode step (fourth workload configuration) in one
+           captured HIP graph: us per token step and tokens/s.
   sweep  - (--suite all) Q4 skinny M in {1,4,16} and the 70B-MLP shapes.
   roofline      - the GEMM kernel against dense bf16 MFMA peak: 2*M*K*N flop
                   per launch over the kernel's average duration, from the start
@@ -177,6 +179,58 @@ def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
     tf = c.flops / ms / 1e9
     return {"workload": name, "fmt": fmt, "m": m, "k": k, "n": n, "x": xdt, "y": ydt,
             "us": round(ms * 1e3, 3), "TFLOPs": round(tf, 2), "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def decoder_line(torch, ctx, replays=200):
+    """The two-layer decode step (d 2048, 16 x 128 heads, SwiGLU 5632, Q8_0,
+    128 cached positions, batch 1), captured in one HIP graph and replayed
+    back to back; us per step (one token), tokens/s and the GB/s of the
+    linears' weight bytes."""
+    from raster_amd import workloads as wl
+    from raster_amd.decoder import DecoderLayer
+
+    cfg = wl.DECODER
+    layers, x = wl.decoder_weights(cfg, seed=0)
+    dl = [DecoderLayer(ctx, L["weights"], L["gain1"], L["gain2"], cfg["d"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"],
+                       cfg["ffn"], cfg["eps"], cfg["theta"]) for L in layers]
+    kcs = [torch.from_numpy(L["kcache"]).cuda() for L in layers]
+    vcs = [torch.from_numpy(L["vcache"]).cuda() for L in layers]
+    xin = torch.from_numpy(x).cuda()
+    pos = cfg["cached"]
+
+    def step():
+        h = xin
+        for layer, kc, vc in zip(dl, kcs, vcs):
+            h = layer.step(h, kc, vc, pos)
+        return h
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for _ in range(10):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(replays):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / replays * 1e3
+    wbytes = sum(layer.matmul_bytes() for layer in dl)
+    del g
+    for layer in dl:
+        layer.destroy()
+    return {"workload": "two-layer decode step, d 2048, 16x128 heads, SwiGLU 5632, Q8_0, 128 cached positions",
+            "us_per_step": round(us, 3), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wbytes,
+            "weight_GBs": round(wbytes / us / 1e3, 1), "frac_hbm": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "note": "weights fit the 256 MB MALL, so replays read them warm; glue ops are f32 torch kernels"}
 
 
 COPY_ELEMS = 64 << 20  # f32 elements of the calibration copy: 256 MiB read + 256 MiB written
@@ -381,6 +435,11 @@ def main():
                                    "kernel": "rq::skinny_kernel<0, float, 0, 4, 16, 4>",
                                    "bytes_per_launch": gv["bytes"], "kernel_avg_us": gv["cold_us"]}
         log(f"gemv: cold {gv['cold_us']} us {gv['cold_GBs']} GB/s; warm {gv['warm_us']} us {gv['warm_GBs']} GB/s")
+
+    if not args.only_gemm:
+        log("two-layer decode step")
+        result["decoder"] = decoder_line(torch, ctx)
+        log(f"decoder: {result['decoder']['us_per_step']} us/step, {result['decoder']['tokens_per_s']} tokens/s")
 
     if args.suite == "all" and not args.only_gemm:
         sweep = []

@@ -74,6 +74,13 @@ def _declare(L):
         "rqo_q8_quantize": ([p, i64, i64, p, p], C.c_int),
         "rqo_dequant_q8_dense": ([p, p, i64, i64, p], None),
         "rqo_qlinear_q8": ([p, p, p, i64, i64, i64, p], None),
+        "rqo_rms_norm": ([p, p, p, i64, i64, d, d], None),
+        "rqo_rope_pos": ([p, p, i64, i64, i64, d, i64], None),
+        "rqo_gqa_decode_attention": ([p, p, p, i64, i64, i64, i64, d, p, p], None),
+        "rqo_silu_mul": ([p, p, p, i64], None),
+        "rqo_residual_add": ([p, p, p, i64], None),
+        "rqo_kv_append": ([p, p, i64, i64], None),
+        "rqo_decoder_layer": ([p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64, d, d, p], None),
         "rqo_qlinear_q8_dx": ([p, p, p, i64, i64, i64, p], None),
         "rqo_quantize_weight": ([p, i64, C.c_int, C.c_int, C.c_int, p, p], None),
         "rqo_dequant_weight": ([p, p, i64, C.c_int, C.c_int, p], None),
@@ -345,6 +352,67 @@ def dense_matmul_nt_f64(X, W, m: int, in_: int, out: int) -> np.ndarray:
     y = np.empty(m * out, np.float64)
     lib().rqo_dense_matmul_nt_f64(_ptr(X), _ptr(W), m, in_, out, _ptr(y))
     return y
+
+
+# ---------------------------------------------------------------- decoder glue
+def rms_norm(x, w, rows: int, features: int, eps: float, gain_offset: float) -> np.ndarray:
+    """raster.dl.nn/rms-norm! (nn.clj:497-516)."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    out = np.empty(rows * features, np.float32)
+    lib().rqo_rms_norm(_ptr(x), _ptr(w), _ptr(out), rows, features, eps, gain_offset)
+    return out
+
+
+def rope_pos(x, seq_len: int, heads: int, head_dim: int, theta: float, pos_offset: int) -> np.ndarray:
+    """raster.dl.attention/rope-pos (attention.clj:197-214)."""
+    x = _c(x, np.float32)
+    out = np.empty(seq_len * heads * head_dim, np.float32)
+    lib().rqo_rope_pos(_ptr(x), _ptr(out), seq_len, heads, head_dim, theta, pos_offset)
+    return out
+
+
+def gqa_decode_attention(q, k, v, cache_len: int, n_q: int, n_kv: int, head_dim: int, scale: float) -> np.ndarray:
+    """raster.dl.attention/gqa-decode-attention (attention.clj:248-287)."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    out = np.empty(n_q * head_dim, np.float32)
+    sc = np.empty(max(cache_len, 1), np.float32)
+    lib().rqo_gqa_decode_attention(_ptr(q), _ptr(k), _ptr(v), cache_len, n_q, n_kv, head_dim, scale, _ptr(out),
+                                   _ptr(sc))
+    return out
+
+
+def silu_mul(gate, up, n: int) -> np.ndarray:
+    """raster.dl.nn/silu-mul! (nn.clj:200-203)."""
+    gate, up = _c(gate, np.float32), _c(up, np.float32)
+    out = np.empty(n, np.float32)
+    lib().rqo_silu_mul(_ptr(gate), _ptr(up), _ptr(out), n)
+    return out
+
+
+def residual_add(a, b, n: int) -> np.ndarray:
+    """raster.dl.nn/residual-add! (nn.clj:217-219)."""
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    out = np.empty(n, np.float32)
+    lib().rqo_residual_add(_ptr(a), _ptr(b), _ptr(out), n)
+    return out
+
+
+def decoder_layer(x, weights, gain1, gain2, kcache, vcache, d: int, n_q: int, n_kv: int, head_dim: int, ffn: int,
+                  cache_len: int, eps: float, theta: float):
+    """One pre-norm decoder layer step (rqo_decoder_layer). weights: seven
+    (codes, scales) pairs for q, k, v, o, gate, up, down. Returns (x_out,
+    kcache, vcache) with the new position appended (copies; inputs untouched)."""
+    x = _c(x, np.float32).copy()
+    kc, vc = _c(kcache, np.float32).copy(), _c(vcache, np.float32).copy()
+    codes = [_c(c, np.int8) for c, _ in weights]
+    scales = [_c(s_, np.float32) for _, s_ in weights]
+    wp = (C.c_void_p * 7)(*[c.ctypes.data for c in codes])
+    sp = (C.c_void_p * 7)(*[s_.ctypes.data for s_ in scales])
+    g1, g2 = _c(gain1, np.float32), _c(gain2, np.float32)
+    scratch = np.empty(3 * d + 5 * n_q * head_dim + 3 * ffn + cache_len, np.float32)
+    lib().rqo_decoder_layer(_ptr(x), C.cast(wp, C.c_void_p), C.cast(sp, C.c_void_p), _ptr(g1), _ptr(g2), _ptr(kc),
+                            _ptr(vc), d, n_q, n_kv, head_dim, ffn, cache_len, eps, theta, _ptr(scratch))
+    return x, kc, vc
 
 
 def normwise_relerr(a, ref) -> float:

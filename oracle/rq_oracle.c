@@ -593,3 +593,140 @@ void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t 
       y[p * out + o] = s;
     }
 }
+
+/* ------------------------------------------------------------------------- */
+/* decoder-step glue (the host ops around the quantized linears)             */
+/* ------------------------------------------------------------------------- */
+/* rms-norm!: raster/dl/nn.clj:497-516. Row mean of squares in double, one
+ * f32 store of x * inv * (gain_offset + w). */
+void rqo_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t features, double eps,
+                  double gain_offset) {
+  for (int64_t r = 0; r < rows; r++) {
+    const float* xr = x + r * features;
+    double s = 0.0;
+    for (int64_t i = 0; i < features; i++) s += (double)xr[i] * (double)xr[i];
+    const double ms = s / (double)features;
+    const double inv = 1.0 / sqrt(ms + eps);
+    for (int64_t i = 0; i < features; i++)
+      out[r * features + i] = (float)((double)xr[i] * inv * (gain_offset + (double)w[i]));
+  }
+}
+
+/* rope-pos: raster/dl/attention.clj:197-214 (NeoX half split, positions
+ * pos_offset .. pos_offset + seq_len - 1). */
+void rqo_rope_pos(const float* x, float* out, int64_t seq_len, int64_t heads, int64_t head_dim, double theta,
+                  int64_t pos_offset) {
+  const int64_t half = head_dim / 2;
+  const double ln_theta = log(theta);
+  for (int64_t p = 0; p < seq_len; p++)
+    for (int64_t h = 0; h < heads; h++) {
+      const int64_t base = p * heads * head_dim + h * head_dim;
+      const double pos = (double)(pos_offset + p);
+      for (int64_t i = 0; i < half; i++) {
+        const double freq = exp((-2.0 * (double)i / (double)head_dim) * ln_theta);
+        const double ang = pos * freq;
+        const double c = cos(ang), s = sin(ang);
+        const double x0 = x[base + i], x1 = x[base + i + half];
+        out[base + i] = (float)(x0 * c - x1 * s);
+        out[base + i + half] = (float)(x1 * c + x0 * s);
+      }
+    }
+}
+
+/* gqa-decode-attention: raster/dl/attention.clj:248-287. Scores and the
+ * softmax numerators are stored as f32 (the `sc` scratch is an array like q);
+ * dot products, the sum and the output accumulation run in double. */
+void rqo_gqa_decode_attention(const float* q, const float* k, const float* v, int64_t cache_len, int64_t n_q,
+                              int64_t n_kv, int64_t head_dim, double scale, float* out, float* sc) {
+  const int64_t group = n_q / n_kv;
+  for (int64_t hq = 0; hq < n_q; hq++) {
+    const int64_t hkv = hq / group, qb = hq * head_dim;
+    for (int64_t j = 0; j < cache_len; j++) {
+      const int64_t kb = j * n_kv * head_dim + hkv * head_dim;
+      double dot = 0.0;
+      for (int64_t d = 0; d < head_dim; d++) dot += (double)q[qb + d] * (double)k[kb + d];
+      sc[j] = (float)(dot * scale);
+    }
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < cache_len; j++) mx = sc[j] > mx ? sc[j] : mx;
+    double sum = 0.0;
+    for (int64_t j = 0; j < cache_len; j++) {
+      const double e = exp((double)sc[j] - (double)mx);
+      sc[j] = (float)e;
+      sum += e;
+    }
+    const double inv = 1.0 / sum;
+    for (int64_t d = 0; d < head_dim; d++) {
+      double a = 0.0;
+      for (int64_t j = 0; j < cache_len; j++) {
+        const int64_t kvb = j * n_kv * head_dim + hkv * head_dim;
+        a += ((double)sc[j] * inv) * (double)v[kvb + d];
+      }
+      out[qb + d] = (float)a;
+    }
+  }
+}
+
+/* silu-mul!: raster/dl/nn.clj:200-203. */
+void rqo_silu_mul(const float* gate, const float* up, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    const double g = gate[i];
+    out[i] = (float)((g * (1.0 / (1.0 + exp(-g)))) * (double)up[i]);
+  }
+}
+
+/* residual-add!: raster/dl/nn.clj:217-219 (the double sum of two floats is
+ * exact, so this is the correctly rounded f32 sum). */
+void rqo_residual_add(const float* a, const float* b, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = (float)((double)a[i] + (double)b[i]);
+}
+
+/* kv-append!: raster/dl/attention.clj:413-416. */
+void rqo_kv_append(const float* src, float* cache, int64_t kvrow, int64_t pos) {
+  memcpy(cache + pos * kvrow, src, (size_t)kvrow * sizeof(float));
+}
+
+/* One pre-norm decoder layer for one token (Llama form of the step the
+ * reference chains in test/raster/dl/decoder_layer_gpu_test.clj:25-83, with
+ * RMSNorm, NeoX RoPE, SwiGLU and no q/k norms): the seven linears are
+ * rqo_qlinear_q8 over Q8_0 weights w[0..6] = q, k, v, o, gate, up, down
+ * (codes) with scales s[0..6]. kcache / vcache hold cache_len - 1 earlier
+ * positions of n_kv * head_dim floats and receive the new one at position
+ * cache_len - 1; x (d floats) is updated in place. gain1 / gain2 are the two
+ * RMSNorm weights (gain offset 0). scratch needs 3 * d + 5 * n_q * head_dim +
+ * 3 * ffn + cache_len floats. */
+void rqo_decoder_layer(float* x, const int8_t* const* w, const float* const* s, const float* gain1,
+                       const float* gain2, float* kcache, float* vcache, int64_t d, int64_t n_q, int64_t n_kv,
+                       int64_t head_dim, int64_t ffn, int64_t cache_len, double eps, double theta,
+                       float* scratch) {
+  const int64_t qd = n_q * head_dim, kvd = n_kv * head_dim, pos = cache_len - 1;
+  float* xn = scratch;
+  float* q = xn + d;
+  float* kk = q + qd;
+  float* vv = kk + qd;
+  float* qr = vv + qd;
+  float* at = qr + qd;
+  float* o = at + qd;
+  float* gate = o + d;
+  float* up = gate + ffn;
+  float* h = up + ffn;
+  float* dn = h + ffn;
+  float* sc = dn + d;
+  rqo_rms_norm(x, gain1, xn, 1, d, eps, 0.0);
+  rqo_qlinear_q8(xn, w[0], s[0], 1, d, qd, q);
+  rqo_qlinear_q8(xn, w[1], s[1], 1, d, kvd, kk);
+  rqo_qlinear_q8(xn, w[2], s[2], 1, d, kvd, vv);
+  rqo_rope_pos(q, qr, 1, n_q, head_dim, theta, pos);
+  rqo_rope_pos(kk, kcache + pos * kvd, 1, n_kv, head_dim, theta, pos); /* rotate straight into the cache */
+  rqo_kv_append(vv, vcache, kvd, pos);
+  rqo_gqa_decode_attention(qr, kcache, vcache, cache_len, n_q, n_kv, head_dim, 1.0 / sqrt((double)head_dim), at,
+                           sc);
+  rqo_qlinear_q8(at, w[3], s[3], 1, qd, d, o);
+  rqo_residual_add(x, o, x, d);
+  rqo_rms_norm(x, gain2, xn, 1, d, eps, 0.0);
+  rqo_qlinear_q8(xn, w[4], s[4], 1, d, ffn, gate);
+  rqo_qlinear_q8(xn, w[5], s[5], 1, d, ffn, up);
+  rqo_silu_mul(gate, up, h, ffn);
+  rqo_qlinear_q8(h, w[6], s[6], 1, ffn, d, dn);
+  rqo_residual_add(x, dn, x, d);
+}

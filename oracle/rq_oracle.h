@@ -129,6 +129,29 @@ void rqo_qmatmul_i8_gemm(const int32_t* xp, const float* xs, const int32_t* wp, 
 /* i8gemv-dp4a!: raster/quant/kernels_k.clj:141-150. */
 void rqo_i8gemv_dp4a(const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out);
 
+/* ---- decoder-step glue (f32 arrays, double arithmetic as on the JVM) ---- */
+/* rms-norm!: raster/dl/nn.clj:497-516. */
+void rqo_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t features, double eps,
+                  double gain_offset);
+/* rope-pos: raster/dl/attention.clj:197-214. */
+void rqo_rope_pos(const float* x, float* out, int64_t seq_len, int64_t heads, int64_t head_dim, double theta,
+                  int64_t pos_offset);
+/* gqa-decode-attention: raster/dl/attention.clj:248-287 (sc: cache_len floats of scratch). */
+void rqo_gqa_decode_attention(const float* q, const float* k, const float* v, int64_t cache_len, int64_t n_q,
+                              int64_t n_kv, int64_t head_dim, double scale, float* out, float* sc);
+/* silu-mul!: raster/dl/nn.clj:200-203. */
+void rqo_silu_mul(const float* gate, const float* up, float* out, int64_t n);
+/* residual-add!: raster/dl/nn.clj:217-219. */
+void rqo_residual_add(const float* a, const float* b, float* out, int64_t n);
+/* kv-append!: raster/dl/attention.clj:413-416. */
+void rqo_kv_append(const float* src, float* cache, int64_t kvrow, int64_t pos);
+/* One pre-norm decoder layer for one token over Q8_0 linears (q, k, v, o,
+ * gate, up, down); see rq_oracle.c. */
+void rqo_decoder_layer(float* x, const int8_t* const* w, const float* const* s, const float* gain1,
+                       const float* gain2, float* kcache, float* vcache, int64_t d, int64_t n_q, int64_t n_kv,
+                       int64_t head_dim, int64_t ffn, int64_t cache_len, double eps, double theta,
+                       float* scratch);
+
 /* ---- dense helpers (brute force, f64) used to pin the restatements ---- */
 void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t in, int64_t out,
                              double* y);

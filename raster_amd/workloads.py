@@ -54,3 +54,29 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:
     """bf16 bits of values already exactly representable in bf16."""
     return (np.ascontiguousarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+# The two-layer decode step: d_model 2048, 16 heads x 128, SwiGLU FFN 5632,
+# Q8_0 linears, RMSNorm gains 1.0, batch 1 against 128 cached positions.
+DECODER = dict(d=2048, n_q=16, n_kv=16, head_dim=128, ffn=5632, layers=2, cached=128, eps=1e-5, theta=1e4)
+
+
+def decoder_weights(cfg=DECODER, seed: int = 0):
+    """Per layer: seven (codes, scales) pairs (q, k, v, o, gate, up, down),
+    RMSNorm gains (1.0), and K / V caches of cfg['cached'] positions ~ N(0, 1)
+    with one free row for the new token. Returns (layers, x)."""
+    d, hd, ffn = cfg["d"], cfg["head_dim"], cfg["ffn"]
+    qd, kvd = cfg["n_q"] * hd, cfg["n_kv"] * hd
+    shapes = ((qd, d), (kvd, d), (kvd, d), (d, qd), (ffn, d), (ffn, d), (d, ffn))
+    layers = []
+    for li in range(cfg["layers"]):
+        ws = [q8_weights(o, i, seed=seed + 100 * li + j) for j, (o, i) in enumerate(shapes)]
+        rng = np.random.default_rng(seed + 100 * li + 50)
+        kc = np.zeros(((cfg["cached"] + 1), kvd), np.float32)
+        vc = np.zeros(((cfg["cached"] + 1), kvd), np.float32)
+        kc[:cfg["cached"]] = rng.standard_normal((cfg["cached"], kvd), dtype=np.float32)
+        vc[:cfg["cached"]] = rng.standard_normal((cfg["cached"], kvd), dtype=np.float32)
+        layers.append(dict(weights=ws, gain1=np.ones(d, np.float32), gain2=np.ones(d, np.float32), kcache=kc,
+                           vcache=vc))
+    x = np.random.default_rng(seed + 7).standard_normal(d, dtype=np.float32)
+    return layers, x

@@ -365,3 +365,121 @@ def test_staged_equals_flat_with_power_of_two_scales(orc):
     Wd = orc.dequant_q8_dense(codes, scales, in_, out)
     flat = orc.dense_matmul_nt_f64(x, Wd, m, in_, out)
     assert np.array_equal(y.astype(np.float64), flat)
+
+
+# ---------------------------------------------------------------- decoder-step glue
+def test_rms_norm_closed_forms(orc):
+    # [3, 4]: mean square 12.5, so out = x / sqrt(12.5); scaling x leaves the
+    # output unchanged (eps 0); the weight (plus the gain offset) scales it
+    out = orc.rms_norm(np.array([3, 4], np.float32), np.ones(2, np.float32), 1, 2, 0.0, 0.0)
+    assert np.allclose(out, np.array([3, 4]) / np.sqrt(12.5), rtol=1e-7)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(3 * 64).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    a = orc.rms_norm(x, w, 3, 64, 0.0, 0.0)
+    b = orc.rms_norm(x * np.float32(8), w, 3, 64, 0.0, 0.0)
+    assert np.array_equal(a, b)  # power-of-two scale: exact
+    one = orc.rms_norm(x, np.zeros(64, np.float32), 3, 64, 0.0, 1.0)  # gain-offset form (weight 0 + 1)
+    rms = np.sqrt(np.mean(one.reshape(3, 64).astype(np.float64) ** 2, axis=1))
+    assert np.allclose(rms, 1.0, atol=1e-6)
+    assert np.allclose(a, one * np.tile(w, 3), rtol=2e-7, atol=1e-7)
+
+
+def test_rope_pos_known_answer_and_rotation(orc):
+    # head_dim 4, theta 1e4: pair (0, 2) turns by pos * 1, pair (1, 3) by pos * 1e-2;
+    # NeoX half split: element i pairs with i + head_dim/2
+    out = orc.rope_pos(np.array([1, 0, 0, 0], np.float32), 1, 1, 4, 1e4, 1)
+    assert np.allclose(out, [np.cos(1.0), 0, np.sin(1.0), 0], atol=1e-7)
+    out = orc.rope_pos(np.array([0, 1, 0, 0], np.float32), 1, 1, 4, 1e4, 3)
+    assert np.allclose(out, [0, np.cos(0.03), 0, np.sin(0.03)], atol=1e-7)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(2 * 3 * 16).astype(np.float32)  # 2 positions x 3 heads x 16
+    assert np.array_equal(orc.rope_pos(x, 2, 3, 16, 1e4, 0)[:48], x[:48])  # position 0 is the identity
+    r = orc.rope_pos(x, 2, 3, 16, 1e4, 5).reshape(2, 3, 2, 8).astype(np.float64)
+    xr = x.reshape(2, 3, 2, 8).astype(np.float64)
+    assert np.allclose((r ** 2).sum(axis=2), (xr ** 2).sum(axis=2), rtol=1e-6)  # pairwise norms kept
+    # rotating by 5 then by 7 equals rotating by 12 (second token: positions 6 and 13)
+    twice = orc.rope_pos(orc.rope_pos(x, 2, 3, 16, 1e4, 5), 2, 3, 16, 1e4, 7)
+    once = orc.rope_pos(x, 2, 3, 16, 1e4, 12)
+    assert np.allclose(twice[:48], once[:48], atol=1e-5)
+
+
+def test_gqa_decode_attention_closed_forms(orc):
+    hd = 8
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(2 * hd).astype(np.float32)
+    k1 = rng.standard_normal(hd).astype(np.float32)
+    v1 = rng.standard_normal(hd).astype(np.float32)
+    # one cached position: every query head returns that value row
+    out = orc.gqa_decode_attention(q, k1, v1, 1, 2, 1, hd, 0.5)
+    assert np.allclose(out, np.tile(v1, 2), atol=1e-7)
+    # two positions with equal keys: the mean of the values
+    k = np.tile(k1, 2)
+    v = rng.standard_normal(2 * hd).astype(np.float32)
+    out = orc.gqa_decode_attention(q[:hd], k, v, 2, 1, 1, hd, 0.5)
+    assert np.allclose(out, v.reshape(2, hd).mean(axis=0), atol=1e-6)
+    # two positions whose scores differ by t: weights sigmoid(t), 1 - sigmoid(t)
+    ka = np.zeros(hd, np.float32)
+    ka[0] = 1.0
+    kb = np.zeros(hd, np.float32)
+    qq = np.zeros(hd, np.float32)
+    qq[0] = 2.0
+    out = orc.gqa_decode_attention(qq, np.concatenate([ka, kb]), v, 2, 1, 1, hd, 0.25)
+    t = 2.0 * 0.25
+    wa = 1.0 / (1.0 + np.exp(-t))
+    assert np.allclose(out, wa * v[:hd] + (1 - wa) * v[hd:], atol=1e-6)
+    # grouped heads: query heads 0,1 read kv head 0, heads 2,3 kv head 1
+    kk = rng.standard_normal(3 * 2 * hd).astype(np.float32)
+    vv = rng.standard_normal(3 * 2 * hd).astype(np.float32)
+    qs = rng.standard_normal(4 * hd).astype(np.float32)
+    full = orc.gqa_decode_attention(qs, kk, vv, 3, 4, 2, hd, 0.3)
+    sel = lambda a, h: a.reshape(3, 2, hd)[:, h, :].ravel()
+    for hq in range(4):
+        one = orc.gqa_decode_attention(qs[hq * hd:(hq + 1) * hd], sel(kk, hq // 2), sel(vv, hq // 2), 3, 1, 1, hd, 0.3)
+        assert np.array_equal(full[hq * hd:(hq + 1) * hd], one)
+
+
+def test_silu_mul_and_residual_add(orc):
+    g = np.array([0.0, 1.0, -1.0, 30.0], np.float32)
+    u = np.array([5.0, 2.0, 2.0, 1.0], np.float32)
+    out = orc.silu_mul(g, u, 4)
+    assert out[0] == 0.0
+    assert np.isclose(out[1], 2.0 / (1.0 + np.exp(-1.0)), rtol=1e-7)
+    assert np.isclose(out[1] - out[2], 2.0, rtol=1e-6)  # silu(x) - silu(-x) = x
+    assert np.isclose(out[3], 30.0, rtol=1e-7)
+    a = np.array([1.0, 1e8, -3.5], np.float32)
+    b = np.array([2.0, 1.0, 3.5], np.float32)
+    assert np.array_equal(orc.residual_add(a, b, 3), a + b)  # correctly rounded f32 sum
+
+
+def test_decoder_layer_composes_the_glue(orc):
+    # the layer equals its steps run one by one through the oracle's own pieces
+    # (checks the wiring: which buffer feeds which op, cache position, residuals)
+    d, nq, hd, ffn, clen = 64, 2, 32, 96, 4
+    rng = np.random.default_rng(4)
+    ws = []
+    for out, in_ in ((nq * hd, d), (nq * hd, d), (nq * hd, d), (d, nq * hd), (ffn, d), (ffn, d), (d, ffn)):
+        ws.append((rng.integers(-127, 128, out * in_).astype(np.int8),
+                   rng.uniform(0.002, 0.02, out * (in_ // 32)).astype(np.float32)))
+    x = rng.standard_normal(d).astype(np.float32)
+    g1 = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    g2 = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kc = rng.standard_normal(clen * nq * hd).astype(np.float32)
+    vc = rng.standard_normal(clen * nq * hd).astype(np.float32)
+    y, kc2, vc2 = orc.decoder_layer(x, ws, g1, g2, kc, vc, d, nq, nq, hd, ffn, clen, 1e-5, 1e4)
+    xn = orc.rms_norm(x, g1, 1, d, 1e-5, 0.0)
+    q = orc.qlinear_q8(xn, *ws[0], 1, d, nq * hd)
+    k = orc.qlinear_q8(xn, *ws[1], 1, d, nq * hd)
+    v = orc.qlinear_q8(xn, *ws[2], 1, d, nq * hd)
+    pos = clen - 1
+    kr = orc.rope_pos(k, 1, nq, hd, 1e4, pos)
+    kref, vref = kc.copy(), vc.copy()
+    kref[pos * nq * hd:] = kr
+    vref[pos * nq * hd:] = v
+    assert np.array_equal(kc2, kref) and np.array_equal(vc2, vref)
+    at = orc.gqa_decode_attention(orc.rope_pos(q, 1, nq, hd, 1e4, pos), kref, vref, clen, nq, nq, hd, hd ** -0.5)
+    x1 = orc.residual_add(x, orc.qlinear_q8(at, *ws[3], 1, nq * hd, d), d)
+    x1n = orc.rms_norm(x1, g2, 1, d, 1e-5, 0.0)
+    h = orc.silu_mul(orc.qlinear_q8(x1n, *ws[4], 1, d, ffn), orc.qlinear_q8(x1n, *ws[5], 1, d, ffn), ffn)
+    want = orc.residual_add(x1, orc.qlinear_q8(h, *ws[6], 1, ffn, d), d)
+    assert np.array_equal(y, want)
