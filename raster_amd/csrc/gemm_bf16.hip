@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void pack_x_kernel(const uint16_t* __restrict_
   if (b < nb) *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = t[r * 17 + (i >> 6) * 4 + fg];
 }
 
-template <int FMT, typename ST, int MT, int NTW>
+template <int FMT, typename ST, int MT, int NTW, int WD = 6>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                        const uint16_t* __restrict__ xf, void* __restrict__ y, int M,
                                                        int K, int N, int npad, int y_dtype, int tiles_m) {
@@ -158,14 +158,17 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
     for (int j = 0; j < NTW; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // Register rings (indices are compile-time inside the 6-step unrolled body):
-  //   areg: staged activation pieces of steps s+2 (written to LDS at step s)
-  //         and s+3 (loaded at step s)
+  //   areg: staged activation pieces of steps s+2 .. s+4 (step s+2 is
+  //         written to LDS at step s and its slot refilled with step s+5)
   //   afr:  activation fragments of steps s, s+1 (read from LDS one step ahead)
-  //   wc:   weight codes of steps s+1 .. s+3 (loaded 3 steps ahead)
+  //   wc:   weight codes of steps s+1 .. s+WD (loaded WD steps ahead: the
+  //         weights come from HBM, whose latency a shallower ring leaves
+  //         exposed)
   //   wf:   dequantized weight fragments of steps s, s+1
-  u32x4 areg[2][AP];
+  u32x4 areg[3][AP];
   bf16x8 afr[2][MT];
-  WCodes wc[3][NTW];
+  static_assert(WD == 3 || WD == 6, "the 6-step unrolled body indexes the ring modulo WD");
+  WCodes wc[WD][NTW];
   bf16x8 wf[2][NTW];
 
 #define RQ_LOAD_A(slot, kb_)                                                              \
@@ -191,42 +194,47 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
         load_wcodes<FMT, ST>(wc[slot][j], q, sc, wchunk[j] + kk_, fr, fg);                \
   } while (0)
 
-  // prologue: LDS buffers 0, 1 hold steps 0, 1; areg[0] holds step 2;
-  // afr[0] and wf[0] hold step 0; wc[1], wc[2] hold steps 1, 2.
+  // prologue: LDS buffers 0, 1 hold steps 0, 1; areg[s % 3] holds step s
+  // for s = 2, 3, 4; afr[0] and wf[0] hold step 0; wc[1 .. WD-1] hold steps
+  // 1 .. WD-1.
   RQ_LOAD_A(0, 0);
   RQ_LOAD_A(1, 1);
-  RQ_LOAD_W(0, 0);
-  RQ_LOAD_W(1, 1);
-  RQ_LOAD_W(2, 2);
+  RQ_LOAD_A(2, 2);
+#pragma unroll
+  for (int st = 0; st < WD; st++) RQ_LOAD_W(st, st);
   RQ_STORE_A(0, 0);
   RQ_STORE_A(1, 1);
-  RQ_LOAD_A(0, 2);
+  RQ_LOAD_A(0, 3);
+  RQ_LOAD_A(1, 4);
 #pragma unroll
   for (int j = 0; j < NTW; j++) wf[0][j] = dequant_frag<FMT>(wc[0][j], fg);
   __syncthreads();
   RQ_READ_A(0, 0);
 
   // k-step s (u = s % 6), software-pipelined:
-  //   global: activation pieces of step s+3 -> areg[(u+1) % 2];
-  //           weight codes of step s+3 -> wc[u % 3]
-  //   LDS:    write areg[u % 2] (step s+2) into buffer (u+2) % 3;
+  //   LDS:    write areg[(u+2) % 3] (step s+2) into buffer (u+2) % 3;
   //           read step s+1's activation fragments from buffer (u+1) % 3
+  //   global: activation pieces of step s+5 -> areg[(u+2) % 3];
+  //           weight codes of step s+WD -> wc[u % WD]
   //   MFMA:   wf[u % 2] (A operand, weights) x afr[u % 2] (B operand, activations)
-  //   VALU:   dequantize wc[(u+1) % 3] (step s+1) into wf[(u+1) % 2],
+  //   VALU:   dequantize wc[(u+1) % WD] (step s+1) into wf[(u+1) % 2],
   //           interleaved with the MFMAs.
   // One barrier per step: a buffer is rewritten two steps after its last read.
+  // Every load is consumed at least three steps after it is issued: the
+  // loads complete in issue order, so a shorter distance for either stream
+  // would make the wait for it also wait for the other's recent loads.
 #define RQ_STEP(kb_, u_)                                                                  \
   do {                                                                                    \
-    RQ_LOAD_A(((u_) + 1) % 2, (kb_) + 3);                                                 \
-    RQ_LOAD_W((u_) % 3, (kb_) + 3);                                                       \
-    RQ_STORE_A((u_) % 2, ((u_) + 2) % 3);                                                 \
+    RQ_STORE_A(((u_) + 2) % 3, ((u_) + 2) % 3);                                           \
+    RQ_LOAD_A(((u_) + 2) % 3, (kb_) + 5);                                                 \
+    RQ_LOAD_W((u_) % WD, (kb_) + WD);                                                     \
     RQ_READ_A(((u_) + 1) % 2, ((u_) + 1) % 3);                                            \
     __builtin_amdgcn_sched_barrier(0);                                                    \
     _Pragma("unroll") for (int j = 0; j < NTW; j++) {                                     \
       _Pragma("unroll") for (int i = 0; i < MT; i++)                                      \
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[(u_) % 2][j], afr[(u_) % 2][i], \
                                                             acc[i][j], 0, 0, 0);          \
-      wf[((u_) + 1) % 2][j] = dequant_frag<FMT>(wc[((u_) + 1) % 3][j], fg);               \
+      wf[((u_) + 1) % 2][j] = dequant_frag<FMT>(wc[((u_) + 1) % WD][j], fg);              \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
     __syncthreads();                                                                      \
@@ -285,6 +293,185 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   }
 }
 
+// Workgroup-shared weights: the 4 waves stack along M (MT 16-row activation
+// fragments each, BM = 64 MT rows) and share NT dequantized 16-row weight
+// fragments (BN = 16 NT columns) through LDS. Per k-step every weight element
+// is dequantized once per workgroup and each fragment feeds 4 MT MFMAs;
+// activation fragments go from the fragment-major copy straight into
+// registers (no LDS), since no two waves use the same rows.
+// Pipeline per k-step s (unrolled by R so every ring index is compile-time):
+//   VMEM: activation fragments of step s+R-1 -> ring slot (s+R-1) % R, weight
+//         codes of step s+R -> slot s % R (loads complete in issue order, so
+//         both streams get at least R-2 steps of slack)
+//   LDS:  read step s+1's weight fragments (buffer (s+1) % 4) into registers;
+//         write step s+2's, dequantized, into buffer (s+2) % 4
+//   MFMA: step s, with the weight fragments read during step s-1
+//   one barrier
+template <int FMT, typename ST, int MT, int NT, int R>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_wl_kernel(
+    const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
+    int M, int K, int N, int npad, int y_dtype, int tiles_m) {
+  constexpr int CW = (NT + 3) / 4;  // weight fragments a wave dequantizes per step (at most)
+  static_assert(R % 4 == 0 && R >= 4, "ring depth: a multiple of the 4 LDS buffers");
+  __shared__ __attribute__((aligned(16))) bf16x8 Bs[4][NT][64];
+
+  const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nkb = K / 32;
+  const int m0 = tm * (64 * MT) + wave * (16 * MT);  // this wave's first row
+  const int n0 = tn * (16 * NT);
+
+  // activation fragment i of this wave (rows m0 + 16 i ..): clamped to the
+  // padded rows, whose outputs are never stored
+  const int mt_last = (M + 15) / 16 - 1;
+  const uint16_t* asrc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; i++) asrc[i] = xf + (int64_t)min(m0 / 16 + i, mt_last) * nkb * 512 + lane * 8;
+  // weight fragments this wave dequantizes: c = wave + 4 j < NT
+  const int g_last = npad / 16 - 1;
+  int64_t wchunk[CW];
+#pragma unroll
+  for (int j = 0; j < CW; j++) wchunk[j] = (int64_t)min(n0 / 16 + min(wave + 4 * j, NT - 1), g_last) * nkb;
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int c = 0; c < NT; c++) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  bf16x8 a[R][MT];
+  WCodes wc[R][CW];
+  bf16x8 b[2][NT];
+
+#define WL_LOAD_A(kb_)                                                                            \
+  do {                                                                                            \
+    const int kk_ = min((kb_), nkb - 1);                                                          \
+    _Pragma("unroll") for (int i = 0; i < MT; i++) a[(kb_) % R][i] =                              \
+        *reinterpret_cast<const bf16x8*>(asrc[i] + (int64_t)kk_ * 512);                           \
+  } while (0)
+#define WL_LOAD_W(kb_)                                                                            \
+  do {                                                                                            \
+    const int kk_ = min((kb_), nkb - 1);                                                          \
+    _Pragma("unroll") for (int j = 0; j < CW; j++)                                                \
+        load_wcodes<FMT, ST>(wc[(kb_) % R][j], q, sc, wchunk[j] + kk_, fr, fg);                   \
+  } while (0)
+#define WL_DEQUANT(kb_)                                                                           \
+  do {                                                                                            \
+    _Pragma("unroll") for (int j = 0; j < CW; j++) {                                              \
+      const bf16x8 d_ = dequant_frag<FMT>(wc[(kb_) % R][j], fg);                                  \
+      if (wave + 4 * j < NT) Bs[(kb_) % 4][wave + 4 * j][lane] = d_;                              \
+    }                                                                                             \
+  } while (0)
+#define WL_READ_B(kb_)                                                                            \
+  do {                                                                                            \
+    _Pragma("unroll") for (int c = 0; c < NT; c++) b[(kb_) % 2][c] = Bs[(kb_) % 4][c][lane];      \
+  } while (0)
+#define WL_MFMA(kb_, c0, c1)                                                                      \
+  do {                                                                                            \
+    _Pragma("unroll") for (int c = (c0); c < (c1); c++)                                           \
+      _Pragma("unroll") for (int i = 0; i < MT; i++)                                              \
+        acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[(kb_) % 2][c], a[(kb_) % R][i], acc[i][c], 0, 0, 0); \
+  } while (0)
+
+  // prologue: a holds steps 0..R-2, wc steps 0..R-1; LDS buffers 0, 1
+  // hold steps 0, 1 and b[0] step 0
+#pragma unroll
+  for (int st = 0; st < R - 1; st++) {
+    WL_LOAD_A(st);
+    WL_LOAD_W(st);
+  }
+  WL_LOAD_W(R - 1);
+  WL_DEQUANT(0);
+  WL_DEQUANT(1);
+  __syncthreads();
+  WL_READ_B(0);
+
+  // the step body for kb_ with compile-time residue u_ = kb_ % R
+#define WL_STEP(kb_, u_)                                                                          \
+  do {                                                                                            \
+    WL_LOAD_A_U((kb_) + R - 1, (u_) + R - 1);                                                     \
+    WL_LOAD_W_U((kb_) + R, (u_) + R);                                                             \
+    WL_READ_B_U((u_) + 1);                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    WL_MFMA_U(u_, 0, NT / 2);                                                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    WL_DEQUANT_U((u_) + 2);                                                                       \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    WL_MFMA_U(u_, NT / 2, NT);                                                                    \
+    __syncthreads();                                                                              \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  } while (0)
+// ring indices from the residue u (a multiple-of-R shift leaves every ring
+// index unchanged); the load macros take the true step for address clamping
+#define WL_LOAD_A_U(kb_, u_)                                                                      \
+  do {                                                                                            \
+    const int kk_ = min((kb_), nkb - 1);                                                          \
+    _Pragma("unroll") for (int i = 0; i < MT; i++) a[(u_) % R][i] =                               \
+        *reinterpret_cast<const bf16x8*>(asrc[i] + (int64_t)kk_ * 512);                           \
+  } while (0)
+#define WL_LOAD_W_U(kb_, u_)                                                                      \
+  do {                                                                                            \
+    const int kk_ = min((kb_), nkb - 1);                                                          \
+    _Pragma("unroll") for (int j = 0; j < CW; j++)                                                \
+        load_wcodes<FMT, ST>(wc[(u_) % R][j], q, sc, wchunk[j] + kk_, fr, fg);                    \
+  } while (0)
+#define WL_READ_B_U(u_) WL_READ_B(u_)
+#define WL_DEQUANT_U(u_) WL_DEQUANT(u_)
+#define WL_MFMA_U(u_, c0, c1) WL_MFMA(u_, c0, c1)
+
+  int kb = 0;
+  for (; kb + R <= nkb; kb += R) {
+#pragma unroll
+    for (int u = 0; u < R; u++) WL_STEP(kb + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u < R - 1; u++)
+    if (kb + u < nkb) WL_STEP(kb + u, u);
+#undef WL_STEP
+#undef WL_LOAD_A_U
+#undef WL_LOAD_W_U
+#undef WL_READ_B_U
+#undef WL_DEQUANT_U
+#undef WL_MFMA_U
+#undef WL_MFMA
+#undef WL_READ_B
+#undef WL_DEQUANT
+#undef WL_LOAD_W
+#undef WL_LOAD_A
+
+  // epilogue: acc[i][c] holds y[m][n .. n+3], m = m0 + 16 i + fr,
+  // n = n0 + 16 c + 4 fg
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int m = m0 + i * 16 + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int c = 0; c < NT; c++) {
+      const int n = n0 + c * 16 + 4 * fg;
+      const f32x4 v = acc[i][c];
+      if (vec && n + 3 < N) {
+        if (y_dtype == RQ_F32)
+          *reinterpret_cast<float4*>(static_cast<float*>(y) + (int64_t)m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
+        else
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + (int64_t)m * N + n) =
+              make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (n + r >= N) break;
+          if (y_dtype == RQ_F32)
+            static_cast<float*>(y)[(int64_t)m * N + n + r] = v[r];
+          else
+            static_cast<uint16_t*>(y)[(int64_t)m * N + n + r] = (uint16_t)f32_to_bf16_bits(v[r]);
+        }
+      }
+    }
+  }
+}
+
 hipError_t launch_pack_x(const MatmulArgs& a) {
   const int64_t pack_blocks = (a.m + 15) / 16 * ((a.k / 32 + 3) / 4);
   hipLaunchKernelGGL(pack_x_kernel, dim3((unsigned)pack_blocks), dim3(256), 0, a.stream,
@@ -305,14 +492,28 @@ static hipError_t launch_t(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-// Tile: BM = 128 rows (64 when M <= 64) x BN = 128 columns. Measured with
-// random data at M = 512 (K 4096, N 11008) and M = 256 (K 8192, N 28672)
-// against 64 x 128, 128 x 192 and a variant that dequantizes each weight tile
-// once into LDS for 256-row tiles: 128 x 128 was fastest or within 1% at both
-// shapes, on par with hipBLASLt's dense bf16 GEMM there.
+template <int FMT, typename ST, int MT, int NT, int R>
+static hipError_t launch_wl(const MatmulArgs& a) {
+  const int tiles_m = (int)((a.m + 64 * MT - 1) / (64 * MT));
+  const int tiles_n = (int)((a.npad / 16 + NT - 1) / NT);
+  if (hipError_t e = launch_pack_x(a)) return e;
+  hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
+                        a.stream, a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype, tiles_m);
+  return hipGetLastError();
+}
+
+// Kernel and tile by M, measured with random data at M = 256, 512, 1024
+// (K 4096 / 8192, N 11008 / 28672): for M > 128 the shared-weight kernel with
+// 256 x 64 tiles and 4-deep rings (two workgroups per CU) is 8 to 25% faster
+// than 128 x 128 per-wave weights, whose tile suits smaller M. (Deeper rings
+// make the compiler wait for every load and 6 or more shared fragments per
+// tile were slower still.)
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   (void)cu_count;
+  if (a.m > 128) return launch_wl<FMT, ST, 4, 4, 4>(a);
   if (a.m <= 64) return launch_t<FMT, ST, 4, 2>(a);
   return launch_t<FMT, ST, 8, 2>(a);
 }
