@@ -181,18 +181,16 @@ def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
             "us": round(ms * 1e3, 3), "TFLOPs": round(tf, 2), "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
-def decoder_line(torch, ctx, replays=200):
-    """The two-layer decode step (d 2048, 16 x 128 heads, SwiGLU 5632, Q8_0,
-    128 cached positions, batch 1), captured in one HIP graph and replayed
-    back to back; us per step (one token), tokens/s and the GB/s of the
-    linears' weight bytes."""
+def decoder_step_us(torch, ctx, fused, replays=200):
+    """us per replay of the two-layer decode step captured in one HIP graph,
+    and the linears' weight bytes."""
     from raster_amd import workloads as wl
     from raster_amd.decoder import DecoderLayer
 
     cfg = wl.DECODER
     layers, x = wl.decoder_weights(cfg, seed=0)
     dl = [DecoderLayer(ctx, L["weights"], L["gain1"], L["gain2"], cfg["d"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"],
-                       cfg["ffn"], cfg["eps"], cfg["theta"]) for L in layers]
+                       cfg["ffn"], cfg["eps"], cfg["theta"], fused=fused) for L in layers]
     kcs = [torch.from_numpy(L["kcache"]).cuda() for L in layers]
     vcs = [torch.from_numpy(L["vcache"]).cuda() for L in layers]
     xin = torch.from_numpy(x).cuda()
@@ -227,10 +225,22 @@ def decoder_line(torch, ctx, replays=200):
     del g
     for layer in dl:
         layer.destroy()
+    return us, wbytes
+
+
+def decoder_line(torch, ctx):
+    """The two-layer decode step (d 2048, 16 x 128 heads, SwiGLU 5632, Q8_0,
+    128 cached positions, batch 1), captured in one HIP graph and replayed
+    back to back: us per step (one token), tokens/s and the GB/s of the
+    linears' weight bytes, for the fused chain (norms, SwiGLU and residuals in
+    the matmuls, one attention kernel) and for the unfused one (torch glue)."""
+    us, wbytes = decoder_step_us(torch, ctx, fused=True)
+    us_unfused, _ = decoder_step_us(torch, ctx, fused=False)
     return {"workload": "two-layer decode step, d 2048, 16x128 heads, SwiGLU 5632, Q8_0, 128 cached positions",
             "us_per_step": round(us, 3), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wbytes,
             "weight_GBs": round(wbytes / us / 1e3, 1), "frac_hbm": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "note": "weights fit the 256 MB MALL, so replays read them warm; glue ops are f32 torch kernels"}
+            "unfused_us_per_step": round(us_unfused, 3),
+            "note": "weights fit the 256 MB MALL, so replays read them warm; fused: 5 librq launches per layer"}
 
 
 COPY_ELEMS = 64 << 20  # f32 elements of the calibration copy: 256 MiB read + 256 MiB written
@@ -322,7 +332,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
     ap.add_argument("--only-decode", action="store_true",
-                    help="time the decode shapes only (C1 GEMV, Q4 skinny, 70B M=1) for profiling")
+                    help="time the decode shapes only (C1 GEMV, Q4 skinny, 70B M=1, decoder step) for profiling")
     ap.add_argument("--traffic-run", action="store_true",
                     help="a short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: a copy kernel of "
                          "known size (calibration), then the headline GEMM and the cold C1 decode kernel")
@@ -356,8 +366,10 @@ def main():
         for ln in lines:
             log(f"{ln['workload']} {ln['fmt']} m={ln['m']}: cold {ln['cold_us']} us {ln['cold_GBs']} GB/s, "
                 f"warm {ln['warm_us']} us {ln['warm_GBs']} GB/s")
+        dec = decoder_line(torch, ctx)
+        log(f"decoder: {dec['us_per_step']} us/step fused, {dec['unfused_us_per_step']} us/step unfused")
         ctx.close()
-        print(json.dumps({"decode": lines}), flush=True)
+        print(json.dumps({"decode": lines, "decoder": dec}), flush=True)
         return
 
     if args.traffic_run:
@@ -439,7 +451,8 @@ def main():
     if not args.only_gemm:
         log("two-layer decode step")
         result["decoder"] = decoder_line(torch, ctx)
-        log(f"decoder: {result['decoder']['us_per_step']} us/step, {result['decoder']['tokens_per_s']} tokens/s")
+        log(f"decoder: {result['decoder']['us_per_step']} us/step fused, {result['decoder']['tokens_per_s']} tokens/s;"
+            f" {result['decoder']['unfused_us_per_step']} us/step unfused")
 
     if args.suite == "all" and not args.only_gemm:
         sweep = []

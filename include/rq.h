@@ -162,6 +162,44 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
 int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                void* stream);
 
+/* Options of rq_qmatmul_fused; a NULL / 0 field is off. They fold the
+ * decoder glue around a linear into its decode kernel (Raster chains them as
+ * separate ops, test/raster/dl/decoder_layer_gpu_test.clj:25-83):
+ *  - norm_gain (device f32[in], 16-byte aligned): each row of x is first
+ *    RMS-normalised, x * (mean(x^2) + norm_eps)^-1/2 * norm_gain[k]
+ *    (rms-norm! with gain offset 0, raster/dl/nn.clj:497-516);
+ *  - residual (device, y's dtype and shape): y = residual + x . W^T
+ *    (residual-add!, raster/dl/nn.clj:217-219);
+ *  - swiglu: weight rows 2i and 2i+1 are a gate row and an up row; y[m, i] =
+ *    silu(z[m, 2i]) * z[m, 2i+1] for the product z, so y has out/2 columns
+ *    (silu-mul!, raster/dl/nn.clj:200-203). Not combined with residual.
+ * The epilogue math runs in f32. */
+typedef struct {
+  const float* norm_gain;
+  float norm_eps;
+  const void* residual;
+  int swiglu;
+} rq_fused_ops;
+
+/* rq_qmatmul with fused options, for m <= 16 (the decode kernel); larger m
+ * fails with RQ_ERR_SHAPE. No counterpart in the reference as one call: it
+ * replaces the op sequences named in rq_fused_ops around a qlinear. */
+int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+                     const rq_fused_ops* ops, void* stream);
+
+/* One decode step of RoPE, KV-cache append and single-query attention, the
+ * glue between a decoder layer's q/k/v and o linears, all on the device:
+ * rope-pos (raster/dl/attention.clj:197-214, NeoX half split, angle
+ * pos * theta^(-2i/head_dim)) of q f32[n_q*head_dim] and of k
+ * f32[n_kv*head_dim]; kv-append! (attention.clj:413-416) of the rotated k and
+ * of v f32[n_kv*head_dim] into row pos of kcache / vcache (f32, rows of
+ * n_kv*head_dim); gqa-decode-attention (attention.clj:248-287) of the rotated
+ * query over rows 0..pos with the given scale: out f32[n_q*head_dim]. Query
+ * head h reads KV head h / (n_q/n_kv). pos + 1 <= about 40K positions. */
+int rq_decode_attention(rq_ctx ctx, const float* q, const float* k, const float* v, float* kcache, float* vcache,
+                        int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale,
+                        float* out, void* stream);
+
 /* Writes the dequantized f32 weight W[out*in] (device pointer) using the same
  * device-side decode as the matmul kernels. Replaces dequant-q8-dense
  * (raster/quant/train.clj:60-71) and the Q4_0 dequant

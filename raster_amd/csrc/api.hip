@@ -578,7 +578,13 @@ static int lookup(rq_ctx h, rq_weight wh, Ctx** c, Weight* copy) {
   return RQ_OK;
 }
 
-int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m, void* stream) {
+}  // extern "C"
+
+namespace rq {
+
+// rq_qmatmul / rq_qmatmul_fused; ops == nullptr is the plain product.
+static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+                        const rq_fused_ops* ops, void* stream) {
   Ctx* c;
   Weight w;
   if (int s = lookup(h, wh, &c, &w)) return s;
@@ -590,6 +596,19 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
   if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
   if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
+  DecodeOps dops = {nullptr, 0.0f, nullptr, 0};
+  if (ops) {
+    if (!plan.ok) return fail(RQ_ERR_SHAPE, "fused options need the decode kernel: m <= 16");
+    if (ops->norm_gain && ((uintptr_t)ops->norm_gain & 15) != 0)
+      return fail(RQ_ERR_SHAPE, "norm_gain must be 16-byte aligned");
+    if (ops->norm_gain && !(ops->norm_eps >= 0.0f)) return fail(RQ_ERR_SHAPE, "norm_eps must be >= 0");
+    if (ops->swiglu && (w.out % 2) != 0) return fail(RQ_ERR_SHAPE, "swiglu needs an even number of rows");
+    if (ops->swiglu && ops->residual) return fail(RQ_ERR_SHAPE, "swiglu and residual cannot be combined");
+    if (ops->residual && ((uintptr_t)ops->residual & (y_dtype == RQ_F32 ? 3 : 1)) != 0)
+      return fail(RQ_ERR_SHAPE, "residual misaligned");
+    dops = {ops->norm_gain, ops->norm_eps, ops->residual, ops->swiglu ? 1 : 0};
+  }
   if (int s = set_device(c)) return s;
   MatmulArgs a;
   a.q = w.q;
@@ -608,7 +627,7 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
   a.scratch = nullptr;
   a.part = nullptr;
   a.cnt = nullptr;
-  const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
+  a.ops = dops;
   if (plan.ok && plan.ksplit > 1) {
     if (int s = stream_split(c, a.stream, plan.counters, plan.part_bytes, &a.cnt, &a.part)) return s;
   } else if (!plan.ok && x_dtype == RQ_BF16) {
@@ -624,6 +643,40 @@ int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int 
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return RQ_OK;
+}
+
+}  // namespace rq
+
+extern "C" {
+
+int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m, void* stream) {
+  return qmatmul_impl(h, wh, x, x_dtype, y, y_dtype, m, nullptr, stream);
+}
+
+int rq_qmatmul_fused(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+                     const rq_fused_ops* ops, void* stream) {
+  if (!ops) return fail(RQ_ERR_NULL, "ops is NULL");
+  return qmatmul_impl(h, wh, x, x_dtype, y, y_dtype, m, ops, stream);
+}
+
+int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v, float* kcache, float* vcache,
+                        int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale,
+                        float* out, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!q || !k || !v || !kcache || !vcache || !out) return fail(RQ_ERR_NULL, "NULL argument");
+  if (pos < 0 || n_q <= 0 || n_kv <= 0 || head_dim <= 0) return fail(RQ_ERR_SHAPE, "negative or zero dimension");
+  if (n_q % n_kv != 0) return fail(RQ_ERR_SHAPE, "n_q must be a multiple of n_kv");
+  if (head_dim % 2 != 0) return fail(RQ_ERR_SHAPE, "head_dim must be even");
+  if (n_q > 65535 || head_dim > 65536 || pos > INT32_MAX - 1) return fail(RQ_ERR_SHAPE, "dimension too large");
+  if (decode_attention_lds(pos, head_dim) > 163840)
+    return fail(RQ_ERR_SHAPE, "cache longer than one workgroup's LDS holds (about 40K positions)");
+  if (!(theta > 0.0)) return fail(RQ_ERR_SHAPE, "theta must be positive");
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_decode_attention(q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out,
+                                         (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "attention launch");
   return RQ_OK;
 }
 

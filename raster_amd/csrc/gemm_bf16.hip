@@ -303,17 +303,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
 //   VMEM: activation fragments of step s+R-1 -> ring slot (s+R-1) % R, weight
 //         codes of step s+R -> slot s % R (loads complete in issue order, so
 //         both streams get at least R-2 steps of slack)
-//   LDS:  read step s+1's weight fragments (buffer (s+1) % 4) into registers;
-//         write step s+2's, dequantized, into buffer (s+2) % 4
+//   LDS:  read step s+1's weight fragments (buffer (s+1) % L) into registers;
+//         write step s+2's, dequantized, into buffer (s+2) % L (L = 4 LDS
+//         buffers when R is a multiple of 4, else 3, so that R steps cover
+//         whole turns of every ring)
 //   MFMA: step s, with the weight fragments read during step s-1
 //   one barrier
-template <int FMT, typename ST, int MT, int NT, int R>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_wl_kernel(
+template <int FMT, typename ST, int MT, int NT, int R, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_wl_kernel(
     const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
     int M, int K, int N, int npad, int y_dtype, int tiles_m) {
   constexpr int CW = (NT + 3) / 4;  // weight fragments a wave dequantizes per step (at most)
-  static_assert(R % 4 == 0 && R >= 4, "ring depth: a multiple of the 4 LDS buffers");
-  __shared__ __attribute__((aligned(16))) bf16x8 Bs[4][NT][64];
+  constexpr int L = R % 4 == 0 ? 4 : 3;
+  static_assert(R >= 4 && R % L == 0 && R % 2 == 0, "ring depth: whole turns of the LDS and fragment rings");
+  __shared__ __attribute__((aligned(16))) bf16x8 Bs[L][NT][64];
 
   const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -361,12 +364,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   do {                                                                                            \
     _Pragma("unroll") for (int j = 0; j < CW; j++) {                                              \
       const bf16x8 d_ = dequant_frag<FMT>(wc[(kb_) % R][j], fg);                                  \
-      if (wave + 4 * j < NT) Bs[(kb_) % 4][wave + 4 * j][lane] = d_;                              \
+      if (wave + 4 * j < NT) Bs[(kb_) % L][wave + 4 * j][lane] = d_;                              \
     }                                                                                             \
   } while (0)
 #define WL_READ_B(kb_)                                                                            \
   do {                                                                                            \
-    _Pragma("unroll") for (int c = 0; c < NT; c++) b[(kb_) % 2][c] = Bs[(kb_) % 4][c][lane];      \
+    _Pragma("unroll") for (int c = 0; c < NT; c++) b[(kb_) % 2][c] = Bs[(kb_) % L][c][lane];      \
   } while (0)
 #define WL_MFMA(kb_, c0, c1)                                                                      \
   do {                                                                                            \
@@ -492,12 +495,12 @@ static hipError_t launch_t(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-template <int FMT, typename ST, int MT, int NT, int R>
+template <int FMT, typename ST, int MT, int NT, int R, int WPE>
 static hipError_t launch_wl(const MatmulArgs& a) {
   const int tiles_m = (int)((a.m + 64 * MT - 1) / (64 * MT));
   const int tiles_n = (int)((a.npad / 16 + NT - 1) / NT);
   if (hipError_t e = launch_pack_x(a)) return e;
-  hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
+  hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R, WPE>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
                         a.stream, a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m);
@@ -513,7 +516,7 @@ static hipError_t launch_wl(const MatmulArgs& a) {
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   (void)cu_count;
-  if (a.m > 128) return launch_wl<FMT, ST, 4, 4, 4>(a);
+  if (a.m > 128) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
   if (a.m <= 64) return launch_t<FMT, ST, 4, 2>(a);
   return launch_t<FMT, ST, 8, 2>(a);
 }

@@ -161,7 +161,8 @@ template <int FMT, typename ST, int XT, int MT, int WAVES, int NB>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                            const void* __restrict__ x, void* __restrict__ y, int M,
                                                            int K, int N, int npad, int y_dtype, int ksplit,
-                                                           float* __restrict__ part, int* __restrict__ cnt) {
+                                                           float* __restrict__ part, int* __restrict__ cnt,
+                                                           DecodeOps ops) {
   constexpr int MG = MT / 4;                 // MFMAs per window (4 activation rows each)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nb = K / 32, nw = (K + 63) / 64;
@@ -176,6 +177,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   float* xsf = reinterpret_cast<float*>(smem + L.xsf);
   int* xs = reinterpret_cast<int*>(smem + L.xs);
   float* red = reinterpret_cast<float*>(smem + L.red);
+  // optional input RMSNorm factors 1 / sqrt(mean(x^2) + eps), one per row
+  // (in `red`, unused until the first group finishes)
+  float* nrm = red;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers and branches
@@ -271,11 +275,48 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
       const int it0 = base + lane + 64 * j;
       const int it = min(it0, witems - 1);
       const int mm = it / (nblk_w * 8), rb = rb0 + (it >> 3) % nblk_w, pt = it & 7;
+      if (ops.norm_gain) {
+        const int k = min(32 * (2 * s_beg + rb) + 4 * pt, K - 4);
+        const f32x4 gv = *reinterpret_cast<const f32x4*>(ops.norm_gain + k);
+        const float f = nrm[mm];
+#pragma unroll
+        for (int e = 0; e < 4; e++) xv[j][e] = xv[j][e] * (f * gv[e]);
+      }
       decompose_item(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
     }
   };
   const int gcols = (int)gridDim.x / ksplit;  // workgroups per slice
   const int gfirst = (int)blockIdx.x / ksplit;
+  // the norm factors over all of K (every workgroup reads the whole rows;
+  // they are small at m <= 16): M results, then the waves' partial sums
+  if (ops.norm_gain) {
+    float ss[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; mm++) ss[mm] = 0.0f;
+    for (int k = 4 * tid; k < K; k += 4 * 64 * WAVES) {
+#pragma unroll
+      for (int mm = 0; mm < MT; mm++) {
+        if (mm >= M) break;
+        float v[4];
+        load_x4<XT>(x, (int64_t)mm * K + k, true, v);
+        ss[mm] += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      }
+    }
+#pragma unroll
+    for (int mm = 0; mm < MT; mm++) {
+      float t = ss[mm];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+      if (lane == 0 && mm < M) nrm[16 + mm * WAVES + wave] = t;
+    }
+    __syncthreads();
+    if (tid < M) {
+      float t = 0.0f;
+      for (int wv = 0; wv < WAVES; wv++) t += nrm[16 + tid * WAVES + wv];
+      nrm[tid] = 1.0f / sqrtf(t / (float)K + ops.norm_eps);
+    }
+    __syncthreads();
+  }
   load_chunk(0);
   // keep the scheduler from hoisting the weight loads above the activation
   // loads: the decomposition below waits for the activations only
@@ -295,6 +336,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // the wave reads back what its own lanes wrote
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
+  // the norm factors live in `red`, which the first finished group
+  // overwrites: every wave must be done with them first
+  if (ops.norm_gain) __syncthreads();
 
   float acc[MG];
 #pragma unroll
@@ -418,14 +462,25 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
         }
       }
       if (store) {
+        // swiglu: lane r (even) holds the gate row, lane r + 1 the up row
+        const int ny = ops.swiglu ? N / 2 : N, oy = ops.swiglu ? o / 2 : o;
 #pragma unroll
         for (int mg = 0; mg < MG; mg++) {
           const int m = 4 * mg + g4;
-          if (m < M && o < N) {
+          float out = v[mg];
+          if (ops.swiglu) {
+            const float up = __shfl_down(out, 1, 64);
+            out = out / (1.0f + expf(-out)) * up;
+          }
+          const bool mine = m < M && o < N && (!ops.swiglu || (r & 1) == 0);
+          if (mine) {
+            if (ops.residual)
+              out += y_dtype == RQ_F32 ? static_cast<const float*>(ops.residual)[(int64_t)m * ny + oy]
+                                       : bf16_bits_to_f32(static_cast<const uint16_t*>(ops.residual)[(int64_t)m * ny + oy]);
             if (y_dtype == RQ_F32)
-              static_cast<float*>(y)[(int64_t)m * N + o] = v[mg];
+              static_cast<float*>(y)[(int64_t)m * ny + oy] = out;
             else
-              static_cast<uint16_t*>(y)[(int64_t)m * N + o] = (uint16_t)f32_to_bf16_bits(v[mg]);
+              static_cast<uint16_t*>(y)[(int64_t)m * ny + oy] = (uint16_t)f32_to_bf16_bits(out);
           }
         }
       }
@@ -500,7 +555,7 @@ static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
   }
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(64 * WAVES), (unsigned)p.lds_bytes, a.stream,
                         a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m,
-                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.cnt);
+                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.cnt, a.ops);
   return hipGetLastError();
 }
 

@@ -60,6 +60,14 @@ __host__ __device__ __forceinline__ int64_t scale_off(int64_t row, int64_t b, in
   return chunk_of(row, b, nb) * 16 + (row & 15);
 }
 
+// Fused decode options (rq_qmatmul_fused); all off when zero.
+struct DecodeOps {
+  const float* norm_gain;  // RMSNorm of each x row first, times gain[k]
+  float norm_eps;
+  const void* residual;    // y = residual + product (y's dtype and shape)
+  int swiglu;              // y[m][i] = silu(z[m][2i]) * z[m][2i+1]; y has n / 2 columns
+};
+
 // Launch descriptor for the matmul kernels.
 struct MatmulArgs {
   const uint8_t* q;
@@ -76,6 +84,7 @@ struct MatmulArgs {
   void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
   float* part;      // decode with K-split: partial sums, DecodePlan::part_bytes
   int* cnt;         // decode with K-split: one zeroed counter per 16-row group
+  DecodeOps ops = {nullptr, 0.0f, nullptr, 0};
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
   // and these events take that dispatch's own start and end timestamps
   hipEvent_t ev_main[2] = {nullptr, nullptr};
@@ -99,6 +108,11 @@ hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).
 hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
+// RoPE + KV append + single-query attention for one decode step (attention.hip).
+size_t decode_attention_lds(int64_t pos, int64_t head_dim);
+hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
+                                   int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
+                                   double scale, float* out, hipStream_t stream);
 // Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
                                int64_t in, int64_t npad, uint8_t* q, void* s, hipStream_t stream);

@@ -12,11 +12,20 @@ reference's names and math:
   residual_add          raster/dl/nn.clj:217-219
   kv_append             raster/dl/attention.clj:413-416
 
-The seven linears (q, k, v, o, gate, up, down) run through rq_qmatmul: the
-decode kernel at m = 1. q, k and v share one resident weight (their rows
-stacked), and so do gate and up, so a layer makes four matmul calls; stacking
-rows changes no output element. The glue runs as f32 torch ops on the same
-stream: device-memory plumbing around the matmuls, which are the hot path.
+The seven linears (q, k, v, o, gate, up, down) run on librq's decode kernel
+at m = 1. q, k and v share one resident weight (their rows stacked), and so do
+gate and up, so a layer makes four matmul calls; stacking rows changes no
+output element. Two ways to run the glue:
+
+  fused (default)  five librq calls per layer, no torch op: the RMSNorms ride
+                   in the q/k/v and gate/up matmuls (rq_qmatmul_fused), the
+                   residual adds in the o and down matmuls, SwiGLU in the
+                   gate/up epilogue (gate and up rows interleaved), and RoPE,
+                   KV append and attention in rq_decode_attention.
+  unfused          rq_qmatmul for the linears and the glue as f32 torch ops
+                   on the same stream (the functions above, a plain
+                   restatement kept as the second path of the parity tests).
+
 A whole step can be captured in one HIP graph (no call allocates).
 """
 from __future__ import annotations
@@ -25,7 +34,7 @@ import math
 
 import numpy as np
 
-from .quant import Context, QWeight
+from .quant import Context, QWeight, decode_attention
 
 
 def rms_norm(torch, x, weight, eps: float, gain_offset: float = 0.0):
@@ -82,18 +91,25 @@ class DecoderLayer:
     layout for q, k, v, o, gate, up, down."""
 
     def __init__(self, ctx: Context, weights, gain1, gain2, d: int, n_q: int, n_kv: int, head_dim: int, ffn: int,
-                 eps: float = 1e-5, theta: float = 1e4):
+                 eps: float = 1e-5, theta: float = 1e4, fused: bool = True):
         import torch
 
         if n_q % n_kv:
             raise ValueError("n_q must be a multiple of n_kv")
+        self.ctx, self.fused = ctx, fused
         self.d, self.n_q, self.n_kv, self.hd, self.ffn = d, n_q, n_kv, head_dim, ffn
         self.eps, self.theta = eps, theta
         qd, kvd = n_q * head_dim, n_kv * head_dim
         (cq, sq), (ck, sk), (cv, sv), (co, so), (cg, sg), (cu, su), (cd, sd) = weights
         self.w_qkv = QWeight.q8(np.concatenate([cq, ck, cv]), np.concatenate([sq, sk, sv]), qd + 2 * kvd, d, ctx)
         self.w_o = QWeight.q8(co, so, d, qd, ctx)
-        self.w_gu = QWeight.q8(np.concatenate([cg, cu]), np.concatenate([sg, su]), 2 * ffn, d, ctx)
+        if fused:
+            # rows 2i / 2i+1 = gate row i / up row i: the SwiGLU epilogue pairs them
+            gu = np.stack([np.asarray(cg).reshape(ffn, d), np.asarray(cu).reshape(ffn, d)], axis=1).reshape(-1)
+            gus = np.stack([np.asarray(sg).reshape(ffn, -1), np.asarray(su).reshape(ffn, -1)], axis=1).reshape(-1)
+            self.w_gu = QWeight.q8(np.ascontiguousarray(gu), np.ascontiguousarray(gus), 2 * ffn, d, ctx)
+        else:
+            self.w_gu = QWeight.q8(np.concatenate([cg, cu]), np.concatenate([sg, su]), 2 * ffn, d, ctx)
         self.w_d = QWeight.q8(cd, sd, d, ffn, ctx)
         dev = torch.device("cuda", ctx.device)
         self.g1 = torch.as_tensor(np.ascontiguousarray(gain1, np.float32), device=dev)
@@ -107,6 +123,13 @@ class DecoderLayer:
         import torch
 
         qd, kvd = self.n_q * self.hd, self.n_kv * self.hd
+        if self.fused:
+            qkv = self.w_qkv.matmul_fused(x.view(1, -1), norm_gain=self.g1, norm_eps=self.eps).view(-1)
+            at = decode_attention(self.ctx, qkv[:qd], qkv[qd:qd + kvd], qkv[qd + kvd:], kcache, vcache, pos,
+                                  self.n_q, self.n_kv, self.hd, self.theta, 1.0 / math.sqrt(self.hd))
+            x1 = self.w_o.matmul_fused(at.view(1, -1), residual=x.view(1, -1))
+            h = self.w_gu.matmul_fused(x1, norm_gain=self.g2, norm_eps=self.eps, swiglu=True)
+            return self.w_d.matmul_fused(h, residual=x1).view(-1)
         if pos not in self._rope:
             self._rope[pos] = rope_tables(torch, self.hd, self.theta, pos, x.device)
         cos, sin = self._rope[pos]

@@ -23,7 +23,7 @@ from . import _lib
 from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, RqError, call, lib
 
 __all__ = [
-    "Context", "QWeight", "RqError", "context", "qlinear_q8", "dequant_q8_dense",
+    "Context", "QWeight", "RqError", "context", "decode_attention", "qlinear_q8", "dequant_q8_dense",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]
 
@@ -181,6 +181,36 @@ class QWeight:
              C.c_void_p(y.data_ptr()), _dtype_code(y), m, _stream_ptr(stream))
         return y
 
+    def matmul_fused(self, x, y=None, out_dtype=None, norm_gain=None, norm_eps: float = 0.0, residual=None,
+                     swiglu: bool = False, stream=None):
+        """rq_qmatmul_fused (m <= 16): the decode matmul with an optional
+        RMSNorm of x's rows (norm_gain f32[in]) before it, and either a SwiGLU
+        of row pairs (rows 2i / 2i+1 = gate / up; y is [m, out/2]) or a
+        residual add (residual [m, out], y's dtype) after it."""
+        import torch
+
+        _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous CUDA tensor")
+        _need(x.numel() % self.in_ == 0, "x.numel() must be a multiple of in")
+        m = x.numel() // self.in_
+        ny = self.out // 2 if swiglu else self.out
+        if y is None:
+            y = torch.empty((m, ny), dtype=out_dtype or torch.float32, device=x.device)
+        _need(y.is_cuda and y.is_contiguous() and y.numel() == m * ny, "y must be a contiguous CUDA tensor of m rows")
+        ops = _lib.FusedOps(None, float(norm_eps), None, 1 if swiglu else 0)
+        if norm_gain is not None:
+            _need(norm_gain.is_cuda and norm_gain.dtype == torch.float32 and norm_gain.is_contiguous()
+                  and norm_gain.numel() == self.in_, "norm_gain must be a contiguous f32 CUDA tensor of in elements")
+            ops.norm_gain = norm_gain.data_ptr()
+        if residual is not None:
+            _need(residual.is_cuda and residual.is_contiguous() and residual.dtype == y.dtype
+                  and residual.numel() == m * ny, "residual must match y")
+            ops.residual = residual.data_ptr()
+        if stream is None:
+            stream = torch.cuda.current_stream(x.device)
+        call("rq_qmatmul_fused", self.ctx.handle, self.handle, C.c_void_p(x.data_ptr()), _dtype_code(x),
+             C.c_void_p(y.data_ptr()), _dtype_code(y), m, C.byref(ops), _stream_ptr(stream))
+        return y
+
     def dequant(self, stream=None):
         """Dequantized f32 W[out, in] computed on the device."""
         import torch
@@ -200,6 +230,33 @@ class QWeight:
         if self.handle:
             call("rq_weight_destroy", self.handle)
             self.handle = None
+
+
+def decode_attention(ctx: Context, q, k, v, kcache, vcache, pos: int, n_q: int, n_kv: int, head_dim: int,
+                     theta: float, scale: float, out=None, stream=None):
+    """rq_decode_attention: RoPE of q [n_q*head_dim] and k [n_kv*head_dim] at
+    `pos`, append of the rotated k and of v to row pos of kcache / vcache
+    ([rows, n_kv*head_dim] f32), and single-query attention over rows 0..pos.
+    Returns out [n_q*head_dim] f32."""
+    import torch
+
+    kvd = n_kv * head_dim
+    for t, n in ((q, n_q * head_dim), (k, kvd), (v, kvd)):
+        _need(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32 and t.numel() == n,
+              "q, k, v must be contiguous f32 CUDA tensors of n_q*head_dim / n_kv*head_dim elements")
+    for t in (kcache, vcache):
+        _need(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32 and t.numel() >= (pos + 1) * kvd,
+              "kcache / vcache must be contiguous f32 CUDA tensors of at least pos+1 rows")
+    if out is None:
+        out = torch.empty(n_q * head_dim, dtype=torch.float32, device=q.device)
+    _need(out.is_cuda and out.is_contiguous() and out.dtype == torch.float32 and out.numel() == n_q * head_dim,
+          "out must be a contiguous f32 CUDA tensor of n_q*head_dim elements")
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device)
+    ptr = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    call("rq_decode_attention", ctx.handle, ptr(q), ptr(k), ptr(v), ptr(kcache), ptr(vcache), pos, n_q, n_kv,
+         head_dim, float(theta), float(scale), ptr(out), _stream_ptr(stream))
+    return out
 
 
 def _need(cond: bool, msg: str) -> None:

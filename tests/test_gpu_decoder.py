@@ -34,11 +34,11 @@ def ctx(torch):
     c.close()
 
 
-def run_decoder(torch, ctx, cfg, layers, x, graph=False, replays=1):
+def run_decoder(torch, ctx, cfg, layers, x, graph=False, replays=1, fused=True):
     from raster_amd.decoder import DecoderLayer
 
     dl = [DecoderLayer(ctx, L["weights"], L["gain1"], L["gain2"], cfg["d"], cfg["n_q"], cfg["n_kv"],
-                       cfg["head_dim"], cfg["ffn"], cfg["eps"], cfg["theta"]) for L in layers]
+                       cfg["head_dim"], cfg["ffn"], cfg["eps"], cfg["theta"], fused=fused) for L in layers]
     kcs = [torch.from_numpy(L["kcache"]).cuda() for L in layers]
     vcs = [torch.from_numpy(L["vcache"]).cuda() for L in layers]
     pos = cfg["cached"]
@@ -102,20 +102,23 @@ def orc_err(a, b):
     return float(np.max(np.abs(a - b)) / max(1e-9, np.max(np.abs(b))))
 
 
-def test_two_layer_decode_step(torch, ctx, orc):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_two_layer_decode_step(torch, ctx, orc, fused):
     cfg = wl.DECODER
     layers, x = wl.decoder_weights(cfg, seed=0)
-    print(f"[gpu] decoder d={cfg['d']} layers={cfg['layers']} cached={cfg['cached']}", flush=True)
-    outs, kcs, vcs = run_decoder(torch, ctx, cfg, layers, x)
+    print(f"[gpu] decoder d={cfg['d']} layers={cfg['layers']} cached={cfg['cached']} fused={fused}", flush=True)
+    outs, kcs, vcs = run_decoder(torch, ctx, cfg, layers, x, fused=fused)
     check(outs, kcs, vcs, oracle_decoder(orc, cfg, layers, x), cfg)
 
 
-def test_decode_step_graph_replays(torch, ctx, orc):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_decode_step_graph_replays(torch, ctx, orc, fused):
     # a captured step replayed several times (eager work in between) gives the
     # eager result every time; a small grouped-query config
     cfg = dict(wl.DECODER, d=512, n_q=8, n_kv=2, head_dim=64, ffn=1024, cached=9)
     layers, x = wl.decoder_weights(cfg, seed=3)
-    outs, kcs, vcs = run_decoder(torch, ctx, cfg, layers, x, graph=True, replays=3)
+    print(f"[gpu] decoder graph d={cfg['d']} n_q={cfg['n_q']} n_kv={cfg['n_kv']} fused={fused}", flush=True)
+    outs, kcs, vcs = run_decoder(torch, ctx, cfg, layers, x, graph=True, replays=3, fused=fused)
     ref = oracle_decoder(orc, cfg, layers, x)
     check(outs, kcs, vcs, ref, cfg)
     assert all(np.array_equal(outs[0], o) for o in outs[1:])
