@@ -195,7 +195,9 @@ int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* 
  * of v f32[n_kv*head_dim] into row pos of kcache / vcache (f32, rows of
  * n_kv*head_dim); gqa-decode-attention (attention.clj:248-287) of the rotated
  * query over rows 0..pos with the given scale: out f32[n_q*head_dim]. Query
- * head h reads KV head h / (n_q/n_kv). pos + 1 <= about 40K positions. */
+ * head h reads KV head h / (n_q/n_kv). head_dim a multiple of 4 up to 512:
+ * any cache length; other even head_dim: pos + 1 <= about 40K positions
+ * (the scores sit in one workgroup's LDS). */
 int rq_decode_attention(rq_ctx ctx, const float* q, const float* k, const float* v, float* kcache, float* vcache,
                         int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale,
                         float* out, void* stream);

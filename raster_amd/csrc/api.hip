@@ -671,7 +671,8 @@ int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v
   if (head_dim % 2 != 0) return fail(RQ_ERR_SHAPE, "head_dim must be even");
   if (n_q > 65535 || head_dim > 65536 || pos > INT32_MAX - 1) return fail(RQ_ERR_SHAPE, "dimension too large");
   if (decode_attention_lds(pos, head_dim) > 163840)
-    return fail(RQ_ERR_SHAPE, "cache longer than one workgroup's LDS holds (about 40K positions)");
+    return fail(RQ_ERR_SHAPE, "cache longer than one workgroup's LDS holds (head_dim not a multiple of 4 "
+                              "or above 512: about 40K positions)");
   if (!(theta > 0.0)) return fail(RQ_ERR_SHAPE, "theta must be positive");
   if (int s = set_device(c)) return s;
   hipError_t e = launch_decode_attention(q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out,

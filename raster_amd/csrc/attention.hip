@@ -7,11 +7,24 @@
 //   gqa-decode-attention   raster/dl/attention.clj:248-287
 // One workgroup per query head. It rotates its query and its KV head's new
 // key (angles pos * theta^(-2i/head_dim) in double, as the reference), takes
-// the scores of positions 0..pos (the new key straight from registers, the
-// older ones from the cache), their softmax, and the weighted sum of values.
-// The first query head of each KV head writes the rotated key and the value
-// into the caches at row pos; the others never read that row from memory, so
-// no workgroup waits for another.
+// the scores of positions 0..pos (the new key from LDS, the older ones from
+// the cache), their softmax, and the weighted sum of values. The first query
+// head of each KV head writes the rotated key and the value into the caches
+// at row pos; no workgroup reads row pos from memory, so none waits for
+// another.
+//
+// Two kernels:
+//   chunk kernel (head_dim a multiple of 4, at most 512): the cached rows
+//     0..pos-1 stream through registers in chunks of rows, K and V of a chunk
+//     loaded together as 16-byte vectors and the next chunk's loads in flight
+//     while the current one is used. TPR lanes hold one row (4 or 8 of its
+//     dimensions each), so a wave holds 64/TPR rows per load. Each wave keeps
+//     its own running maximum, sum and weighted values (the usual online
+//     softmax); the four waves' states are combined at the end. Memory
+//     latency is paid about once per two chunks instead of once per row.
+//   generic kernel (any even head_dim): a wave per position for the scores,
+//     a thread per dimension for the values; the scores sit in LDS, so the
+//     cache length is bounded by it.
 #include <atomic>
 #include <cmath>
 
@@ -110,13 +123,230 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
   }
 }
 
+namespace {
+
+// lanes per row and 4-dimension vectors per lane of the chunk kernel, or 0
+int chunk_tpr(int64_t head_dim) {
+  if (head_dim % 4 != 0 || head_dim > 512) return 0;
+  return head_dim <= 64 ? 16 : head_dim <= 128 ? 32 : 64;
+}
+
+constexpr int kMaxDims = 512;
+
+}  // namespace
+
+// TPR lanes per row, NV 4-dimension vectors per lane (dimension
+// 4 (lane % TPR) + 4 TPR v), NP rows per lane per chunk
+template <int TPR, int NV, int NP>
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ kcache,
+    float* __restrict__ vcache, int pos, int n_q, int n_kv, int head_dim, double theta, float scale,
+    float* __restrict__ out) {
+  constexpr int WAVES = kAttnThreads / 64;
+  constexpr int RW = 64 / TPR;         // rows per wave per load
+  constexpr int CH = WAVES * RW * NP;  // rows per chunk
+  __shared__ __attribute__((aligned(16))) float qr[kMaxDims];
+  __shared__ __attribute__((aligned(16))) float kr[kMaxDims];
+  __shared__ __attribute__((aligned(16))) float vn[kMaxDims];
+  __shared__ __attribute__((aligned(16))) float wacc[WAVES][kMaxDims];
+  __shared__ float wm[WAVES], wl[WAVES];
+  const int hq = blockIdx.x, group = n_q / n_kv, hkv = hq / group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane % TPR, rg = lane / TPR;
+  const int half = head_dim / 2, kvd = n_kv * head_dim;
+  const int nrows = pos;  // cached rows read from memory
+  const int nch = (nrows + CH - 1) / CH;
+  const float* kb = kcache + hkv * head_dim;
+  const float* vb = vcache + hkv * head_dim;
+
+  // this lane's rows of chunk c: c CH + p WAVES RW + wave RW + rg. Loads are
+  // unconditional at clamped rows / dimensions; the masks act at use.
+  f32x4 kx[2][NP][NV], vx[2][NP][NV];
+  auto load = [&](int slot, int c) {
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int row = min(c * CH + p * WAVES * RW + wave * RW + rg, nrows - 1);
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) {
+        const int d = min(4 * sub + 4 * TPR * nv, head_dim - 4);
+        kx[slot][p][nv] = *reinterpret_cast<const f32x4*>(kb + (int64_t)row * kvd + d);
+        vx[slot][p][nv] = *reinterpret_cast<const f32x4*>(vb + (int64_t)row * kvd + d);
+      }
+    }
+  };
+  if (nch > 0) load(0, 0);
+
+  // RoPE of this head's query and of the KV head's new key; the value as is
+  const double ln_theta = log(theta);
+  for (int i = tid; i < half; i += kAttnThreads) {
+    const double ang = (double)pos * exp((-2.0 * (double)i / (double)head_dim) * ln_theta);
+    const double c = cos(ang), s = sin(ang);
+    const double q0 = q[hq * head_dim + i], q1 = q[hq * head_dim + i + half];
+    qr[i] = (float)(q0 * c - q1 * s);
+    qr[i + half] = (float)(q1 * c + q0 * s);
+    const double k0 = k[hkv * head_dim + i], k1 = k[hkv * head_dim + i + half];
+    kr[i] = (float)(k0 * c - k1 * s);
+    kr[i + half] = (float)(k1 * c + k0 * s);
+  }
+  for (int d = tid; d < head_dim; d += kAttnThreads) vn[d] = v[hkv * head_dim + d];
+  __syncthreads();
+  if (hq % group == 0) {
+    for (int d = tid; d < head_dim; d += kAttnThreads) {
+      kcache[(int64_t)pos * kvd + hkv * head_dim + d] = kr[d];
+      vcache[(int64_t)pos * kvd + hkv * head_dim + d] = vn[d];
+    }
+  }
+  // the lane's query dimensions (zero past head_dim)
+  f32x4 q4[NV];
+  bool dlive[NV];
+#pragma unroll
+  for (int nv = 0; nv < NV; nv++) {
+    const int d = 4 * sub + 4 * TPR * nv;
+    dlive[nv] = d < head_dim;
+    const f32x4 t = *reinterpret_cast<const f32x4*>(qr + min(d, head_dim - 4));
+    q4[nv] = dlive[nv] ? t : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // the wave's online softmax state: running maximum m (wave-uniform), the
+  // sum of exp(s - m) over the lane's row group, and the weighted values
+  float m = -INFINITY, l = 0.0f;
+  f32x4 acc[NV];
+#pragma unroll
+  for (int nv = 0; nv < NV; nv++) acc[nv] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto fold = [&](float (&s)[NP], f32x4 (&vv)[NP][NV]) {
+    float mc = s[0];
+#pragma unroll
+    for (int p = 1; p < NP; p++) mc = fmaxf(mc, s[p]);
+#pragma unroll
+    for (int off = TPR; off < 64; off <<= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
+    const float mn = fmaxf(m, mc);
+    const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++) acc[nv] *= alpha;
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const float e = s[p] == -INFINITY ? 0.0f : expf(s[p] - mn);
+      l += e;
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) acc[nv] += e * vv[p][nv];
+    }
+    m = mn;
+  };
+  auto compute = [&](int slot, int c) {
+    float s[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) {
+        const f32x4 kk = kx[slot][p][nv];
+        dot += q4[nv][0] * kk[0] + q4[nv][1] * kk[1] + q4[nv][2] * kk[2] + q4[nv][3] * kk[3];
+      }
+#pragma unroll
+      for (int off = TPR / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+      const int row = c * CH + p * WAVES * RW + wave * RW + rg;
+      s[p] = row < nrows ? dot * scale : -INFINITY;
+    }
+    fold(s, vx[slot]);
+  };
+  for (int c = 0; c < nch; c += 2) {
+    if (c + 1 < nch) load(1, c + 1);
+    compute(0, c);
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) load(0, c + 2);
+    compute(1, c + 1);
+  }
+
+  // the new row (pos) from LDS, folded into wave 0's state by its row group 0
+  if (wave == 0) {
+    float dot = 0.0f;
+    f32x4 vv[NP][NV];
+    float s[NP];
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++) {
+      const int d = min(4 * sub + 4 * TPR * nv, head_dim - 4);
+      const f32x4 kk = *reinterpret_cast<const f32x4*>(kr + d);
+      dot += q4[nv][0] * kk[0] + q4[nv][1] * kk[1] + q4[nv][2] * kk[2] + q4[nv][3] * kk[3];
+      vv[0][nv] = *reinterpret_cast<const f32x4*>(vn + d);
+    }
+#pragma unroll
+    for (int off = TPR / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+    s[0] = rg == 0 ? dot * scale : -INFINITY;
+#pragma unroll
+    for (int p = 1; p < NP; p++) {
+      s[p] = -INFINITY;
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) vv[p][nv] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    fold(s, vv);
+  }
+
+  // the wave's row groups, then the waves
+#pragma unroll
+  for (int off = TPR; off < 64; off <<= 1) {
+    l += __shfl_xor(l, off, 64);
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[nv][e] += __shfl_xor(acc[nv][e], off, 64);
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++)
+      if (dlive[nv]) *reinterpret_cast<f32x4*>(&wacc[wave][4 * sub + 4 * TPR * nv]) = acc[nv];
+  }
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  __syncthreads();
+  float mx = wm[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; w++) mx = fmaxf(mx, wm[w]);
+  float f[WAVES], sum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < WAVES; w++) {
+    f[w] = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - mx);
+    sum += f[w] * wl[w];
+  }
+  const float inv = 1.0f / sum;
+  for (int d = tid; d < head_dim; d += kAttnThreads) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) a += f[w] * wacc[w][d];
+    out[hq * head_dim + d] = a * inv;
+  }
+}
+
 size_t decode_attention_lds(int64_t pos, int64_t head_dim) {
+  if (chunk_tpr(head_dim)) return (size_t)(3 + kAttnThreads / 64) * kMaxDims * sizeof(float);
   return (size_t)(3 * head_dim + pos + 1 + 8) * sizeof(float);
 }
 
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
                                    double scale, float* out, hipStream_t stream) {
+  switch (chunk_tpr(head_dim)) {
+#define RQ_ATTN(TPR, NV, NP)                                                                                        \
+  hipLaunchKernelGGL((decode_attention_chunk_kernel<TPR, NV, NP>), dim3((unsigned)n_q), dim3(kAttnThreads), 0,   \
+                     stream, q, k, v, kcache, vcache, (int)pos, (int)n_q, (int)n_kv, (int)head_dim, theta,        \
+                     (float)scale, out);                                                                           \
+  return hipGetLastError();
+    case 16:
+      RQ_ATTN(16, 1, 8)
+    case 32:
+      RQ_ATTN(32, 1, 8)
+    case 64:
+      if (head_dim <= 256) {
+        RQ_ATTN(64, 1, 8)
+      }
+      RQ_ATTN(64, 2, 4)
+#undef RQ_ATTN
+    default:
+      break;
+  }
   const size_t lds = decode_attention_lds(pos, head_dim);
   if (lds > 65536) {
     static std::atomic<uint64_t> attr_set{0};

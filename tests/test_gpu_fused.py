@@ -193,11 +193,15 @@ def test_fused_rejects_bad_options(torch, ctx):
 
 
 # ---------------------------------------------------------------- decode attention
-@pytest.mark.parametrize("n_q,n_kv,hd,pos", [(16, 16, 128, 128), (8, 2, 64, 9), (32, 8, 128, 1000), (4, 4, 64, 0),
-                                             (4, 1, 256, 5), (2, 2, 320, 3), (8, 8, 128, 20000)])
+@pytest.mark.parametrize("n_q,n_kv,hd,pos", [
+    (16, 16, 128, 128), (8, 2, 64, 9), (32, 8, 128, 1000), (4, 4, 64, 0), (4, 1, 256, 5), (2, 2, 320, 3),
+    (8, 8, 128, 20000), (4, 2, 128, 63), (4, 2, 128, 64), (4, 2, 128, 65), (6, 3, 96, 200), (2, 1, 512, 70),
+    (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000)])
 def test_decode_attention(torch, ctx, orc, n_q, n_kv, hd, pos):
-    # (.., 0): only the new key; hd 320: more dimensions than threads;
-    # pos 20000: scores beyond 64 KB of LDS
+    # head_dim a multiple of 4 up to 512 runs the chunk kernel (chunks of 64
+    # rows at hd 128: pos 63 / 64 / 65 end inside, at and past a chunk;
+    # hd 96 / 320 leave lanes idle); 66 and 18 run the generic kernel
+    # ((3, 3, 66, 30000): scores beyond 64 KB of LDS). (.., 0): only the new key
     import raster_amd
 
     kvd = n_kv * hd
@@ -242,8 +246,8 @@ def test_decode_attention_rejects_bad_shapes(torch, ctx):
         raster_amd.decode_attention(ctx, z(3 * 64), z(2 * 64), z(2 * 64), z(4 * 128), z(4 * 128), 1, 3, 2, 64, 1e4,
                                     0.125)
     assert e.value.status == RQ_ERR_SHAPE
-    with pytest.raises(RqError) as e:  # cache too long for LDS
+    with pytest.raises(RqError) as e:  # generic kernel: cache too long for LDS
         n = 50000
-        raster_amd.decode_attention(ctx, z(64), z(64), z(64), z((n + 1) * 64), z((n + 1) * 64), n, 1, 1, 64, 1e4,
+        raster_amd.decode_attention(ctx, z(66), z(66), z(66), z((n + 1) * 66), z((n + 1) * 66), n, 1, 1, 66, 1e4,
                                     0.125)
     assert e.value.status == RQ_ERR_SHAPE
