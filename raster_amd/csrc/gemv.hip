@@ -60,6 +60,7 @@ struct SkinnyLds {
   int xs;       // i32 xs[mt + 1][xstr]: sum of X over the block (Q4 zero-point); row mt zero
   int zero;     // 16 zero bytes
   int red;      // f32 red[waves][mg][64]
+  int nss;      // f32 nss[waves][mt]: the waves' partial sums of squares (input RMSNorm)
   int bytes;
   __host__ __device__ SkinnyLds(int mt, int k, int waves) {
     kp = (k + 63) / 64 * 64;
@@ -71,7 +72,8 @@ struct SkinnyLds {
     xs = xsf + (mt + 1) * xstr * 4;
     zero = xs + (mt + 1) * xstr * 4;
     red = zero + 16;
-    bytes = red + waves * (mt / 4) * 64 * 4;
+    nss = red + waves * (mt / 4) * 64 * 4;
+    bytes = nss + waves * mt * 4;
   }
 };
 
@@ -177,9 +179,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   float* xsf = reinterpret_cast<float*>(smem + L.xsf);
   int* xs = reinterpret_cast<int*>(smem + L.xs);
   float* red = reinterpret_cast<float*>(smem + L.red);
-  // optional input RMSNorm factors 1 / sqrt(mean(x^2) + eps), one per row
-  // (in `red`, unused until the first group finishes)
-  float* nrm = red;
+  float* nss = reinterpret_cast<float*>(smem + L.nss);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers and branches
@@ -276,19 +276,28 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
       const int it = min(it0, witems - 1);
       const int mm = it / (nblk_w * 8), rb = rb0 + (it >> 3) % nblk_w, pt = it & 7;
       if (ops.norm_gain) {
+        // the gain here; the row's 1 / rms factors out of the dot products
+        // and is applied to the result
         const int k = min(32 * (2 * s_beg + rb) + 4 * pt, K - 4);
         const f32x4 gv = *reinterpret_cast<const f32x4*>(ops.norm_gain + k);
-        const float f = nrm[mm];
 #pragma unroll
-        for (int e = 0; e < 4; e++) xv[j][e] = xv[j][e] * (f * gv[e]);
+        for (int e = 0; e < 4; e++) xv[j][e] *= gv[e];
       }
       decompose_item(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
     }
   };
   const int gcols = (int)gridDim.x / ksplit;  // workgroups per slice
   const int gfirst = (int)blockIdx.x / ksplit;
-  // the norm factors over all of K (every workgroup reads the whole rows;
-  // they are small at m <= 16): M results, then the waves' partial sums
+  load_chunk(0);
+  // keep the scheduler from hoisting the weight loads above the activation
+  // loads: the decomposition below waits for the activations only
+  __builtin_amdgcn_sched_barrier(0);
+  load_batch(0, wbeg, min(gfirst, ngroups - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  // optional input RMSNorm: sums of squares of the rows over all of K (every
+  // workgroup reads the whole rows; they are small at m <= 16), a partial
+  // per wave in nss, read after the first group's barrier. These loads go out
+  // after the first weight batch: waiting for them costs no extra round trip.
   if (ops.norm_gain) {
     float ss[MT];
 #pragma unroll
@@ -304,25 +313,13 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     }
 #pragma unroll
     for (int mm = 0; mm < MT; mm++) {
+      if (mm >= M) break;
       float t = ss[mm];
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
-      if (lane == 0 && mm < M) nrm[16 + mm * WAVES + wave] = t;
+      if (lane == 0) nss[wave * MT + mm] = t;
     }
-    __syncthreads();
-    if (tid < M) {
-      float t = 0.0f;
-      for (int wv = 0; wv < WAVES; wv++) t += nrm[16 + tid * WAVES + wv];
-      nrm[tid] = 1.0f / sqrtf(t / (float)K + ops.norm_eps);
-    }
-    __syncthreads();
   }
-  load_chunk(0);
-  // keep the scheduler from hoisting the weight loads above the activation
-  // loads: the decomposition below waits for the activations only
-  __builtin_amdgcn_sched_barrier(0);
-  load_batch(0, wbeg, min(gfirst, ngroups - 1));
-  __builtin_amdgcn_sched_barrier(0);
   if (lane < 4) reinterpret_cast<uint32_t*>(smem + L.zero)[lane] = 0u;
   if (lane < nblk_w) {
     xsf[MT * L.xstr + rb0 + lane] = 0.0f;
@@ -336,9 +333,6 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // the wave reads back what its own lanes wrote
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  // the norm factors live in `red`, which the first finished group
-  // overwrites: every wave must be done with them first
-  if (ops.norm_gain) __syncthreads();
 
   float acc[MG];
 #pragma unroll
@@ -468,6 +462,12 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
         for (int mg = 0; mg < MG; mg++) {
           const int m = 4 * mg + g4;
           float out = v[mg];
+          if (ops.norm_gain && m < M) {
+            float t = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < WAVES; wv++) t += nss[wv * MT + m];
+            out *= 1.0f / sqrtf(t / (float)K + ops.norm_eps);
+          }
           if (ops.swiglu) {
             const float up = __shfl_down(out, 1, 64);
             out = out / (1.0f + expf(-out)) * up;
