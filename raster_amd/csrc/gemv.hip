@@ -502,12 +502,14 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
 constexpr int kBatch = 4;  // windows per batch
 
 // Split and grid for the decode kernel.
-//  * waves per workgroup and workgroups per CU, measured with cold weights on
-//    the 4096 x 4096 Q8 and 14336 x 4096 Q4 shapes at m = 1..16: with more
-//    16-row groups than CUs, 16 waves (m <= 4); with at most one group per CU,
-//    8 waves for m <= 2 and 16 for m = 3, 4; 8 waves for m > 4, one workgroup per CU (their register use
-//    leaves room for no more, and a second workgroup would only repeat the
-//    activation decomposition).
+//  * waves per workgroup, measured with cold weights on the 4096 x 4096 Q8
+//    and 14336 x 4096 Q4 shapes at m = 1..16 and warm on the decoder's
+//    K = 2048 / 5632 shapes at m = 1: 16 waves for m <= 4 when there are more
+//    16-row groups than CUs or m > 2, as long as every wave still gets a full
+//    batch of windows (K >= 4096); 8 waves otherwise (at K = 2048 a 16-wave
+//    workgroup leaves half of each batch empty: 7.1 against 5.0 us at
+//    6144 x 2048). One workgroup per CU: a second one only repeats the
+//    activation decomposition (measured no faster at 6144 and 11264 x 2048).
 //  * A workgroup holds the activations of its K-range in LDS; when the whole
 //    K does not fit, each 16-row group is cut into ksplit K-slices handled by
 //    different workgroups, whose partial sums the last one to finish adds up.
@@ -518,8 +520,8 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
   if (m < 1 || m > 16) return p;
   const int64_t nw = (k + 63) / 64, ngroups = npad / 16;
   p.mt = m <= 4 ? 4 : m <= 8 ? 8 : 16;
-  p.waves = p.mt == 4 && (ngroups > cu_count || m > 2) ? 16 : 8;
-  const int per_cu_max = p.mt == 4 ? 16 / p.waves : 1;
+  p.waves = p.mt == 4 && (ngroups > cu_count || m > 2) && nw >= 16 * kBatch ? 16 : 8;
+  const int per_cu_max = 1;
   int64_t ks = 1;
   while (SkinnyLds(p.mt, (int)(64 * ((nw + ks - 1) / ks)), p.waves).bytes > 163840) {
     if (ks >= nw) return p;
