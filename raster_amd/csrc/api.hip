@@ -99,7 +99,7 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   const size_t qbytes_rm = (size_t)out * (size_t)(in / 32) * code_bytes(format);
   const size_t sbytes_rm = (size_t)out * (size_t)(in / 32) * ssz;
   const size_t qbytes = (size_t)npad * (size_t)(in / 32) * code_bytes(format);
-  const size_t sbytes = (size_t)npad * (size_t)(in / 32) * ssz;
+  const size_t sbytes = (size_t)npad * (size_t)scale_nb8(in / 32) * ssz;
   const size_t total = align256(qbytes) + align256(sbytes);
   if (int s = set_device(c)) return s;
   void* base = nullptr;

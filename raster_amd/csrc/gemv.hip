@@ -118,6 +118,33 @@ __device__ __forceinline__ int sum8(int v) {
   return v + dpp_half_mirror(v);
 }
 
+// A row's 8 block scales of one scale batch (see scale_in_group).
+template <typename ST>
+struct ScaleBatch;
+template <>
+struct ScaleBatch<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float get(int j) const { return j < 4 ? a[j] : b[j - 4]; }
+};
+template <>
+struct ScaleBatch<uint16_t> {
+  u32x4 a;
+  __device__ __forceinline__ void load(const uint16_t* p) { a = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ float get(int j) const {
+    return f16_bits_to_f32((uint16_t)(a[j >> 1] >> (16 * (j & 1))));
+  }
+};
+
+// Windows per K-slice of the decode kernel: a whole number of batches of nb
+// windows (the host sizes LDS with the same count).
+__host__ __device__ __forceinline__ int slice_windows(int nw, int ksplit, int nb) {
+  return ((nw + ksplit - 1) / ksplit + nb - 1) / nb * nb;
+}
+
 // Decomposition of one item: 4 activations (row mm, elements k..k+3 of block
 // b) of the 8 lanes sharing a block. Writes both int8 levels to LDS and, from
 // the block's first lane, the block factor and level sum. All 8 lanes of a
@@ -172,7 +199,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // ---- this workgroup's K-slice: windows [s_beg, s_end), fixed for all its
   // groups. LDS holds the activations of the slice only (slice-relative).
   const int s = (int)blockIdx.x % ksplit;
-  const int sw = (nw + ksplit - 1) / ksplit;
+  const int sw = slice_windows(nw, ksplit, NB);
   const int s_beg = min(nw, s * sw), s_end = min(nw, s_beg + sw);
   const SkinnyLds L(MT, 64 * sw, WAVES);
   int8_t* lev = reinterpret_cast<int8_t*>(smem + L.lev);
@@ -203,8 +230,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
 #pragma unroll
   for (int mg = 0; mg < MG; mg++) xrow[mg] = (4 * mg + g4 < M ? 4 * mg + g4 : MT) * L.xstr;
 
-  // ---- wave's window range inside the slice (absolute window numbers)
-  const int per = (sw + WAVES - 1) / WAVES;
+  // ---- wave's window range inside the slice (absolute window numbers); a
+  // whole number of batches, so every batch starts on a scale batch
+  const int per = ((sw + WAVES - 1) / WAVES + NB - 1) / NB * NB;
   const int wbeg = min(s_end, s_beg + wave * per), wend = min(s_end, wbeg + per);
 
   // weight bytes per 16-row chunk, and this lane's offset inside a window
@@ -215,16 +243,18 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // which the zero A variants cancel)
   const int wmax = (nb - 1 - (g4 >> 1)) / 2;
 
+  static_assert(NB == 4, "a batch is one 8-block scale batch");
   u32x4 wq[2][NB];
-  float s0[2][NB], s1[2][NB];
-  // weight window w of group g: this lane's 16 (Q8) / 8 (Q4) code bytes and
-  // the row's two block scales. All loads are unconditional at clamped
-  // addresses and nothing here uses the loaded values: any condition or
-  // select on them would make the compiler wait for the loads right here and
-  // lose the overlap with the work that follows.
+  ScaleBatch<ST> sb[2];
+  const int nsb = scale_nb8(nb) / 8;  // scale batches per group
+  // weight window w of group g: this lane's 16 (Q8) / 8 (Q4) code bytes, and
+  // the row's 8 block scales of the batch in one or two 16-byte loads (zero
+  // past the last block). All loads are unconditional at clamped addresses
+  // and nothing here uses the loaded values: any condition or select on them
+  // would make the compiler wait for the loads right here and lose the
+  // overlap with the work that follows.
   auto load_batch = [&](int slot, int wb, int g) {
     const uint8_t* qg = q + (int64_t)g * nb * CB * 16;  // the group's chunks
-    const ST* sg = sc + (int64_t)g * nb * 16;           // and scales
 #pragma unroll
     for (int i = 0; i < NB; i++) {
       const int w = min(wb + i, nw - 1);
@@ -235,11 +265,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
         const u32x2 t = *reinterpret_cast<const u32x2*>(qg + off);
         wq[slot][i] = u32x4{t[0], t[1], 0u, 0u};
       }
-      s0[slot][i] = load_scale<ST>(sg, 32 * w + r);
-      // a missing second block (odd block count) rereads the first block's
-      // scale; compute_batch zeroes it
-      s1[slot][i] = load_scale<ST>(sg, 16 * min(2 * w + 1, nb - 1) + r);
     }
+    sb[slot].load(sc + scale_group(g, nb) + scale_in_group(8 * min(wb / NB, nsb - 1), r));
   };
 
   // ---- activation decomposition into LDS. A wave only ever reads the
@@ -396,8 +423,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
           t0 -= 8 * x0[i][mg];
           t1 -= 8 * x1[i][mg];
         }
-        acc[mg] = fmaf((float)t0, s0[slot][i] * f0[i][mg], acc[mg]);
-        acc[mg] = fmaf((float)t1, s1[slot][i] * f1[i][mg], acc[mg]);
+        acc[mg] = fmaf((float)t0, sb[slot].get(2 * i) * f0[i][mg], acc[mg]);
+        acc[mg] = fmaf((float)t1, sb[slot].get(2 * i + 1) * f1[i][mg], acc[mg]);
       }
   };
 
@@ -523,11 +550,11 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
   p.waves = p.mt == 4 && (ngroups > cu_count || m > 2) && nw >= 16 * kBatch ? 16 : 8;
   const int per_cu_max = 1;
   int64_t ks = 1;
-  while (SkinnyLds(p.mt, (int)(64 * ((nw + ks - 1) / ks)), p.waves).bytes > 163840) {
+  while (SkinnyLds(p.mt, 64 * slice_windows((int)nw, (int)ks, kBatch), p.waves).bytes > 163840) {
     if (ks >= nw) return p;
     ks++;
   }
-  const int lds = SkinnyLds(p.mt, (int)(64 * ((nw + ks - 1) / ks)), p.waves).bytes;
+  const int lds = SkinnyLds(p.mt, 64 * slice_windows((int)nw, (int)ks, kBatch), p.waves).bytes;
   const int per_cu = std::max(1, std::min(163840 / lds, per_cu_max));
   const int64_t gcols = std::min<int64_t>(ngroups, std::max<int64_t>(1, (int64_t)per_cu * cu_count / ks));
   if (gcols * ks > INT32_MAX) return p;

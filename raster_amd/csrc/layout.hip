@@ -25,10 +25,12 @@ __global__ __launch_bounds__(256) void chunk_scales_kernel(const ST* __restrict_
                                                           int64_t out, int64_t nb, int64_t n) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= n) return;
-  const int64_t chunk = e / 16, r = e % 16;
-  const int64_t g = chunk / nb, b = chunk % nb;
+  // e = scale_group(g) + scale_in_group(b, r): [g][batch][r][b % 8]
+  const int64_t per_group = scale_nb8(nb) * 16;
+  const int64_t g = e / per_group, t = e % per_group;
+  const int64_t b = (t / 128) * 8 + (t % 8), r = (t % 128) / 8;
   const int64_t row = 16 * g + r;
-  dst[e] = row < out ? src[row * nb + b] : ST(0);
+  dst[e] = row < out && b < nb ? src[row * nb + b] : ST(0);
 }
 
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
@@ -41,7 +43,7 @@ hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm,
     hipLaunchKernelGGL((chunk_codes_kernel<32>), gq, dim3(256), 0, stream, q_rm, q, out, nb, npieces);
   else
     hipLaunchKernelGGL((chunk_codes_kernel<16>), gq, dim3(256), 0, stream, q_rm, q, out, nb, npieces);
-  const int64_t ns = npad * nb;
+  const int64_t ns = npad * scale_nb8(nb);
   const dim3 gs((unsigned)((ns + 255) / 256));
   if (scale_dtype == RQ_F16)
     hipLaunchKernelGGL((chunk_scales_kernel<uint16_t>), gs, dim3(256), 0, stream,

@@ -55,9 +55,18 @@ template <int FMT>
 __host__ __device__ __forceinline__ int64_t code_off(int64_t row, int64_t b, int64_t nb) {
   return chunk_of(row, b, nb) * (16 * code_bytes(FMT)) + (row & 15) * code_bytes(FMT);
 }
+// Chunked scales: per 16-row group, the blocks in batches of 8 (4 windows of
+// 64 elements), each batch stored row by row: [batch][row 0..15][8 blocks],
+// the last batch zero-padded. A decode lane gets all of its row's scales for
+// a batch in one 16-byte (f16) or two (f32) loads.
+__host__ __device__ __forceinline__ int64_t scale_nb8(int64_t nb) { return (nb + 7) / 8 * 8; }
+// first scale of 16-row group g
+__host__ __device__ __forceinline__ int64_t scale_group(int64_t g, int64_t nb) { return g * scale_nb8(nb) * 16; }
+// offset of (block b, row r) inside its group
+__host__ __device__ __forceinline__ int scale_in_group(int b, int r) { return (b >> 3) * 128 + r * 8 + (b & 7); }
 // element offset of (row, block b) in the chunked scales
 __host__ __device__ __forceinline__ int64_t scale_off(int64_t row, int64_t b, int64_t nb) {
-  return chunk_of(row, b, nb) * 16 + (row & 15);
+  return scale_group(row >> 4, nb) + scale_in_group((int)b, (int)(row & 15));
 }
 
 // Fused decode options (rq_qmatmul_fused); all off when zero.
