@@ -428,7 +428,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(kern_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": read_traffic("gemm_bf16_q8_C2"),
                      "peak_from_device_props": round(peak_props, 1),
-                     "kernel": "rq::gemm_wl_kernel<0, float, 4, 4, 4>", "flop_per_launch": head.flops,
+                     "kernel": "rq::gemm_wl_kernel<0, float, 4, 4, 4, 2>", "flop_per_launch": head.flops,
                      "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
 
@@ -444,7 +444,7 @@ def main():
         result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["cold_GBs"], "peak": HBM_PEAK_GBS,
                                    "unit": "GB/s", "frac": gv["cold_frac_hbm"],
                                    "traffic": read_traffic("skinny_q8_f32_C1"),
-                                   "kernel": "rq::skinny_kernel<0, float, 0, 4, 16, 4>",
+                                   "kernel": "rq::skinny_kernel<0, float, 0, 4, 8, 4, 2>",
                                    "bytes_per_launch": gv["bytes"], "kernel_avg_us": gv["cold_us"]}
         log(f"gemv: cold {gv['cold_us']} us {gv['cold_GBs']} GB/s; warm {gv['warm_us']} us {gv['warm_GBs']} GB/s")
 

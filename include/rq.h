@@ -123,10 +123,10 @@ int rq_weight_info(rq_weight w, int* format, int64_t* out, int64_t* in, int* sca
  * npad = ceil(out/16)*16 and stored in 16-row x 32-element chunks, chunk
  * (r/16, b) at index (r/16)*(in/32) + b. A chunk holds the 16 rows' code blocks
  * back to back (16 x 32 B for Q8_0, 16 x 16 B for Q4_0, each block in Raster's
- * byte order). Scales: per 16-row group g, nb8 = ceil(in/256)*8 entries per
- * row, in batches of 8 blocks stored row by row: scale (row r, block b) of
- * group g at g*nb8*16 + (b/8)*128 + (r%16)*8 + b%8 (blocks past in/32 zero).
- * Padded rows are zero codes with zero scales. */
+ * byte order) and the scales chunk holds the 16 rows' scales of block b.
+ * Padded rows are zero codes with zero scales. The weight also holds a second
+ * copy of the scales, ordered for the decode kernel (per 16-row group, batches
+ * of 8 blocks stored row by row); device_bytes counts both. */
 int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
 
 /* ---- compute ---------------------------------------------------------------- */

@@ -99,8 +99,9 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   const size_t qbytes_rm = (size_t)out * (size_t)(in / 32) * code_bytes(format);
   const size_t sbytes_rm = (size_t)out * (size_t)(in / 32) * ssz;
   const size_t qbytes = (size_t)npad * (size_t)(in / 32) * code_bytes(format);
-  const size_t sbytes = (size_t)npad * (size_t)scale_nb8(in / 32) * ssz;
-  const size_t total = align256(qbytes) + align256(sbytes);
+  const size_t sbytes = (size_t)npad * (size_t)(in / 32) * ssz;
+  const size_t sbytes_rb = (size_t)npad * (size_t)scale_nb8(in / 32) * ssz;
+  const size_t total = align256(qbytes) + align256(sbytes) + align256(sbytes_rb);
   if (int s = set_device(c)) return s;
   void* base = nullptr;
   hipError_t e = hipMalloc(&base, total);
@@ -131,13 +132,15 @@ static int make_weight(Ctx* c, int format, int scale_dtype, int64_t out, int64_t
   w->base = base;
   w->q = static_cast<uint8_t*>(base);
   w->scales = static_cast<uint8_t*>(base) + align256(qbytes);
+  w->scales_rb = static_cast<uint8_t*>(base) + align256(qbytes) + align256(sbytes);
   w->bytes = total;
   w->ctx = c;
   uint8_t* q_rm = static_cast<uint8_t*>(stage);
   uint8_t* s_rm = q_rm + align256(qbytes_rm);
   e = hipMemcpy(q_rm, qhost, qbytes_rm, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(s_rm, shost, sbytes_rm, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = launch_chunk_weight(format, scale_dtype, q_rm, s_rm, out, in, npad, w->q, w->scales, nullptr);
+  if (e == hipSuccess) e = launch_chunk_weight(format, scale_dtype, q_rm, s_rm, out, in, npad, w->q, w->scales, w->scales_rb,
+                                               nullptr);
   if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
   (void)hipFree(stage);
   if (e != hipSuccess) {
@@ -613,6 +616,7 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
   MatmulArgs a;
   a.q = w.q;
   a.scales = w.scales;
+  a.scales_rb = w.scales_rb;
   a.scale_dtype = w.scale_dtype;
   a.format = w.format;
   a.x = x;

@@ -45,12 +45,12 @@ struct WCodes {
 
 template <int FMT, typename ST>
 __device__ __forceinline__ void load_wcodes(WCodes& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                            int64_t chunk, int64_t soff, int fr, int fg) {
+                                            int64_t chunk, int fr, int fg) {
   if (FMT == RQ_Q8_0)
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
   else
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + fr * 16 + 8 * (fg & 1));
-  c.s = load_scale<ST>(sc, soff);
+  c.s = load_scale<ST>(sc, chunk * 16 + fr);
 }
 
 // Dequantized fragment (8 bf16): exact f32 scale * code, one RNE rounding to bf16.
@@ -147,13 +147,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   }
   // this wave's weight chunks (16-row groups, clamped to the padded rows)
   const int g_last = npad / 16 - 1;
-  int64_t wchunk[NTW], wsg[NTW];
+  int64_t wchunk[NTW];
 #pragma unroll
-  for (int j = 0; j < NTW; j++) {
-    const int g = min(n0 / 16 + wave * NTW + j, g_last);
-    wchunk[j] = (int64_t)g * nkb;
-    wsg[j] = scale_group(g, nkb);
-  }
+  for (int j = 0; j < NTW; j++) wchunk[j] = (int64_t)min(n0 / 16 + wave * NTW + j, g_last) * nkb;
 
   f32x4 acc[MT][NTW];
 #pragma unroll
@@ -195,8 +191,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   do {                                                                                    \
     const int kk_ = min((kb_), nkb - 1);                                                  \
     _Pragma("unroll") for (int j = 0; j < NTW; j++)                                       \
-        load_wcodes<FMT, ST>(wc[slot][j], q, sc, wchunk[j] + kk_,                         \
-                             wsg[j] + scale_in_group(kk_, fr), fr, fg);                   \
+        load_wcodes<FMT, ST>(wc[slot][j], q, sc, wchunk[j] + kk_, fr, fg);                \
   } while (0)
 
   // prologue: LDS buffers 0, 1 hold steps 0, 1; areg[s % 3] holds step s
@@ -339,13 +334,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   for (int i = 0; i < MT; i++) asrc[i] = xf + (int64_t)min(m0 / 16 + i, mt_last) * nkb * 512 + lane * 8;
   // weight fragments this wave dequantizes: c = wave + 4 j < NT
   const int g_last = npad / 16 - 1;
-  int64_t wchunk[CW], wsg[CW];
+  int64_t wchunk[CW];
 #pragma unroll
-  for (int j = 0; j < CW; j++) {
-    const int g = min(n0 / 16 + min(wave + 4 * j, NT - 1), g_last);
-    wchunk[j] = (int64_t)g * nkb;
-    wsg[j] = scale_group(g, nkb);
-  }
+  for (int j = 0; j < CW; j++) wchunk[j] = (int64_t)min(n0 / 16 + min(wave + 4 * j, NT - 1), g_last) * nkb;
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -367,8 +358,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   do {                                                                                            \
     const int kk_ = min((kb_), nkb - 1);                                                          \
     _Pragma("unroll") for (int j = 0; j < CW; j++)                                                \
-        load_wcodes<FMT, ST>(wc[(kb_) % R][j], q, sc, wchunk[j] + kk_,                            \
-                             wsg[j] + scale_in_group(kk_, fr), fr, fg);                           \
+        load_wcodes<FMT, ST>(wc[(kb_) % R][j], q, sc, wchunk[j] + kk_, fr, fg);                   \
   } while (0)
 #define WL_DEQUANT(kb_)                                                                           \
   do {                                                                                            \
@@ -428,8 +418,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   do {                                                                                            \
     const int kk_ = min((kb_), nkb - 1);                                                          \
     _Pragma("unroll") for (int j = 0; j < CW; j++)                                                \
-        load_wcodes<FMT, ST>(wc[(u_) % R][j], q, sc, wchunk[j] + kk_,                             \
-                             wsg[j] + scale_in_group(kk_, fr), fr, fg);                           \
+        load_wcodes<FMT, ST>(wc[(u_) % R][j], q, sc, wchunk[j] + kk_, fr, fg);                    \
   } while (0)
 #define WL_READ_B_U(u_) WL_READ_B(u_)
 #define WL_DEQUANT_U(u_) WL_DEQUANT(u_)

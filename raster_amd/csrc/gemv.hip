@@ -118,7 +118,7 @@ __device__ __forceinline__ int sum8(int v) {
   return v + dpp_half_mirror(v);
 }
 
-// A row's 8 block scales of one scale batch (see scale_in_group).
+// A row's 8 block scales of one batch of the row-batched scales.
 template <typename ST>
 struct ScaleBatch;
 template <>
@@ -186,7 +186,7 @@ __device__ __forceinline__ void decompose_item(const float (&v)[4], bool valid, 
 
 }  // namespace
 
-template <int FMT, typename ST, int XT, int MT, int WAVES, int NB>
+template <int FMT, typename ST, int XT, int MT, int WAVES, int NB, int RING>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                            const void* __restrict__ x, void* __restrict__ y, int M,
                                                            int K, int N, int npad, int y_dtype, int ksplit,
@@ -244,8 +244,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   const int wmax = (nb - 1 - (g4 >> 1)) / 2;
 
   static_assert(NB == 4, "a batch is one 8-block scale batch");
-  u32x4 wq[2][NB];
-  ScaleBatch<ST> sb[2];
+  u32x4 wq[RING][NB];
+  ScaleBatch<ST> sb[RING];
   const int nsb = scale_nb8(nb) / 8;  // scale batches per group
   // weight window w of group g: this lane's 16 (Q8) / 8 (Q4) code bytes, and
   // the row's 8 block scales of the batch in one or two 16-byte loads (zero
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
         wq[slot][i] = u32x4{t[0], t[1], 0u, 0u};
       }
     }
-    sb[slot].load(sc + scale_group(g, nb) + scale_in_group(8 * min(wb / NB, nsb - 1), r));
+    sb[slot].load(sc + scale_rb_group(g, nb) + scale_rb_in_group(8 * min(wb / NB, nsb - 1), r));
   };
 
   // ---- activation decomposition into LDS. A wave only ever reads the
@@ -514,19 +514,27 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     }
     __syncthreads();
   };
-  // task 0's batch went out with the prologue (slot 0)
-  for (int t = 0; t < ntask; t += 2) {
-    task_load(1, t + 1);
-    compute_batch(0, wbeg + (t % nbg) * NB);
-    if (t % nbg == nbg - 1) finish_group(t);
-    if (t + 1 >= ntask) break;
-    task_load(0, t + 2);
-    compute_batch(1, wbeg + ((t + 1) % nbg) * NB);
-    if ((t + 1) % nbg == nbg - 1) finish_group(t + 1);
+  // a ring of RING batch slots: task t computes from slot t % RING while the
+  // loads of tasks t + 1 .. t + RING - 1 are in flight. Task 0's batch went
+  // out with the prologue; tasks 1 .. RING - 2 go out now.
+#pragma unroll
+  for (int u = 1; u < RING - 1; u++) task_load(u, u);
+  for (int t0 = 0; t0 < ntask; t0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; u++) {
+      const int t = t0 + u;
+      if (t >= ntask) break;
+      task_load((u + RING - 1) % RING, t + RING - 1);
+      compute_batch(u, wbeg + (t % nbg) * NB);
+      if (t % nbg == nbg - 1) finish_group(t);
+    }
   }
 }
 
 constexpr int kBatch = 4;  // windows per batch
+// batch slots in flight per wave
+template <int FMT>
+constexpr int kRing = 2;
 
 // Split and grid for the decode kernel.
 //  * waves per workgroup, measured with cold weights on the 4096 x 4096 Q8
@@ -569,7 +577,7 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
 
 template <int FMT, typename ST, int XT, int MT, int WAVES>
 static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
-  auto kernel = &skinny_kernel<FMT, ST, XT, MT, WAVES, kBatch>;
+  auto kernel = &skinny_kernel<FMT, ST, XT, MT, WAVES, kBatch, kRing<FMT>>;
   // dynamic LDS above 64 KB must be allowed once per kernel and device (bit d
   // of `attr_set`; setting it twice from racing threads is harmless)
   static std::atomic<uint64_t> attr_set{0};
@@ -583,7 +591,7 @@ static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(64 * WAVES), (unsigned)p.lds_bytes, a.stream,
-                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m,
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales_rb), a.x, a.y, (int)a.m,
                         (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.cnt, a.ops);
   return hipGetLastError();
 }

@@ -42,7 +42,8 @@ struct Weight {
   int64_t out, in, npad;
   void* base;       // device allocation
   uint8_t* q;       // chunked codes / packed nibbles
-  void* scales;     // chunked scales
+  void* scales;     // chunked scales, block-major (prefill kernels, dequant)
+  void* scales_rb;  // the same scales row-batched (decode kernel)
   size_t bytes;
   struct Ctx* ctx;
 };
@@ -55,19 +56,22 @@ template <int FMT>
 __host__ __device__ __forceinline__ int64_t code_off(int64_t row, int64_t b, int64_t nb) {
   return chunk_of(row, b, nb) * (16 * code_bytes(FMT)) + (row & 15) * code_bytes(FMT);
 }
-// Chunked scales: per 16-row group, the blocks in batches of 8 (4 windows of
-// 64 elements), each batch stored row by row: [batch][row 0..15][8 blocks],
-// the last batch zero-padded. A decode lane gets all of its row's scales for
-// a batch in one 16-byte (f16) or two (f32) loads.
-__host__ __device__ __forceinline__ int64_t scale_nb8(int64_t nb) { return (nb + 7) / 8 * 8; }
-// first scale of 16-row group g
-__host__ __device__ __forceinline__ int64_t scale_group(int64_t g, int64_t nb) { return g * scale_nb8(nb) * 16; }
-// offset of (block b, row r) inside its group
-__host__ __device__ __forceinline__ int scale_in_group(int b, int r) { return (b >> 3) * 128 + r * 8 + (b & 7); }
-// element offset of (row, block b) in the chunked scales
+// Chunked scales are kept in two orders, each read by the kernels it suits:
+//  * block-major: chunk (g, b) holds the 16 rows' scales of block b. A
+//    prefill step reads one block of 16 rows: 64 contiguous bytes.
+//  * row-batched: per 16-row group, the blocks in batches of 8 (4 windows of
+//    64 elements), each batch stored row by row, [batch][row 0..15][8 blocks],
+//    the last batch zero-padded. A decode lane gets all of its row's scales
+//    for a batch in one 16-byte (f16) or two (f32) loads.
+// element offset of (row, block b) in the block-major scales
 __host__ __device__ __forceinline__ int64_t scale_off(int64_t row, int64_t b, int64_t nb) {
-  return scale_group(row >> 4, nb) + scale_in_group((int)b, (int)(row & 15));
+  return chunk_of(row, b, nb) * 16 + (row & 15);
 }
+__host__ __device__ __forceinline__ int64_t scale_nb8(int64_t nb) { return (nb + 7) / 8 * 8; }
+// first row-batched scale of 16-row group g
+__host__ __device__ __forceinline__ int64_t scale_rb_group(int64_t g, int64_t nb) { return g * scale_nb8(nb) * 16; }
+// offset of (block b, row r) inside its group, row-batched
+__host__ __device__ __forceinline__ int scale_rb_in_group(int b, int r) { return (b >> 3) * 128 + r * 8 + (b & 7); }
 
 // Fused decode options (rq_qmatmul_fused); all off when zero.
 struct DecodeOps {
@@ -80,7 +84,8 @@ struct DecodeOps {
 // Launch descriptor for the matmul kernels.
 struct MatmulArgs {
   const uint8_t* q;
-  const void* scales;
+  const void* scales;     // block-major
+  const void* scales_rb;  // row-batched
   int scale_dtype;
   int format;
   const void* x;
@@ -124,7 +129,7 @@ hipError_t launch_decode_attention(const float* q, const float* k, const float* 
                                    double scale, float* out, hipStream_t stream);
 // Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
-                               int64_t in, int64_t npad, uint8_t* q, void* s, hipStream_t stream);
+                               int64_t in, int64_t npad, uint8_t* q, void* s, void* s_rb, hipStream_t stream);
 
 // ---- device helpers shared by every kernel that decodes weights -----------
 
