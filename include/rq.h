@@ -76,9 +76,11 @@ int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz
  * whose microbench (raster/runtime/microbench.clj:20-60) times whole calls;
  * this one separates the main kernel of a call (the MFMA GEMM or the decode
  * kernel) from the small activation-packing pass of the bf16 GEMM.
- * While enabled, every rq_qmatmul on this context launches its main kernel
- * with a pair of HIP events that take that dispatch's own start and end
- * timestamps (hipExtLaunchKernel; not on a stream that is being captured).
+ * While enabled, every rq_qmatmul on this context records a pair of HIP
+ * events around its main kernel (hipExtLaunchKernel; not on a stream that is
+ * being captured): for the bf16 prefill GEMM, the end of the packing pass
+ * and the end of the GEMM, which follows it directly; for the other kernels,
+ * the dispatch's own start and end.
  * rq_ctx_kernel_time waits for the pending pairs, returns their summed
  * duration and count, and clears them. Disabling frees the events. */
 int rq_ctx_set_kernel_timing(rq_ctx ctx, int enable);

@@ -318,7 +318,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   static_assert(R >= 4 && R % L == 0 && R % 2 == 0, "ring depth: whole turns of the LDS and fragment rings");
   __shared__ __attribute__((aligned(16))) bf16x8 Bs[L][NT][64];
 
-  const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
+  // Tile order: column tile major, row tiles (which share the column tile's
+  // weights) consecutive. Workgroups are dealt to the 8 XCDs round-robin by
+  // id, so ids are remapped to give each XCD a contiguous run of that order:
+  // the row tiles of a column tile then meet in one XCD's L2 instead of
+  // fetching the weights from HBM once per XCD.
+  const int nblk = (int)gridDim.x, bid = (int)blockIdx.x;
+  const int xcd = bid & 7, per = nblk >> 3, rem = nblk & 7;
+  const int tord = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
+  const int tm = tord % tiles_m, tn = tord / tiles_m;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
@@ -475,10 +483,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   }
 }
 
+// Kernel timing (a.ev_main set): the packing pass's end and the GEMM's end.
+// A start event would put an extra packet, and an idle gap of a few
+// microseconds, in front of the GEMM; the GEMM follows the packing pass
+// directly, so its duration is the span between the two end events.
 hipError_t launch_pack_x(const MatmulArgs& a) {
   const int64_t pack_blocks = (a.m + 15) / 16 * ((a.k / 32 + 3) / 4);
-  hipLaunchKernelGGL(pack_x_kernel, dim3((unsigned)pack_blocks), dim3(256), 0, a.stream,
-                     static_cast<const uint16_t*>(a.x), static_cast<uint16_t*>(a.scratch), (int)a.m, (int)a.k);
+  hipExtLaunchKernelGGL(pack_x_kernel, dim3((unsigned)pack_blocks), dim3(256), 0, a.stream, nullptr, a.ev_main[0], 0,
+                        static_cast<const uint16_t*>(a.x), static_cast<uint16_t*>(a.scratch), (int)a.m, (int)a.k);
   return hipGetLastError();
 }
 
@@ -488,7 +500,7 @@ static hipError_t launch_t(const MatmulArgs& a) {
   const int tiles_m = (int)((a.m + BM - 1) / BM), tiles_n = (int)((a.n + BN - 1) / BN);
   if (hipError_t e = launch_pack_x(a)) return e;
   dim3 grid((unsigned)(tiles_m * tiles_n));
-  hipExtLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, MT, NTW>), grid, dim3(256), 0, a.stream, a.ev_main[0],
+  hipExtLaunchKernelGGL((gemm_bf16_kernel<FMT, ST, MT, NTW>), grid, dim3(256), 0, a.stream, nullptr,
                         a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m);
@@ -501,7 +513,7 @@ static hipError_t launch_wl(const MatmulArgs& a) {
   const int tiles_n = (int)((a.npad / 16 + NT - 1) / NT);
   if (hipError_t e = launch_pack_x(a)) return e;
   hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R, WPE>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
-                        a.stream, a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m);
   return hipGetLastError();
