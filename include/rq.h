@@ -176,13 +176,22 @@ int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int
  *    (residual-add!, raster/dl/nn.clj:217-219);
  *  - swiglu: weight rows 2i and 2i+1 are a gate row and an up row; y[m, i] =
  *    silu(z[m, 2i]) * z[m, 2i+1] for the product z, so y has out/2 columns
- *    (silu-mul!, raster/dl/nn.clj:200-203). Not combined with residual.
+ *    (silu-mul!, raster/dl/nn.clj:200-203). Not combined with residual;
+ *  - act_i8: the activations (after the norm's gain) are quantized in the
+ *    kernel to Raster's int8 blocks exactly as rq_quantize_act_i8 does and
+ *    multiplied as rq_qmatmul_i8 does, instead of the default 16-bit block
+ *    fixed point: Raster's int-activation numerics (qmatmul-q4-composable,
+ *    raster/quant/kernels.clj:140-184). Without a norm the result is bitwise
+ *    that of rq_quantize_act_i8 followed by rq_qmatmul_i8. With a norm the
+ *    row's 1/rms factor is applied to the result (it factors out of the
+ *    dot products), so the blocks quantized are those of x * gain.
  * The epilogue math runs in f32. */
 typedef struct {
   const float* norm_gain;
   float norm_eps;
   const void* residual;
   int swiglu;
+  int act_i8;
 } rq_fused_ops;
 
 /* rq_qmatmul with fused options, for m <= 16 (the decode kernel); larger m
@@ -190,6 +199,27 @@ typedef struct {
  * replaces the op sequences named in rq_fused_ops around a qlinear. */
 int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                      const rq_fused_ops* ops, void* stream);
+
+/* Raster's activation quantizer on the device (quantize-act-i8,
+ * raster/compiler/backend/cpu/quant.clj:282-305,399-415): per row of x
+ * f32[m*in] and 32-element block b, d = max|x| / 127 (in double), q =
+ * clamp(Math/round(x / d), -127, 127) (ties toward +infinity, 0 when d == 0),
+ * xq int8[m*in], xs f32[m*in/32] = (float) d, xsum int32[m*in/32] = sum q
+ * (xsum may be NULL). Bitwise equal to the reference on finite input; its
+ * int8 bytes are also the packed words of quant-act-i8-rows-gpu!
+ * (raster/quant/kernels_k.clj:326-355). x 16-byte and xq 4-byte aligned. */
+int rq_quantize_act_i8(rq_ctx ctx, const float* x, int64_t m, int64_t in, int8_t* xq, float* xs, int32_t* xsum,
+                       void* stream);
+
+/* y[m, out] = sum_b xs[m, b] * scale[o, b] * (dot_b(codes[o], xq[m]) [- 8 *
+ * xsum[m, b] for Q4_0]) with int8 activations from rq_quantize_act_i8: the
+ * integer block dots are exact, the block terms are summed in f32 (Raster sums
+ * in double). Q4_0 needs xsum (qmatmul-q4-composable,
+ * raster/quant/kernels.clj:140-184); Q8_0 ignores it (qmatmul-i8-gemm!,
+ * raster/quant/kernels_k.clj:357-370). m <= 16 runs the decode kernel, larger
+ * m an int8-MFMA GEMM. xq 16-byte aligned. */
+int rq_qmatmul_i8(rq_ctx ctx, rq_weight w, const int8_t* xq, const float* xs, const int32_t* xsum, void* y,
+                  int y_dtype, int64_t m, void* stream);
 
 /* One decode step of RoPE, KV-cache append and single-query attention, the
  * glue between a decoder layer's q/k/v and o linears, all on the device:

@@ -43,6 +43,8 @@ SIGNATURES = {
     "rq_weight_device_ptrs": ([_p, C.POINTER(_p), C.POINTER(_p)], _i),
     "rq_qmatmul": ([_p, _p, _p, _i, _p, _i, _i64, _p], _i),
     "rq_qmatmul_fused": ([_p, _p, _p, _i, _p, _i, _i64, _p, _p], _i),
+    "rq_quantize_act_i8": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
+    "rq_qmatmul_i8": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
     "rq_decode_attention": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, C.c_double, C.c_double, _p, _p], _i),
     "rq_dequant": ([_p, _p, _p, _p], _i),
     "rq_qlinear_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
@@ -52,7 +54,7 @@ SIGNATURES = {
 class FusedOps(C.Structure):
     """rq_fused_ops of include/rq.h."""
 
-    _fields_ = [("norm_gain", _p), ("norm_eps", C.c_float), ("residual", _p), ("swiglu", _i)]
+    _fields_ = [("norm_gain", _p), ("norm_eps", C.c_float), ("residual", _p), ("swiglu", _i), ("act_i8", _i)]
 
 
 class RqError(RuntimeError):

@@ -586,6 +586,9 @@ static int lookup(rq_ctx h, rq_weight wh, Ctx** c, Weight* copy) {
 namespace rq {
 
 // rq_qmatmul / rq_qmatmul_fused; ops == nullptr is the plain product.
+static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
+                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream);
+
 static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                         const rq_fused_ops* ops, void* stream) {
   Ctx* c;
@@ -610,8 +613,20 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
     if (ops->swiglu && ops->residual) return fail(RQ_ERR_SHAPE, "swiglu and residual cannot be combined");
     if (ops->residual && ((uintptr_t)ops->residual & (y_dtype == RQ_F32 ? 3 : 1)) != 0)
       return fail(RQ_ERR_SHAPE, "residual misaligned");
-    dops = {ops->norm_gain, ops->norm_eps, ops->residual, ops->swiglu ? 1 : 0};
+    dops.norm_gain = ops->norm_gain;
+    dops.norm_eps = ops->norm_eps;
+    dops.residual = ops->residual;
+    dops.swiglu = ops->swiglu ? 1 : 0;
+    dops.act_i8 = ops->act_i8 ? 1 : 0;
   }
+  return run_matmul(c, w, plan, x, x_dtype, y, y_dtype, m, dops, (hipStream_t)stream);
+}
+
+// Launches the matmul of a validated call: the decode kernel when the plan
+// allows it, else the GEMM for the activation dtype; per-stream scratch and
+// kernel timing around it.
+static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
+                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream) {
   if (int s = set_device(c)) return s;
   MatmulArgs a;
   a.q = w.q;
@@ -627,7 +642,7 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
   a.k = w.in;
   a.n = w.out;
   a.npad = w.npad;
-  a.stream = (hipStream_t)stream;
+  a.stream = stream;
   a.scratch = nullptr;
   a.part = nullptr;
   a.cnt = nullptr;
@@ -643,6 +658,7 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
   a.ev_main[0] = ev.first;
   a.ev_main[1] = ev.second;
   hipError_t e = plan.ok              ? launch_gemv(a, plan)
+                 : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);
@@ -662,6 +678,45 @@ int rq_qmatmul_fused(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y
                      const rq_fused_ops* ops, void* stream) {
   if (!ops) return fail(RQ_ERR_NULL, "ops is NULL");
   return qmatmul_impl(h, wh, x, x_dtype, y, y_dtype, m, ops, stream);
+}
+
+int rq_quantize_act_i8(rq_ctx h, const float* x, int64_t m, int64_t in, int8_t* xq, float* xs, int32_t* xsum,
+                       void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (m < 0 || in < 0) return fail(RQ_ERR_SHAPE, "negative dimension");
+  if (in % 32 != 0) return fail(RQ_ERR_SHAPE, "in must be a multiple of 32");
+  if (m == 0 || in == 0) return RQ_OK;
+  if (m > ((int64_t)1 << 40) / in) return fail(RQ_ERR_SHAPE, "m * in too large");
+  if (!x || !xq || !xs) return fail(RQ_ERR_NULL, "x, xq or xs is NULL");
+  if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
+  if (((uintptr_t)xq & 3) != 0 || ((uintptr_t)xs & 3) != 0 || ((uintptr_t)xsum & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "xq, xs and xsum must be 4-byte aligned");
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_quantize_act_i8(x, m, in, xq, xs, xsum, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantizer launch");
+  return RQ_OK;
+}
+
+int rq_qmatmul_i8(rq_ctx h, rq_weight wh, const int8_t* xq, const float* xs, const int32_t* xsum, void* y,
+                  int y_dtype, int64_t m, void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
+  if (!xq || !xs || !y) return fail(RQ_ERR_NULL, "xq, xs or y is NULL");
+  if (w.format == RQ_Q4_0 && !xsum) return fail(RQ_ERR_NULL, "Q4_0 needs xsum (the zero-point fold)");
+  if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
+  if (((uintptr_t)xq & 15) != 0) return fail(RQ_ERR_SHAPE, "xq must be 16-byte aligned");
+  if (((uintptr_t)xs & 3) != 0 || ((uintptr_t)xsum & 3) != 0) return fail(RQ_ERR_SHAPE, "xs / xsum misaligned");
+  if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
+  DecodeOps dops{};
+  dops.act_scale = xs;
+  dops.act_sum = w.format == RQ_Q4_0 ? xsum : nullptr;
+  return run_matmul(c, w, plan, xq, kXtI8, y, y_dtype, m, dops, (hipStream_t)stream);
 }
 
 int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v, float* kcache, float* vcache,

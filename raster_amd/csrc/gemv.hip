@@ -81,6 +81,10 @@ template <int XT>
 __device__ __forceinline__ void load_x4(const void* x, int64_t off, bool ok, float (&v)[4]) {
   if (!ok) {
     v[0] = v[1] = v[2] = v[3] = 0.0f;
+  } else if (XT == kXtI8) {
+    // four int8 codes, carried as the bits of v[0]
+    v[0] = __uint_as_float(*reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(x) + off));
+    v[1] = v[2] = v[3] = 0.0f;
   } else if (XT == RQ_F32) {
     const f32x4 t = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + off);
     v[0] = t[0];
@@ -182,6 +186,43 @@ __device__ __forceinline__ void decompose_item(const float (&v)[4], bool valid, 
       xs[mm * xstr + b] = sum;
     }
   }
+}
+
+// Int8 activation blocks (Raster's quantize-act-i8 format): level 0 is zero
+// and level 1 holds the codes, so 256 C0 + C1 is the exact int8 block dot;
+// the block factor is the activation scale xs and the level sum xsum (the
+// Q4_0 zero-point fold of qmatmul-q4-composable).
+__device__ __forceinline__ void store_int8_item(uint32_t word, bool valid, int mm, int b, int part, int k, int lstr,
+                                                int xstr, int8_t* __restrict__ lev, float* __restrict__ xsf,
+                                                int* __restrict__ xs, float scale, int sum) {
+  if (valid) {
+    *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 0) * lstr + k) = 0u;
+    *reinterpret_cast<uint32_t*>(lev + (mm * 2 + 1) * lstr + k) = word;
+    if (part == 0) {
+      xsf[mm * xstr + b] = scale;
+      xs[mm * xstr + b] = sum;
+    }
+  }
+}
+
+// quantize-act-i8 of one item inside the kernel (the 8 lanes of a block run
+// it together): the same math as quantize_act_i8_kernel, so the codes, scale
+// and sum are bitwise those of rq_quantize_act_i8.
+__device__ __forceinline__ void quantize_item_a5(const float (&v)[4], bool valid, int mm, int b, int part, int k,
+                                                 int lstr, int xstr, int8_t* __restrict__ lev,
+                                                 float* __restrict__ xsf, int* __restrict__ xs) {
+  const float amax = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  const double d = (double)amax / 127.0;
+  const double id = d == 0.0 ? 0.0 : 1.0 / d;
+  uint32_t word = 0u;
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int q = java_round_clamp127((double)v[i] * id);
+    word |= (uint32_t)(q & 0xFF) << (8 * i);
+    s += q;
+  }
+  store_int8_item(word, valid, mm, b, part, k, lstr, xstr, lev, xsf, xs, (float)d, sum8(s));
 }
 
 }  // namespace
@@ -293,6 +334,12 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
       // columns past K (the missing half of a last window) reread in-row data
       const int k = min(32 * (2 * s_beg + rb) + 4 * (it & 7), K - 4);
       load_x4<XT>(x, (int64_t)mm * K + k, true, xv[j]);
+      if (XT == kXtI8) {
+        // the block's scale and level sum travel with its codes
+        const int64_t bq = (int64_t)mm * nb + min(2 * s_beg + rb, nb - 1);
+        xv[j][1] = ops.act_scale[bq];
+        xv[j][2] = __int_as_float(ops.act_sum ? (int)ops.act_sum[bq] : 0);
+      }
     }
   };
   auto decompose_chunk = [&](int base) {
@@ -302,7 +349,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
       const int it0 = base + lane + 64 * j;
       const int it = min(it0, witems - 1);
       const int mm = it / (nblk_w * 8), rb = rb0 + (it >> 3) % nblk_w, pt = it & 7;
-      if (ops.norm_gain) {
+      if (XT != kXtI8 && ops.norm_gain) {
         // the gain here; the row's 1 / rms factors out of the dot products
         // and is applied to the result
         const int k = min(32 * (2 * s_beg + rb) + 4 * pt, K - 4);
@@ -310,7 +357,14 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
 #pragma unroll
         for (int e = 0; e < 4; e++) xv[j][e] *= gv[e];
       }
-      decompose_item(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
+      if (XT == kXtI8) {
+        store_int8_item(__float_as_uint(xv[j][0]), it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev,
+                        xsf, xs, xv[j][1], __float_as_int(xv[j][2]));
+      } else if (ops.act_i8) {
+        quantize_item_a5(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
+      } else {
+        decompose_item(xv[j], it0 < witems, mm, rb, pt, 32 * rb + 4 * pt, L.lstr, L.xstr, lev, xsf, xs);
+      }
     }
   };
   const int gcols = (int)gridDim.x / ksplit;  // workgroups per slice
@@ -325,7 +379,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   // workgroup reads the whole rows; they are small at m <= 16), a partial
   // per wave in nss, read after the first group's barrier. These loads go out
   // after the first weight batch: waiting for them costs no extra round trip.
-  if (ops.norm_gain) {
+  if (XT != kXtI8 && ops.norm_gain) {
     float ss[MT];
 #pragma unroll
     for (int mm = 0; mm < MT; mm++) ss[mm] = 0.0f;
@@ -605,6 +659,7 @@ static hipError_t launch_m(const MatmulArgs& a, const DecodePlan& p) {
 
 template <int FMT, typename ST>
 static hipError_t launch_x(const MatmulArgs& a, const DecodePlan& p) {
+  if (a.x_dtype == kXtI8) return launch_m<FMT, ST, kXtI8>(a, p);
   return a.x_dtype == RQ_F32 ? launch_m<FMT, ST, RQ_F32>(a, p) : launch_m<FMT, ST, RQ_BF16>(a, p);
 }
 

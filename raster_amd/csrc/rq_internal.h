@@ -79,7 +79,14 @@ struct DecodeOps {
   float norm_eps;
   const void* residual;    // y = residual + product (y's dtype and shape)
   int swiglu;              // y[m][i] = silu(z[m][2i]) * z[m][2i+1]; y has n / 2 columns
+  int act_i8;              // quantize x to Raster's int8 blocks in the kernel
+  const float* act_scale;  // int8 input (x is int8): xs[m][b]
+  const int32_t* act_sum;  // int8 input: xsum[m][b] (Q4_0)
 };
+
+// Activation dtype code of the decode kernel for int8 input quantized
+// beforehand (not a public rq_dtype).
+constexpr int kXtI8 = 3;
 
 // Launch descriptor for the matmul kernels.
 struct MatmulArgs {
@@ -98,7 +105,7 @@ struct MatmulArgs {
   void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
   float* part;      // decode with K-split: partial sums, DecodePlan::part_bytes
   int* cnt;         // decode with K-split: one zeroed counter per 16-row group
-  DecodeOps ops = {nullptr, 0.0f, nullptr, 0};
+  DecodeOps ops = {nullptr, 0.0f, nullptr, 0, 0, nullptr, nullptr};
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
   // and these events take that dispatch's own start and end timestamps
   hipEvent_t ev_main[2] = {nullptr, nullptr};
@@ -119,9 +126,13 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
+// int8 activations (x_dtype kXtI8, scales / sums in a.ops), m > 16 (gemm_i8.hip)
+hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).
 hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
+hipError_t launch_quantize_act_i8(const float* x, int64_t m, int64_t in, int8_t* xq, float* xs, int32_t* xsum,
+                                  hipStream_t stream);
 // RoPE + KV append + single-query attention for one decode step (attention.hip).
 size_t decode_attention_lds(int64_t pos, int64_t head_dim);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
@@ -159,6 +170,17 @@ __device__ __forceinline__ float load_scale<float>(const float* s, int64_t i) { 
 template <>
 __device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* s, int64_t i) {
   return f16_bits_to_f32(s[i]);
+}
+
+// Math/round of a double clamped to [-127, 127] (the int8 quantizers'
+// rounding, raster/compiler/backend/cpu/quant.clj:296-298): floor, plus one
+// when the fraction is at least 1/2 (x - floor(x) is exact in double), so ties
+// go toward +infinity. NaN gives 0.
+__device__ __forceinline__ int java_round_clamp127(double v) {
+  if (!(v == v)) return 0;
+  const double f = floor(v);
+  const double r = (v - f >= 0.5) ? f + 1.0 : f;
+  return r > 127.0 ? 127 : r < -127.0 ? -127 : (int)r;
 }
 
 // Signed Q8 code j (0..3) of a little-endian dword, as an exact float.

@@ -23,7 +23,8 @@ from . import _lib
 from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, RqError, call, lib
 
 __all__ = [
-    "Context", "QWeight", "RqError", "context", "decode_attention", "qlinear_q8", "dequant_q8_dense",
+    "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "qlinear_q8",
+    "dequant_q8_dense",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]
 
@@ -182,11 +183,12 @@ class QWeight:
         return y
 
     def matmul_fused(self, x, y=None, out_dtype=None, norm_gain=None, norm_eps: float = 0.0, residual=None,
-                     swiglu: bool = False, stream=None):
+                     swiglu: bool = False, act_i8: bool = False, stream=None):
         """rq_qmatmul_fused (m <= 16): the decode matmul with an optional
         RMSNorm of x's rows (norm_gain f32[in]) before it, and either a SwiGLU
         of row pairs (rows 2i / 2i+1 = gate / up; y is [m, out/2]) or a
-        residual add (residual [m, out], y's dtype) after it."""
+        residual add (residual [m, out], y's dtype) after it. act_i8 quantizes
+        the activations to Raster's int8 blocks in the kernel."""
         import torch
 
         _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous CUDA tensor")
@@ -196,7 +198,7 @@ class QWeight:
         if y is None:
             y = torch.empty((m, ny), dtype=out_dtype or torch.float32, device=x.device)
         _need(y.is_cuda and y.is_contiguous() and y.numel() == m * ny, "y must be a contiguous CUDA tensor of m rows")
-        ops = _lib.FusedOps(None, float(norm_eps), None, 1 if swiglu else 0)
+        ops = _lib.FusedOps(None, float(norm_eps), None, 1 if swiglu else 0, 1 if act_i8 else 0)
         if norm_gain is not None:
             _need(norm_gain.is_cuda and norm_gain.dtype == torch.float32 and norm_gain.is_contiguous()
                   and norm_gain.numel() == self.in_, "norm_gain must be a contiguous f32 CUDA tensor of in elements")
@@ -209,6 +211,30 @@ class QWeight:
             stream = torch.cuda.current_stream(x.device)
         call("rq_qmatmul_fused", self.ctx.handle, self.handle, C.c_void_p(x.data_ptr()), _dtype_code(x),
              C.c_void_p(y.data_ptr()), _dtype_code(y), m, C.byref(ops), _stream_ptr(stream))
+        return y
+
+    def matmul_i8(self, xq, xs, xsum=None, y=None, out_dtype=None, stream=None):
+        """rq_qmatmul_i8: y[m, out] from int8 activations (xq int8 [m, in],
+        xs f32 [m, in/32], xsum int32 [m, in/32], needed for Q4_0), as
+        produced by quantize_act_i8."""
+        import torch
+
+        _need(xq.is_cuda and xq.is_contiguous() and xq.dtype == torch.int8, "xq must be a contiguous int8 CUDA tensor")
+        _need(xq.numel() % self.in_ == 0, "xq.numel() must be a multiple of in")
+        m = xq.numel() // self.in_
+        _need(xs.is_cuda and xs.is_contiguous() and xs.dtype == torch.float32 and xs.numel() == m * (self.in_ // 32),
+              "xs must be a contiguous f32 CUDA tensor of m*in/32 elements")
+        if xsum is not None:
+            _need(xsum.is_cuda and xsum.is_contiguous() and xsum.dtype == torch.int32 and xsum.numel() == xs.numel(),
+                  "xsum must be a contiguous int32 CUDA tensor like xs")
+        if y is None:
+            y = torch.empty((m, self.out), dtype=out_dtype or torch.float32, device=xq.device)
+        _need(y.is_cuda and y.is_contiguous() and y.numel() == m * self.out, "y must be a contiguous [m, out] CUDA tensor")
+        if stream is None:
+            stream = torch.cuda.current_stream(xq.device)
+        call("rq_qmatmul_i8", self.ctx.handle, self.handle, C.c_void_p(xq.data_ptr()), C.c_void_p(xs.data_ptr()),
+             C.c_void_p(xsum.data_ptr() if xsum is not None else None), C.c_void_p(y.data_ptr()), _dtype_code(y), m,
+             _stream_ptr(stream))
         return y
 
     def dequant(self, stream=None):
@@ -230,6 +256,24 @@ class QWeight:
         if self.handle:
             call("rq_weight_destroy", self.handle)
             self.handle = None
+
+
+def quantize_act_i8(ctx: Context, x, in_: int, stream=None):
+    """rq_quantize_act_i8 (quantize-act-i8): x f32 [m*in] on the device ->
+    (xq int8 [m, in], xs f32 [m, in/32], xsum int32 [m, in/32])."""
+    import torch
+
+    _need(x.is_cuda and x.is_contiguous() and x.dtype == torch.float32, "x must be a contiguous f32 CUDA tensor")
+    _need(in_ % 32 == 0 and x.numel() % in_ == 0, "x.numel() must be a multiple of in, in a multiple of 32")
+    m = x.numel() // in_
+    xq = torch.empty((m, in_), dtype=torch.int8, device=x.device)
+    xs = torch.empty((m, in_ // 32), dtype=torch.float32, device=x.device)
+    xsum = torch.empty((m, in_ // 32), dtype=torch.int32, device=x.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device)
+    call("rq_quantize_act_i8", ctx.handle, C.c_void_p(x.data_ptr()), m, in_, C.c_void_p(xq.data_ptr()),
+         C.c_void_p(xs.data_ptr()), C.c_void_p(xsum.data_ptr()), _stream_ptr(stream))
+    return xq, xs, xsum
 
 
 def decode_attention(ctx: Context, q, k, v, kcache, vcache, pos: int, n_q: int, n_kv: int, head_dim: int,
