@@ -15,14 +15,18 @@ Beside it, on the same JSON line:
            enough weight copies (> 512 MB) that every call reads its weight
            from HBM, not the 256 MB Infinity Cache ("cold"); warm = one copy.
   decoder - the two-layer decode step (fourth workload configuration) in one
-           captured HIP graph: us per token step and tokens/s.
+           captured HIP graph: us per token step and tokens/s, for the fused
+           chain and for the unfused one (torch glue between the matmuls).
+  int8   - the int8-activation path: rq_quantize_act_i8 over 512 x 4096 f32
+           (GB/s), rq_qmatmul_i8 at the headline shape (TOP/s, activations
+           quantized once before timing) and at M = 1 (cold / warm GB/s).
   sweep  - (--suite all) Q4 skinny M in {1,4,16} and the 70B-MLP shapes.
   roofline      - the GEMM kernel against dense bf16 MFMA peak: 2*M*K*N flop
-                  per launch over the kernel's average duration, from the start
-                  and end timestamps of its own dispatch, which librq captures in
-                  HIP events on the call's stream (rq_ctx_set_kernel_timing)
-                  during the timed steps. A step also runs the small
-                  activation-packing kernel, so `value` is lower.
+                  per launch over the kernel's average duration, from the end
+                  of the activation-packing kernel to the end of the GEMM that
+                  follows it, which librq captures in HIP events on the call's
+                  stream (rq_ctx_set_kernel_timing) during the timed steps. A
+                  step also runs the packing kernel, so `value` is lower.
   roofline_gemv - the decode kernel against HBM peak: algorithmic bytes per
                   launch over its cold per-call time (the graph replays above:
                   one kernel per call, launch gaps included).
@@ -50,6 +54,7 @@ if ROOT not in sys.path:
 METRIC = "qmatmul GEMV GB/s (% of HBM peak) at M=1; GEMM TFLOPS (% MFMA) at M=512"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -58,12 +63,17 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def act_bytes(xdt):
+    # bytes per activation element; int8: the code, f32 scale and int32 sum per 32
+    return {"f32": 4, "bf16": 2, "i8": 1.25}[xdt]
+
+
 def q8_bytes(m, k, n, xb, yb):
-    return n * k + n * (k // 32) * 4 + m * k * xb + m * n * yb
+    return int(n * k + n * (k // 32) * 4 + m * k * xb + m * n * yb)
 
 
 def q4_bytes(m, k, n, xb, yb):
-    return n * k // 2 + n * (k // 32) * 2 + m * k * xb + m * n * yb
+    return int(n * k // 2 + n * (k // 32) * 2 + m * k * xb + m * n * yb)
 
 
 class Case:
@@ -79,15 +89,16 @@ class Case:
         if fmt == "q8":
             codes, scales = wl.q8_weights(n, k, seed=seed)
             self.weights = [raster_amd.QWeight.q8(codes, scales, n, k, ctx) for _ in range(copies)]
-            self.bytes = q8_bytes(m, k, n, 4 if xdt == "f32" else 2, 4 if ydt == "f32" else 2)
+            self.bytes = q8_bytes(m, k, n, act_bytes(xdt), 4 if ydt == "f32" else 2)
         else:
             packed, sc16 = wl.q4_weights(n, k, seed=seed)
             self.weights = [raster_amd.QWeight.q4(packed, sc16.view(np.float16), n, k, ctx)
                             for _ in range(copies)]
-            self.bytes = q4_bytes(m, k, n, 4 if xdt == "f32" else 2, 4 if ydt == "f32" else 2)
+            self.bytes = q4_bytes(m, k, n, act_bytes(xdt), 4 if ydt == "f32" else 2)
         self.flops = 2.0 * m * k * n
-        x = torch.from_numpy(wl.activations(m, k, seed=seed + 1, dtype=xdt)).cuda().reshape(m, k)
-        self.x = x.to(torch.bfloat16) if xdt == "bf16" else x
+        x = torch.from_numpy(wl.activations(m, k, seed=seed + 1, dtype="f32" if xdt == "i8" else xdt)).cuda()
+        self.x = x.reshape(m, k).to(torch.bfloat16) if xdt == "bf16" else x.reshape(m, k)
+        self.xi8 = raster_amd.quantize_act_i8(ctx, x, k) if xdt == "i8" else None
         ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
         self.y = torch.empty((m, n), dtype=ydtype, device="cuda")
         self.i = 0
@@ -95,7 +106,10 @@ class Case:
     def step(self):
         w = self.weights[self.i % len(self.weights)]
         self.i += 1
-        w.matmul(self.x, self.y)
+        if self.xi8 is not None:
+            w.matmul_i8(*self.xi8, y=self.y)
+        else:
+            w.matmul(self.x, self.y)
 
     def destroy(self):
         for w in self.weights:
@@ -170,6 +184,43 @@ def hbm_line(torch, ctx, name, fmt, m, k, n, xdt, ydt):
                warm_us=round(warm_ms * 1e3, 3), warm_GBs=round(wbytes / warm_ms / 1e6, 1),
                warm_cv=round(warm_cv, 4))
     return out
+
+
+class QuantCase:
+    """rq_quantize_act_i8 over an m x k f32 activation block."""
+
+    def __init__(self, torch, ctx, m, k):
+        import raster_amd
+
+        self.ctx, self.k, self.raster_amd = ctx, k, raster_amd
+        self.x = torch.randn(m * k, device="cuda")
+        self.out = (torch.empty((m, k), dtype=torch.int8, device="cuda"),
+                    torch.empty((m, k // 32), dtype=torch.float32, device="cuda"),
+                    torch.empty((m, k // 32), dtype=torch.int32, device="cuda"))
+        self.bytes = m * k * (4 + 1) + m * (k // 32) * 8
+
+    def step(self):
+        self.raster_amd.quantize_act_i8(self.ctx, self.x, self.k, out=self.out)
+
+
+def int8_lines(torch, ctx):
+    """The int8-activation path: the on-device quantizer (HBM-bound), the
+    int8-MFMA GEMM at the headline shape (its activations quantized once,
+    outside the timed region) and the int8 decode kernel at M = 1."""
+    qc = QuantCase(torch, ctx, 512, 4096)
+    q_ms, _ = time_graph(torch, qc)
+    lines = {"quantize_act_i8": {"m": 512, "k": 4096, "us": round(q_ms * 1e3, 3),
+                                 "GBs": round(qc.bytes / q_ms / 1e6, 1)}}
+    c = Case(torch, ctx, "q8", 512, 4096, 11008, "i8", "bf16")
+    ms = time_eager(torch, c, 50, 5)
+    c.destroy()
+    lines["gemm_i8_q8_C2_shape"] = {"m": 512, "k": 4096, "n": 11008, "y": "bf16", "us": round(ms * 1e3, 3),
+                                    "TOPs": round(c.flops / ms / 1e9, 1),
+                                    "frac_int8_mfma": round(c.flops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
+    for fmt, k, n in (("q8", 4096, 4096), ("q4", 4096, 14336)):
+        ln = hbm_line(torch, ctx, "int8 decode", fmt, 1, k, n, "i8", "f32")
+        lines[f"decode_i8_{fmt}_m1_{n}x{k}"] = {kk: ln[kk] for kk in ("cold_us", "cold_GBs", "warm_us", "warm_GBs")}
+    return lines
 
 
 def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
@@ -453,6 +504,12 @@ def main():
         result["decoder"] = decoder_line(torch, ctx)
         log(f"decoder: {result['decoder']['us_per_step']} us/step fused, {result['decoder']['tokens_per_s']} tokens/s;"
             f" {result['decoder']['unfused_us_per_step']} us/step unfused")
+        log("int8-activation path")
+        result["int8"] = i8 = int8_lines(torch, ctx)
+        log(f"int8: quantize {i8['quantize_act_i8']['us']} us {i8['quantize_act_i8']['GBs']} GB/s; "
+            f"gemm {i8['gemm_i8_q8_C2_shape']['us']} us {i8['gemm_i8_q8_C2_shape']['TOPs']} TOP/s; "
+            f"decode q8 cold {i8['decode_i8_q8_m1_4096x4096']['cold_us']} us, "
+            f"q4 cold {i8['decode_i8_q4_m1_14336x4096']['cold_us']} us")
 
     if args.suite == "all" and not args.only_gemm:
         sweep = []

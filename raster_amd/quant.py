@@ -258,17 +258,24 @@ class QWeight:
             self.handle = None
 
 
-def quantize_act_i8(ctx: Context, x, in_: int, stream=None):
+def quantize_act_i8(ctx: Context, x, in_: int, out=None, stream=None):
     """rq_quantize_act_i8 (quantize-act-i8): x f32 [m*in] on the device ->
-    (xq int8 [m, in], xs f32 [m, in/32], xsum int32 [m, in/32])."""
+    (xq int8 [m, in], xs f32 [m, in/32], xsum int32 [m, in/32]), written into
+    `out` when given."""
     import torch
 
     _need(x.is_cuda and x.is_contiguous() and x.dtype == torch.float32, "x must be a contiguous f32 CUDA tensor")
     _need(in_ % 32 == 0 and x.numel() % in_ == 0, "x.numel() must be a multiple of in, in a multiple of 32")
     m = x.numel() // in_
-    xq = torch.empty((m, in_), dtype=torch.int8, device=x.device)
-    xs = torch.empty((m, in_ // 32), dtype=torch.float32, device=x.device)
-    xsum = torch.empty((m, in_ // 32), dtype=torch.int32, device=x.device)
+    if out is None:
+        xq = torch.empty((m, in_), dtype=torch.int8, device=x.device)
+        xs = torch.empty((m, in_ // 32), dtype=torch.float32, device=x.device)
+        xsum = torch.empty((m, in_ // 32), dtype=torch.int32, device=x.device)
+    else:
+        xq, xs, xsum = out
+        _need(xq.numel() == m * in_ and xs.numel() == m * (in_ // 32) and xsum.numel() == xs.numel()
+              and xq.dtype == torch.int8 and xs.dtype == torch.float32 and xsum.dtype == torch.int32
+              and all(t.is_cuda and t.is_contiguous() for t in (xq, xs, xsum)), "out tensors do not match x")
     if stream is None:
         stream = torch.cuda.current_stream(x.device)
     call("rq_quantize_act_i8", ctx.handle, C.c_void_p(x.data_ptr()), m, in_, C.c_void_p(xq.data_ptr()),
