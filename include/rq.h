@@ -53,8 +53,12 @@ enum { RQ_F32 = 0, RQ_BF16 = 1, RQ_F16 = 2 };
 /* weight formats */
 enum {
   RQ_Q8_0 = 0, /* signed int8 codes, W = scale * code (raster/quant/train.clj:13-16) */
-  RQ_Q4_0 = 1  /* unsigned nibbles, zero-point 8, lo = elem k, hi = elem k+16 of each
+  RQ_Q4_0 = 1, /* unsigned nibbles, zero-point 8, lo = elem k, hi = elem k+16 of each
                   32-block (raster/compiler/backend/cpu/quant.clj:27-31) */
+  RQ_Q4_K = 2, /* K-quant super-blocks of 256: x = (da*aq)*q + (db*bq) per 32-sub-block
+                  (raster/compiler/backend/cpu/quant.clj:85-156) */
+  RQ_Q6_K = 3  /* K-quant super-blocks of 256: x = (ds*sc)*(q-32) per 16-sub-block
+                  (raster/compiler/backend/cpu/quant.clj:201-252) */
 };
 
 typedef struct rq_ctx_s* rq_ctx;
@@ -199,6 +203,37 @@ typedef struct {
  * replaces the op sequences named in rq_fused_ops around a qlinear. */
 int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                      const rq_fused_ops* ops, void* stream);
+
+/* K-quant weights from Raster's arrays (Raster's own layout, each row of the
+ * [out x in] matrix its own super-blocks, in % 256 == 0; the encoders are
+ * quantize-weight-q4k / quantize-weight-q6k, quant.clj:92-137,214-239):
+ *  Q4_K: wq u8[out*in/2] nibbles (w[k] low, w[k+16] high per 32-sub-block),
+ *        da, db f32[out*in/256], aq u8[out*in/32] (0..63), bq i8[out*in/32];
+ *  Q6_K: wq u8[out*in] (0..63), sc i8[out*in/16], ds f32[out*in/256].
+ * They take q8_K activations (rq_quantize_act_q8k, rq_qmatmul_q8k); rq_dequant
+ * gives dequant-q4k / dequant-q6k bit for bit. rq_qmatmul and its variants
+ * reject them with RQ_ERR_DTYPE. */
+int rq_weight_create_q4k(rq_ctx ctx, const uint8_t* wq, const float* da, const float* db, const uint8_t* aq,
+                         const int8_t* bq, int64_t out, int64_t in, rq_weight* w);
+int rq_weight_create_q6k(rq_ctx ctx, const uint8_t* wq, const int8_t* sc, const float* ds, int64_t out, int64_t in,
+                         rq_weight* w);
+
+/* q8_K activations on the device (quantize-act-q8k, quant.clj:158-176, the
+ * GPU quant-act-q8k-gpu! of raster/quant/kernels_k.clj:93-134): per row of x
+ * f32[m*in] (in % 256 == 0) and 256-element super-block, d = max|x| / 127 in
+ * double, xq int8[m*in] = clamp(Math/round(x / d), -127, 127), xs f32[m*in/256]
+ * = (float) d, bsums int32[m*in/sub] the sums of sub consecutive codes (sub =
+ * 32 for Q4_K, 16 for Q6_K). Bitwise equal to the reference on finite input. */
+int rq_quantize_act_q8k(rq_ctx ctx, const float* x, int64_t m, int64_t in, int sub, int8_t* xq, float* xs,
+                        int32_t* bsums, void* stream);
+
+/* y[m, out] = the K dot of a Q4_K / Q6_K weight with q8_K activations
+ * (qmatmul-q4k-dp4a! / qmatmul-q6k-dp4a!, raster/quant/kernels_k.clj:186-297):
+ * exact int32 sub-block dots, the scale terms added in f32 (Raster: double).
+ * bsums must use the weight's sub-block size. Decode-oriented: four activation
+ * rows per pass over the weights. xq 16-byte aligned. */
+int rq_qmatmul_q8k(rq_ctx ctx, rq_weight w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
+                   int y_dtype, int64_t m, void* stream);
 
 /* Raster's activation quantizer on the device (quantize-act-i8,
  * raster/compiler/backend/cpu/quant.clj:282-305,399-415): per row of x

@@ -100,6 +100,13 @@ def _declare(L):
         "rqo_qmatmul_i8_gemm": ([p, p, p, p, p, i64, i64, i64], None),
         "rqo_i8gemv_dp4a": ([p, p, p, i64, i64], None),
         "rqo_dense_matmul_nt_f64": ([p, p, i64, i64, i64, p], None),
+        "rqo_quantize_weight_q4k": ([p, i64, p, p, p, p, p], None),
+        "rqo_dequant_q4k": ([p, p, p, p, p, i64, p], None),
+        "rqo_quantize_weight_q6k": ([p, i64, p, p, p], None),
+        "rqo_dequant_q6k": ([p, p, p, i64, p], None),
+        "rqo_quantize_act_q8k": ([p, i64, i64, i64, p, p, p], None),
+        "rqo_qmatmul_q4k": ([p, p, p, p, p, p, p, p, i64, i64, i64, p], None),
+        "rqo_qmatmul_q6k": ([p, p, p, p, p, p, i64, i64, i64, p], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -420,3 +427,66 @@ def normwise_relerr(a, ref) -> float:
     a = np.asarray(a, np.float64).ravel()
     ref = np.asarray(ref, np.float64).ravel()
     return float(np.max(np.abs(a - ref)) / max(1e-9, float(np.max(np.abs(ref)))))
+
+
+# ---------------------------------------------------------------- K-quants
+def quantize_weight_q4k(w):
+    """raster.compiler.backend.cpu.quant/quantize-weight-q4k -> (wq, da, db, aq, bq)."""
+    w = _c(w, np.float32)
+    n = w.size
+    wq = np.empty(n // 2, np.uint8)
+    da, db = np.empty(n // 256, np.float32), np.empty(n // 256, np.float32)
+    aq, bq = np.empty(n // 32, np.uint8), np.empty(n // 32, np.int8)
+    lib().rqo_quantize_weight_q4k(_ptr(w), n, _ptr(wq), _ptr(da), _ptr(db), _ptr(aq), _ptr(bq))
+    return wq, da, db, aq, bq
+
+
+def dequant_q4k(wq, da, db, aq, bq, n: int) -> np.ndarray:
+    """dequant-q4k -> f32[n]."""
+    out = np.empty(n, np.float32)
+    lib().rqo_dequant_q4k(_ptr(_c(wq, np.uint8)), _ptr(_c(da, np.float32)), _ptr(_c(db, np.float32)),
+                          _ptr(_c(aq, np.uint8)), _ptr(_c(bq, np.int8)), n, _ptr(out))
+    return out
+
+
+def quantize_weight_q6k(w):
+    """quantize-weight-q6k -> (wq, sc, ds)."""
+    w = _c(w, np.float32)
+    n = w.size
+    wq, sc, ds = np.empty(n, np.uint8), np.empty(n // 16, np.int8), np.empty(n // 256, np.float32)
+    lib().rqo_quantize_weight_q6k(_ptr(w), n, _ptr(wq), _ptr(sc), _ptr(ds))
+    return wq, sc, ds
+
+
+def dequant_q6k(wq, sc, ds, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().rqo_dequant_q6k(_ptr(_c(wq, np.uint8)), _ptr(_c(sc, np.int8)), _ptr(_c(ds, np.float32)), n, _ptr(out))
+    return out
+
+
+def quantize_act_q8k(x, m: int, in_: int, sub: int):
+    """quantize-act-q8k of m rows -> (xq, xs[m*in/256], bsums[m*in/sub])."""
+    x = _c(x, np.float32)
+    xq = np.empty(m * in_, np.int8)
+    xs = np.empty(m * (in_ // 256), np.float32)
+    bsums = np.empty(m * (in_ // sub), np.int32)
+    lib().rqo_quantize_act_q8k(_ptr(x), m, in_, sub, _ptr(xq), _ptr(xs), _ptr(bsums))
+    return xq, xs, bsums
+
+
+def qmatmul_q4k(xq, xs, bsums, wq, da, db, aq, bq, m: int, in_: int, out: int) -> np.ndarray:
+    """qmatmul-q4k-composable! for m rows -> y[m*out]."""
+    y = np.empty(m * out, np.float32)
+    lib().rqo_qmatmul_q4k(_ptr(_c(xq, np.int8)), _ptr(_c(xs, np.float32)), _ptr(_c(bsums, np.int32)),
+                          _ptr(_c(wq, np.uint8)), _ptr(_c(da, np.float32)), _ptr(_c(db, np.float32)),
+                          _ptr(_c(aq, np.uint8)), _ptr(_c(bq, np.int8)), m, in_, out, _ptr(y))
+    return y
+
+
+def qmatmul_q6k(xq, xs, bsums, wq, sc, ds, m: int, in_: int, out: int) -> np.ndarray:
+    """qmatmul-q6k-composable! for m rows -> y[m*out]."""
+    y = np.empty(m * out, np.float32)
+    lib().rqo_qmatmul_q6k(_ptr(_c(xq, np.int8)), _ptr(_c(xs, np.float32)), _ptr(_c(bsums, np.int32)),
+                          _ptr(_c(wq, np.uint8)), _ptr(_c(sc, np.int8)), _ptr(_c(ds, np.float32)), m, in_, out,
+                          _ptr(y))
+    return y

@@ -585,6 +585,192 @@ void rqo_i8gemv_dp4a(const int32_t* wp, const int32_t* xp, float* y, int64_t kw,
   }
 }
 
+/* ------------------------------------------------------------------------- */
+/* K-quants                                                                   */
+/* ------------------------------------------------------------------------- */
+static inline int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : v > hi ? hi : v; }
+
+/* quantize-weight-q4k: raster/compiler/backend/cpu/quant.clj:92-137. Clojure
+ * arithmetic on floats widens to double; min/max of floats are exact. */
+void rqo_quantize_weight_q4k(const float* w, int64_t len, uint8_t* wq, float* da, float* db, uint8_t* aq,
+                             int8_t* bq) {
+  const int64_t sbk = 256, sub = 32, subs = 8, half = 16, nsb = len / sbk;
+  for (int64_t sb = 0; sb < nsb; sb++) {
+    const int64_t sbase = sb * sbk;
+    double as[8], bs[8];
+    for (int64_t j = 0; j < subs; j++) { /* 1. sub-block scale (max-min)/15 and min */
+      const int64_t base = sbase + j * sub;
+      float lo = w[base], hi = w[base];
+      for (int64_t i = 1; i < sub; i++) {
+        if (w[base + i] < lo) lo = w[base + i];
+        if (w[base + i] > hi) hi = w[base + i];
+      }
+      as[j] = ((double)hi - (double)lo) / 15.0;
+      bs[j] = (double)lo;
+    }
+    double amax = 0.0, bmax = 0.0; /* 2. super-block scales of scales / mins */
+    for (int64_t j = 0; j < subs; j++) {
+      if (as[j] > amax) amax = as[j];
+      if (fabs(bs[j]) > bmax) bmax = fabs(bs[j]);
+    }
+    const double dav = amax / 63.0, dbv = bmax / 31.0;
+    const double ida = dav == 0.0 ? 0.0 : 1.0 / dav, idb = dbv == 0.0 ? 0.0 : 1.0 / dbv;
+    da[sb] = (float)dav;
+    db[sb] = (float)dbv;
+    for (int64_t j = 0; j < subs; j++) {
+      const int64_t aqj = clamp64(rqo_java_round(as[j] * ida), 0, 63);
+      const int64_t bqj = clamp64(rqo_java_round(bs[j] * idb), -32, 31);
+      const double a1 = dav * (double)aqj, b1 = dbv * (double)bqj;
+      const double ia1 = a1 == 0.0 ? 0.0 : 1.0 / a1;
+      const int64_t base = sbase + j * sub, sidx = sb * subs + j;
+      aq[sidx] = (uint8_t)aqj;
+      bq[sidx] = (int8_t)bqj;
+      /* 3. weights against the quantized sub scale / min */
+      for (int64_t k = 0; k < half; k++) {
+        const int64_t q0 = clamp64(rqo_java_round(((double)w[base + k] - b1) * ia1), 0, 15);
+        const int64_t q1 = clamp64(rqo_java_round(((double)w[base + k + half] - b1) * ia1), 0, 15);
+        wq[base / 2 + k] = (uint8_t)(q0 | (q1 << 4));
+      }
+    }
+  }
+}
+
+/* dequant-q4k: quant.clj:139-156 */
+void rqo_dequant_q4k(const uint8_t* wq, const float* da, const float* db, const uint8_t* aq, const int8_t* bq,
+                     int64_t len, float* out) {
+  const int64_t sbk = 256, sub = 32, subs = 8, half = 16, nsb = len / sbk;
+  for (int64_t sb = 0; sb < nsb; sb++) {
+    const double dav = da[sb], dbv = db[sb];
+    for (int64_t j = 0; j < subs; j++) {
+      const int64_t base = sb * sbk + j * sub, sidx = sb * subs + j;
+      const double a1 = dav * (double)(int8_t)aq[sidx], b1 = dbv * (double)bq[sidx];
+      for (int64_t k = 0; k < half; k++) {
+        const int64_t bv = wq[base / 2 + k];
+        out[base + k] = (float)(a1 * (double)(bv & 0xF) + b1);
+        out[base + k + half] = (float)(a1 * (double)(bv >> 4) + b1);
+      }
+    }
+  }
+}
+
+/* quantize-weight-q6k: quant.clj:214-239 */
+void rqo_quantize_weight_q6k(const float* w, int64_t len, uint8_t* wq, int8_t* sc, float* ds) {
+  const int64_t sbk = 256, sub = 16, subs = 16, zp = 32, nsb = len / sbk;
+  for (int64_t sb = 0; sb < nsb; sb++) {
+    const int64_t sbase = sb * sbk;
+    double as[16];
+    for (int64_t j = 0; j < subs; j++) {
+      double mx = 0.0;
+      for (int64_t i = 0; i < sub; i++) {
+        const double a = fabsf(w[sbase + j * sub + i]);
+        if (a > mx) mx = a;
+      }
+      as[j] = mx / 32.0;
+    }
+    double amax = 0.0;
+    for (int64_t j = 0; j < subs; j++)
+      if (as[j] > amax) amax = as[j];
+    const double dv = amax / 127.0, idv = dv == 0.0 ? 0.0 : 1.0 / dv;
+    ds[sb] = (float)dv;
+    for (int64_t j = 0; j < subs; j++) {
+      const int64_t scj = clamp64(rqo_java_round(as[j] * idv), 0, 127);
+      const double a1 = dv * (double)scj, ia1 = a1 == 0.0 ? 0.0 : 1.0 / a1;
+      const int64_t base = sbase + j * sub;
+      sc[sb * subs + j] = (int8_t)scj;
+      for (int64_t k = 0; k < sub; k++)
+        wq[base + k] = (uint8_t)clamp64(rqo_java_round((double)w[base + k] * ia1) + zp, 0, 63);
+    }
+  }
+}
+
+/* dequant-q6k: quant.clj:241-252 */
+void rqo_dequant_q6k(const uint8_t* wq, const int8_t* sc, const float* ds, int64_t len, float* out) {
+  const int64_t sbk = 256, sub = 16, subs = 16, zp = 32, nsb = len / sbk;
+  for (int64_t sb = 0; sb < nsb; sb++) {
+    const double dv = ds[sb];
+    for (int64_t j = 0; j < subs; j++) {
+      const double a1 = dv * (double)sc[sb * subs + j];
+      const int64_t base = sb * sbk + j * sub;
+      for (int64_t k = 0; k < sub; k++) out[base + k] = (float)(a1 * (double)((int64_t)wq[base + k] - zp));
+    }
+  }
+}
+
+/* quantize-act-q8k: quant.clj:158-176, per row */
+void rqo_quantize_act_q8k(const float* x, int64_t m, int64_t in, int64_t sub, int8_t* xq, float* xs,
+                          int32_t* bsums) {
+  const int64_t sbk = 256, nsb = in / sbk, subs = sbk / sub;
+  for (int64_t t = 0; t < m; t++)
+    for (int64_t sb = 0; sb < nsb; sb++) {
+      const int64_t sbase = t * in + sb * sbk;
+      double mx = 0.0;
+      for (int64_t i = 0; i < sbk; i++) {
+        const double a = fabsf(x[sbase + i]);
+        if (a > mx) mx = a;
+      }
+      const double d = mx / 127.0, id = d == 0.0 ? 0.0 : 1.0 / d;
+      xs[t * nsb + sb] = (float)d;
+      for (int64_t j = 0; j < subs; j++) {
+        int64_t s = 0;
+        for (int64_t k = 0; k < sub; k++) {
+          const int64_t e = sbase + j * sub + k;
+          const int64_t q = clamp64(rqo_java_round((double)x[e] * id), -127, 127);
+          xq[e] = (int8_t)q;
+          s += q;
+        }
+        bsums[t * (in / sub) + sb * subs + j] = (int32_t)s;
+      }
+    }
+}
+
+/* qmatmul-q4k-composable!: raster/quant/kernels_k.clj:15-46 */
+void rqo_qmatmul_q4k(const int8_t* xq, const float* xs, const int32_t* bsums, const uint8_t* wq, const float* da,
+                     const float* db, const uint8_t* aq, const int8_t* bq, int64_t m, int64_t in, int64_t out,
+                     float* y) {
+  const int64_t nsb = in / 256, nsub = in / 32, wrow = in / 2;
+  for (int64_t t = 0; t < m; t++)
+    for (int64_t o = 0; o < out; o++) {
+      const int8_t* x = xq + t * in;
+      double a = 0.0;
+      for (int64_t sb = 0; sb < nsb; sb++) {
+        const double dav = da[o * nsb + sb], dbv = db[o * nsb + sb], dact = xs[t * nsb + sb];
+        double s = 0.0;
+        for (int64_t j = 0; j < 8; j++) {
+          const int64_t base = sb * 256 + j * 32, sidx = sb * 8 + j;
+          const double aj = dav * (double)(int8_t)aq[o * nsub + sidx], bj = dbv * (double)bq[o * nsub + sidx];
+          const int64_t dp = rqo_wi8_dot_q4(wq, o * wrow + base / 2, x, base);
+          s = s + aj * (double)dp + bj * (double)bsums[t * nsub + sidx];
+        }
+        a += dact * s;
+      }
+      y[t * out + o] = (float)a;
+    }
+}
+
+/* qmatmul-q6k-composable!: raster/quant/kernels_k.clj:48-79 */
+void rqo_qmatmul_q6k(const int8_t* xq, const float* xs, const int32_t* bsums, const uint8_t* wq, const int8_t* sc,
+                     const float* ds, int64_t m, int64_t in, int64_t out, float* y) {
+  const int64_t nsb = in / 256, nsub = in / 16;
+  for (int64_t t = 0; t < m; t++)
+    for (int64_t o = 0; o < out; o++) {
+      const int8_t* x = xq + t * in;
+      double a = 0.0;
+      for (int64_t sb = 0; sb < nsb; sb++) {
+        const double dv = ds[o * nsb + sb], dact = xs[t * nsb + sb];
+        double s = 0.0;
+        for (int64_t j = 0; j < 16; j++) {
+          const int64_t base = sb * 256 + j * 16, sidx = sb * 16 + j;
+          const int64_t scj = sc[o * nsub + sidx];
+          const int64_t dp = rqo_wi8_dot(wq, o * in + base, x, base, 16);
+          const int64_t folded = dp - 32 * (int64_t)bsums[t * nsub + sidx];
+          s += (double)scj * (double)folded;
+        }
+        a += dv * dact * s;
+      }
+      y[t * out + o] = (float)a;
+    }
+}
+
 void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t in, int64_t out, double* y) {
   for (int64_t p = 0; p < m; p++)
     for (int64_t o = 0; o < out; o++) {

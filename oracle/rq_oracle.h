@@ -152,6 +152,35 @@ void rqo_decoder_layer(float* x, const int8_t* const* w, const float* const* s, 
                        int64_t head_dim, int64_t ffn, int64_t cache_len, double eps, double theta,
                        float* scratch);
 
+/* ---- K-quants (raster/compiler/backend/cpu/quant.clj:78-280; Raster's own
+ * layout, not GGUF's) over a row-major [out x in] matrix, in % 256 == 0, each
+ * row its own super-blocks (raster/quant/kernels_k.clj:1-10) ---- */
+/* quantize-weight-q4k (quant.clj:92-137) of len values: wq[len/2] nibbles
+ * (w[k] low, w[k+16] high per 32-sub-block), da/db[len/256], aq[len/32]
+ * (0..63), bq[len/32] (-32..31). */
+void rqo_quantize_weight_q4k(const float* w, int64_t len, uint8_t* wq, float* da, float* db, uint8_t* aq,
+                             int8_t* bq);
+/* dequant-q4k (quant.clj:139-156): x = (da*aq)*q + (db*bq), in double, one narrowing */
+void rqo_dequant_q4k(const uint8_t* wq, const float* da, const float* db, const uint8_t* aq, const int8_t* bq,
+                     int64_t len, float* out);
+/* quantize-weight-q6k (quant.clj:214-239): wq[len] (0..63, zero point 32),
+ * sc[len/16] (0..127), ds[len/256] */
+void rqo_quantize_weight_q6k(const float* w, int64_t len, uint8_t* wq, int8_t* sc, float* ds);
+/* dequant-q6k (quant.clj:241-252): x = (ds*sc)*(q-32) */
+void rqo_dequant_q6k(const uint8_t* wq, const int8_t* sc, const float* ds, int64_t len, float* out);
+/* quantize-act-q8k (quant.clj:158-176) of m rows of in: xq[m*in], xs[m*in/256]
+ * (d = max|x|/127 per super-block), bsums[m*in/sub] (sub = 32 for Q4_K, 16 for Q6_K) */
+void rqo_quantize_act_q8k(const float* x, int64_t m, int64_t in, int64_t sub, int8_t* xq, float* xs,
+                          int32_t* bsums);
+/* qmatmul-q4k-composable! (raster/quant/kernels_k.clj:15-46) for each of m
+ * activation rows: y[t*out + o] */
+void rqo_qmatmul_q4k(const int8_t* xq, const float* xs, const int32_t* bsums, const uint8_t* wq, const float* da,
+                     const float* db, const uint8_t* aq, const int8_t* bq, int64_t m, int64_t in, int64_t out,
+                     float* y);
+/* qmatmul-q6k-composable! (raster/quant/kernels_k.clj:48-79) */
+void rqo_qmatmul_q6k(const int8_t* xq, const float* xs, const int32_t* bsums, const uint8_t* wq, const int8_t* sc,
+                     const float* ds, int64_t m, int64_t in, int64_t out, float* y);
+
 /* ---- dense helpers (brute force, f64) used to pin the restatements ---- */
 void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t in, int64_t out,
                              double* y);

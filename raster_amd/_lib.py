@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "librq.so")
 
 RQ_OK, RQ_ERR_SHAPE, RQ_ERR_DTYPE, RQ_ERR_NULL, RQ_ERR_OOM, RQ_ERR_HIP, RQ_ERR_HANDLE, RQ_ERR_DEVICE = range(8)
 RQ_F32, RQ_BF16, RQ_F16 = 0, 1, 2
-RQ_Q8_0, RQ_Q4_0 = 0, 1
+RQ_Q8_0, RQ_Q4_0, RQ_Q4_K, RQ_Q6_K = 0, 1, 2, 3
 
 # every exported symbol of include/rq.h with (argtypes, restype)
 _i, _i64, _p, _sz = C.c_int, C.c_int64, C.c_void_p, C.c_size_t
@@ -38,6 +38,8 @@ SIGNATURES = {
     "rq_weight_create_q8_packed": ([_p, _p, _p, _i64, _i64, C.POINTER(_p)], _i),
     "rq_weight_create_q4": ([_p, _p, _p, _i, _i64, _i64, C.POINTER(_p)], _i),
     "rq_weight_create_x8": ([_p, _p, _p, _i, _i64, _i64, C.POINTER(_p)], _i),
+    "rq_weight_create_q4k": ([_p, _p, _p, _p, _p, _p, _i64, _i64, C.POINTER(_p)], _i),
+    "rq_weight_create_q6k": ([_p, _p, _p, _p, _i64, _i64, C.POINTER(_p)], _i),
     "rq_weight_destroy": ([_p], _i),
     "rq_weight_info": ([_p, C.POINTER(_i), C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i), C.POINTER(_sz)], _i),
     "rq_weight_device_ptrs": ([_p, C.POINTER(_p), C.POINTER(_p)], _i),
@@ -45,6 +47,8 @@ SIGNATURES = {
     "rq_qmatmul_fused": ([_p, _p, _p, _i, _p, _i, _i64, _p, _p], _i),
     "rq_quantize_act_i8": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
     "rq_qmatmul_i8": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
+    "rq_quantize_act_q8k": ([_p, _p, _i64, _i64, _i, _p, _p, _p, _p], _i),
+    "rq_qmatmul_q8k": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
     "rq_decode_attention": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, C.c_double, C.c_double, _p, _p], _i),
     "rq_dequant": ([_p, _p, _p, _p], _i),
     "rq_qlinear_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),

@@ -548,6 +548,94 @@ int rq_weight_destroy(rq_weight h) {
   return RQ_OK;
 }
 
+// K-quant weight from host arrays already in the resident order: codes
+// (qbytes), super-block scales (sbytes), sub-block scales (ubytes).
+static int make_weight_k(Ctx* c, int format, int64_t out, int64_t in, const void* codes, size_t qbytes,
+                         const void* sup, size_t sbytes, const void* sub, size_t ubytes, rq_weight* wout) {
+  if (int s = set_device(c)) return s;
+  const size_t total = align256(qbytes) + align256(sbytes) + align256(ubytes);
+  void* base = nullptr;
+  hipError_t e = hipMalloc(&base, total);
+  if (e != hipSuccess || !base) {
+    (void)hipGetLastError();
+    return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(total) + " bytes for weight failed");
+  }
+  Weight* w = new (std::nothrow) Weight();
+  if (!w) {
+    (void)hipFree(base);
+    return fail(RQ_ERR_OOM, "host allocation failed");
+  }
+  w->magic = kWeightMagic;
+  w->format = format;
+  w->scale_dtype = RQ_F32;
+  w->device = c->device;
+  w->out = out;
+  w->in = in;
+  w->npad = out;
+  w->base = base;
+  w->q = static_cast<uint8_t*>(base);
+  w->scales = static_cast<uint8_t*>(base) + align256(qbytes);
+  w->scales_rb = nullptr;
+  w->sub_scales = static_cast<uint8_t*>(base) + align256(qbytes) + align256(sbytes);
+  w->bytes = total;
+  w->ctx = c;
+  e = hipMemcpy(w->q, codes, qbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(w->scales, sup, sbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(w->sub_scales, sub, ubytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(base);
+    delete w;
+    return hip_fail(e, "weight upload");
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!live_ctx(c)) {
+      (void)hipFree(base);
+      delete w;
+      return fail(RQ_ERR_HANDLE, "rq_ctx destroyed during weight creation");
+    }
+    g_weights.insert(w);
+    c->weights.insert(w);
+  }
+  *wout = reinterpret_cast<rq_weight>(w);
+  return RQ_OK;
+}
+
+static int check_shape_k(int64_t out, int64_t in) {
+  if (int s = check_shape(out, in)) return s;
+  if (in % 256 != 0) return fail(RQ_ERR_SHAPE, "K-quants need in % 256 == 0 (super-blocks of 256)");
+  if (in > (int64_t)1 << 15) return fail(RQ_ERR_SHAPE, "K-quant in above 32768 (activations staged in LDS)");
+  return RQ_OK;
+}
+
+int rq_weight_create_q4k(rq_ctx h, const uint8_t* wq, const float* da, const float* db, const uint8_t* aq,
+                         const int8_t* bq, int64_t out, int64_t in, rq_weight* w) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!wq || !da || !db || !aq || !bq || !w) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape_k(out, in)) return s;
+  const int64_t nsb = out * (in / 256), nsub = out * (in / 32);
+  std::vector<float> sup((size_t)(2 * nsb));
+  for (int64_t i = 0; i < nsb; i++) {
+    sup[(size_t)(2 * i)] = da[i];
+    sup[(size_t)(2 * i + 1)] = db[i];
+  }
+  std::vector<uint16_t> sub((size_t)nsub);
+  for (int64_t i = 0; i < nsub; i++) sub[(size_t)i] = (uint16_t)(aq[i] | ((uint16_t)(uint8_t)bq[i] << 8));
+  return make_weight_k(c, RQ_Q4_K, out, in, wq, (size_t)(out * in / 2), sup.data(), sup.size() * 4, sub.data(),
+                       sub.size() * 2, w);
+}
+
+int rq_weight_create_q6k(rq_ctx h, const uint8_t* wq, const int8_t* sc, const float* ds, int64_t out, int64_t in,
+                         rq_weight* w) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!wq || !sc || !ds || !w) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape_k(out, in)) return s;
+  return make_weight_k(c, RQ_Q6_K, out, in, wq, (size_t)(out * in), ds, (size_t)(out * (in / 256)) * 4, sc,
+                       (size_t)(out * (in / 16)), w);
+}
+
 int rq_weight_info(rq_weight h, int* format, int64_t* out, int64_t* in, int* scale_dtype, size_t* bytes) {
   Weight* w = reinterpret_cast<Weight*>(h);
   std::lock_guard<std::mutex> lk(g_mu);
@@ -589,11 +677,15 @@ namespace rq {
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
                       int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream);
 
+static bool kquant(const Weight& w) { return w.format == RQ_Q4_K || w.format == RQ_Q6_K; }
+static const char* kKquantMsg = "K-quant weights take q8_K activations: use rq_qmatmul_q8k";
+
 static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                         const rq_fused_ops* ops, void* stream) {
   Ctx* c;
   Weight w;
   if (int s = lookup(h, wh, &c, &w)) return s;
+  if (kquant(w)) return fail(RQ_ERR_DTYPE, kKquantMsg);
   if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
   if (m == 0) return RQ_OK;
   if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
@@ -703,6 +795,7 @@ int rq_qmatmul_i8(rq_ctx h, rq_weight wh, const int8_t* xq, const float* xs, con
   Ctx* c;
   Weight w;
   if (int s = lookup(h, wh, &c, &w)) return s;
+  if (kquant(w)) return fail(RQ_ERR_DTYPE, kKquantMsg);
   if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
   if (m == 0) return RQ_OK;
   if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
@@ -717,6 +810,49 @@ int rq_qmatmul_i8(rq_ctx h, rq_weight wh, const int8_t* xq, const float* xs, con
   dops.act_scale = xs;
   dops.act_sum = w.format == RQ_Q4_0 ? xsum : nullptr;
   return run_matmul(c, w, plan, xq, kXtI8, y, y_dtype, m, dops, (hipStream_t)stream);
+}
+
+int rq_quantize_act_q8k(rq_ctx h, const float* x, int64_t m, int64_t in, int sub, int8_t* xq, float* xs,
+                        int32_t* bsums, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (m < 0 || in < 0) return fail(RQ_ERR_SHAPE, "negative dimension");
+  if (in % 256 != 0) return fail(RQ_ERR_SHAPE, "in must be a multiple of 256");
+  if (sub != 32 && sub != 16) return fail(RQ_ERR_SHAPE, "sub must be 32 (Q4_K) or 16 (Q6_K)");
+  if (m == 0 || in == 0) return RQ_OK;
+  if (m > ((int64_t)1 << 40) / in) return fail(RQ_ERR_SHAPE, "m * in too large");
+  if (!x || !xq || !xs || !bsums) return fail(RQ_ERR_NULL, "NULL argument");
+  if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
+  if (((uintptr_t)xq & 3) != 0 || ((uintptr_t)xs & 3) != 0 || ((uintptr_t)bsums & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "xq, xs and bsums must be 4-byte aligned");
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_quantize_act_q8k(x, m, in, sub, xq, xs, bsums, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantizer launch");
+  return RQ_OK;
+}
+
+int rq_qmatmul_q8k(rq_ctx h, rq_weight wh, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
+                   int y_dtype, int64_t m, void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (!kquant(w)) return fail(RQ_ERR_DTYPE, "rq_qmatmul_q8k needs a Q4_K or Q6_K weight");
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
+  if (!xq || !xs || !bsums || !y) return fail(RQ_ERR_NULL, "NULL argument");
+  if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
+  if (((uintptr_t)xq & 15) != 0) return fail(RQ_ERR_SHAPE, "xq must be 16-byte aligned");
+  if (((uintptr_t)xs & 3) != 0 || ((uintptr_t)bsums & 3) != 0) return fail(RQ_ERR_SHAPE, "xs / bsums misaligned");
+  if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  if (int s = set_device(c)) return s;
+  const auto ev = timing_pair(c, (hipStream_t)stream);
+  if (ev.first) (void)hipEventRecord(ev.first, (hipStream_t)stream);
+  hipError_t e = launch_kquant_gemv(w, xq, xs, bsums, y, y_dtype, m, c->cu_count, (hipStream_t)stream);
+  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, (hipStream_t)stream);
+  timing_done(c, ev, e == hipSuccess);
+  if (e != hipSuccess) return hip_fail(e, "K-quant GEMV launch");
+  return RQ_OK;
 }
 
 int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v, float* kcache, float* vcache,
@@ -747,7 +883,8 @@ int rq_dequant(rq_ctx h, rq_weight wh, float* w_out, void* stream) {
   if (!w_out) return fail(RQ_ERR_NULL, "w_out is NULL");
   if (((uintptr_t)w_out & 15) != 0) return fail(RQ_ERR_SHAPE, "w_out must be 16-byte aligned");
   if (int s = set_device(c)) return s;
-  hipError_t e = launch_dequant(w, w_out, (hipStream_t)stream);
+  hipError_t e = kquant(w) ? launch_kquant_dequant(w, w_out, (hipStream_t)stream)
+                           : launch_dequant(w, w_out, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "dequant launch");
   return RQ_OK;
 }

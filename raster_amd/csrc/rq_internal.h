@@ -44,6 +44,9 @@ struct Weight {
   uint8_t* q;       // chunked codes / packed nibbles
   void* scales;     // chunked scales, block-major (prefill kernels, dequant)
   void* scales_rb;  // the same scales row-batched (decode kernel)
+  // K-quants (RQ_Q4_K / RQ_Q6_K) keep Raster's row-major codes in q, the
+  // super-block scales in `scales` (Q4_K: da, db side by side) and these:
+  void* sub_scales;  // per (row, sub-block): Q4_K aq, bq side by side; Q6_K sc
   size_t bytes;
   struct Ctx* ctx;
 };
@@ -133,6 +136,13 @@ hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
 hipError_t launch_quantize_act_i8(const float* x, int64_t m, int64_t in, int8_t* xq, float* xs, int32_t* xsum,
                                   hipStream_t stream);
+// K-quants (kquant.hip)
+hipError_t launch_quantize_act_q8k(const float* x, int64_t m, int64_t in, int sub, int8_t* xq, float* xs,
+                                   int32_t* bsums, hipStream_t stream);
+size_t kquant_gemv_lds(int format, int64_t k, int mt);
+hipError_t launch_kquant_gemv(const Weight& w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
+                              int y_dtype, int64_t m, int cu_count, hipStream_t stream);
+hipError_t launch_kquant_dequant(const Weight& w, float* out, hipStream_t stream);
 // RoPE + KV append + single-query attention for one decode step (attention.hip).
 size_t decode_attention_lds(int64_t pos, int64_t head_dim);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,

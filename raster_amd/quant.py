@@ -20,11 +20,11 @@ import threading
 import numpy as np
 
 from . import _lib
-from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, RqError, call, lib
+from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q4_K, RQ_Q6_K, RQ_Q8_0, RqError, call, lib
 
 __all__ = [
-    "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "qlinear_q8",
-    "dequant_q8_dense",
+    "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "quantize_act_q8k",
+    "qlinear_q8", "dequant_q8_dense",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]
 
@@ -156,6 +156,33 @@ class QWeight:
         return cls(ctx, h)
 
     @classmethod
+    def q4k(cls, wq, da, db, aq, bq, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """Q4_K from quantize-weight-q4k's arrays (in % 256 == 0): wq u8[out*in/2],
+        da / db f32[out*in/256], aq u8[out*in/32], bq i8[out*in/32]."""
+        ctx = ctx or context()
+        wq, aq = np.ascontiguousarray(wq, np.uint8), np.ascontiguousarray(aq, np.uint8)
+        da, db = np.ascontiguousarray(da, np.float32), np.ascontiguousarray(db, np.float32)
+        bq = np.ascontiguousarray(bq, np.int8)
+        _need(wq.size == out * in_ // 2 and da.size == db.size == out * (in_ // 256)
+              and aq.size == bq.size == out * (in_ // 32), "array sizes do not match out x in")
+        h = C.c_void_p()
+        call("rq_weight_create_q4k", ctx.handle, _np_ptr(wq), _np_ptr(da), _np_ptr(db), _np_ptr(aq), _np_ptr(bq),
+             out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    @classmethod
+    def q6k(cls, wq, sc, ds, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
+        """Q6_K from quantize-weight-q6k's arrays: wq u8[out*in], sc i8[out*in/16], ds f32[out*in/256]."""
+        ctx = ctx or context()
+        wq, sc = np.ascontiguousarray(wq, np.uint8), np.ascontiguousarray(sc, np.int8)
+        ds = np.ascontiguousarray(ds, np.float32)
+        _need(wq.size == out * in_ and sc.size == out * (in_ // 16) and ds.size == out * (in_ // 256),
+              "array sizes do not match out x in")
+        h = C.c_void_p()
+        call("rq_weight_create_q6k", ctx.handle, _np_ptr(wq), _np_ptr(sc), _np_ptr(ds), out, in_, C.byref(h))
+        return cls(ctx, h)
+
+    @classmethod
     def x8(cls, wqi, wsi, nibble: bool, out: int, in_: int, ctx: Context | None = None) -> "QWeight":
         """From the repack-stream x8 layout of raster/compiler/core/layout.clj:246-286."""
         ctx = ctx or context()
@@ -237,6 +264,29 @@ class QWeight:
              _stream_ptr(stream))
         return y
 
+    def matmul_q8k(self, xq, xs, bsums, y=None, out_dtype=None, stream=None):
+        """rq_qmatmul_q8k: y[m, out] for a K-quant weight from q8_K activations
+        (xq int8 [m, in], xs f32 [m, in/256], bsums int32 [m, in/sub])."""
+        import torch
+
+        _need(self.format in (_lib.RQ_Q4_K, _lib.RQ_Q6_K), "matmul_q8k needs a Q4_K or Q6_K weight")
+        sub = 32 if self.format == _lib.RQ_Q4_K else 16
+        _need(xq.is_cuda and xq.is_contiguous() and xq.dtype == torch.int8 and xq.numel() % self.in_ == 0,
+              "xq must be a contiguous int8 CUDA tensor of m*in elements")
+        m = xq.numel() // self.in_
+        _need(xs.is_cuda and xs.is_contiguous() and xs.dtype == torch.float32 and xs.numel() == m * (self.in_ // 256),
+              "xs must be a contiguous f32 CUDA tensor of m*in/256 elements")
+        _need(bsums.is_cuda and bsums.is_contiguous() and bsums.dtype == torch.int32
+              and bsums.numel() == m * (self.in_ // sub), f"bsums must be int32 [m, in/{sub}]")
+        if y is None:
+            y = torch.empty((m, self.out), dtype=out_dtype or torch.float32, device=xq.device)
+        _need(y.is_cuda and y.is_contiguous() and y.numel() == m * self.out, "y must be a contiguous [m, out] CUDA tensor")
+        if stream is None:
+            stream = torch.cuda.current_stream(xq.device)
+        call("rq_qmatmul_q8k", self.ctx.handle, self.handle, C.c_void_p(xq.data_ptr()), C.c_void_p(xs.data_ptr()),
+             C.c_void_p(bsums.data_ptr()), C.c_void_p(y.data_ptr()), _dtype_code(y), m, _stream_ptr(stream))
+        return y
+
     def dequant(self, stream=None):
         """Dequantized f32 W[out, in] computed on the device."""
         import torch
@@ -281,6 +331,27 @@ def quantize_act_i8(ctx: Context, x, in_: int, out=None, stream=None):
     call("rq_quantize_act_i8", ctx.handle, C.c_void_p(x.data_ptr()), m, in_, C.c_void_p(xq.data_ptr()),
          C.c_void_p(xs.data_ptr()), C.c_void_p(xsum.data_ptr()), _stream_ptr(stream))
     return xq, xs, xsum
+
+
+def quantize_act_q8k(ctx: Context, x, in_: int, sub: int, out=None, stream=None):
+    """rq_quantize_act_q8k (quantize-act-q8k): x f32 [m*in] on the device ->
+    (xq int8 [m, in], xs f32 [m, in/256], bsums int32 [m, in/sub]); sub 32 for
+    Q4_K, 16 for Q6_K."""
+    import torch
+
+    _need(x.is_cuda and x.is_contiguous() and x.dtype == torch.float32, "x must be a contiguous f32 CUDA tensor")
+    _need(in_ % 256 == 0 and x.numel() % in_ == 0 and sub in (16, 32), "in % 256 == 0, sub 16 or 32")
+    m = x.numel() // in_
+    if out is None:
+        out = (torch.empty((m, in_), dtype=torch.int8, device=x.device),
+               torch.empty((m, in_ // 256), dtype=torch.float32, device=x.device),
+               torch.empty((m, in_ // sub), dtype=torch.int32, device=x.device))
+    xq, xs, bsums = out
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device)
+    call("rq_quantize_act_q8k", ctx.handle, C.c_void_p(x.data_ptr()), m, in_, sub, C.c_void_p(xq.data_ptr()),
+         C.c_void_p(xs.data_ptr()), C.c_void_p(bsums.data_ptr()), _stream_ptr(stream))
+    return xq, xs, bsums
 
 
 def decode_attention(ctx: Context, q, k, v, kcache, vcache, pos: int, n_q: int, n_kv: int, head_dim: int,

@@ -483,3 +483,102 @@ def test_decoder_layer_composes_the_glue(orc):
     h = orc.silu_mul(orc.qlinear_q8(x1n, *ws[4], 1, d, ffn), orc.qlinear_q8(x1n, *ws[5], 1, d, ffn), ffn)
     want = orc.residual_add(x1, orc.qlinear_q8(h, *ws[6], 1, ffn, d), d)
     assert np.array_equal(y, want)
+
+
+# ---------------------------------------------------------------- K-quants
+def _ref_matmul_f64(wdq, xdq, out, in_):
+    # ref-matmul of test/raster/quant/kernels_k_test.clj:24-29: double sums, one narrowing
+    return (wdq.reshape(out, in_).astype(np.float64) @ xdq.astype(np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt,wseed,xseed", [("q4k", 1, 2), ("q6k", 3, 4)])
+def test_kquant_reference_test_reproduction(orc, fmt, wseed, xseed):
+    # test/raster/quant/kernels_k_test.clj:31-61: out 8, in 256, java.util.Random
+    # inputs; the composable K dot matches dequant-matmul within 1e-2 per row
+    out, in_ = 8, 256
+    W = orc.jfill_uniform_centered(wseed, out * in_)
+    x = orc.jfill_uniform_centered(xseed, in_)
+    if fmt == "q4k":
+        wq, da, db, aq, bq = orc.quantize_weight_q4k(W)
+        xq, xs, bs = orc.quantize_act_q8k(x, 1, in_, 32)
+        y = orc.qmatmul_q4k(xq, xs, bs, wq, da, db, aq, bq, 1, in_, out)
+        wdq = orc.dequant_q4k(wq, da, db, aq, bq, out * in_)
+    else:
+        wq, sc, ds = orc.quantize_weight_q6k(W)
+        xq, xs, bs = orc.quantize_act_q8k(x, 1, in_, 16)
+        y = orc.qmatmul_q6k(xq, xs, bs, wq, sc, ds, 1, in_, out)
+        wdq = orc.dequant_q6k(wq, sc, ds, out * in_)
+    xdq = (xs[0] * xq.astype(np.float32)).astype(np.float32)  # (float (* dact xq))
+    yref = _ref_matmul_f64(wdq, xdq, out, in_)
+    assert np.all(np.abs(y - yref) < 1e-2)
+
+
+def test_q4k_dot_equals_dequant_dot(orc):
+    # the K dot is the dot of the exact dequantized weight ((da*aq) q + db*bq,
+    # unrounded) with the exact dequantized activation; an independent
+    # vectorized restatement in float64 must agree to rounding
+    rng = np.random.default_rng(21)
+    m, out, in_ = 3, 12, 1024
+    W = rng.standard_normal(out * in_).astype(np.float32)
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    wq, da, db, aq, bq = orc.quantize_weight_q4k(W)
+    xq, xs, bs = orc.quantize_act_q8k(x, m, in_, 32)
+    y = orc.qmatmul_q4k(xq, xs, bs, wq, da, db, aq, bq, m, in_, out).reshape(m, out)
+    nib = wq.reshape(out, in_ // 32, 16).astype(np.float64)
+    q = np.concatenate([nib % 16, nib // 16], axis=2)  # element k low, k + 16 high
+    a1 = (da.astype(np.float64).repeat(8).reshape(out, -1) * aq.reshape(out, -1).astype(np.float64))
+    b1 = (db.astype(np.float64).repeat(8).reshape(out, -1) * bq.reshape(out, -1).astype(np.float64))
+    wexact = (a1[:, :, None] * q + b1[:, :, None]).reshape(out, in_)
+    xexact = (xs.astype(np.float64).reshape(m, -1).repeat(256, axis=1) * xq.reshape(m, in_).astype(np.float64))
+    ref = xexact @ wexact.T
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
+
+
+def test_q6k_dot_equals_dequant_dot(orc):
+    rng = np.random.default_rng(22)
+    m, out, in_ = 2, 10, 768
+    W = rng.standard_normal(out * in_).astype(np.float32)
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    wq, sc, ds = orc.quantize_weight_q6k(W)
+    xq, xs, bs = orc.quantize_act_q8k(x, m, in_, 16)
+    y = orc.qmatmul_q6k(xq, xs, bs, wq, sc, ds, m, in_, out).reshape(m, out)
+    a1 = ds.astype(np.float64).repeat(16).reshape(out, -1) * sc.reshape(out, -1).astype(np.float64)
+    wexact = (a1[:, :, None] * (wq.reshape(out, -1, 16).astype(np.float64) - 32.0)).reshape(out, in_)
+    xexact = (xs.astype(np.float64).reshape(m, -1).repeat(256, axis=1) * xq.reshape(m, in_).astype(np.float64))
+    ref = xexact @ wexact.T
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
+
+
+def test_kquant_encoders_ranges_and_round_trip(orc):
+    rng = np.random.default_rng(23)
+    W = (rng.standard_normal(4 * 512) * rng.uniform(0.01, 3.0, 4 * 512)).astype(np.float32)
+    wq, da, db, aq, bq = orc.quantize_weight_q4k(W)
+    assert aq.max() <= 63 and bq.min() >= -32 and bq.max() <= 31
+    deq = orc.dequant_q4k(wq, da, db, aq, bq, W.size).astype(np.float64)
+    q = np.concatenate([wq.reshape(-1, 16) % 16, wq.reshape(-1, 16) // 16], axis=1).ravel()
+    a1 = (da.astype(np.float64).repeat(8) * aq.astype(np.float64)).repeat(32)
+    inner = (q > 0) & (q < 15)  # unclamped codes: within half a step
+    assert np.all(np.abs(deq - W)[inner] <= a1[inner] / 2 * (1 + 1e-6) + 1e-7)
+    wq6, sc, ds = orc.quantize_weight_q6k(W)
+    assert wq6.max() <= 63 and sc.min() >= 0
+    deq6 = orc.dequant_q6k(wq6, sc, ds, W.size).astype(np.float64)
+    a6 = (ds.astype(np.float64).repeat(16) * sc.astype(np.float64)).repeat(16)
+    inner6 = (wq6 > 0) & (wq6 < 63)
+    assert np.all(np.abs(deq6 - W)[inner6] <= a6[inner6] / 2 * (1 + 1e-6) + 1e-7)
+
+
+@pytest.mark.parametrize("sub", [32, 16])
+def test_quantize_act_q8k_properties(orc, sub):
+    rng = np.random.default_rng(24)
+    m, in_ = 2, 768
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    x[:256] = 0.0  # an all-zero super-block
+    xq, xs, bs = orc.quantize_act_q8k(x, m, in_, sub)
+    sb = x.reshape(-1, 256).astype(np.float64)
+    d = np.max(np.abs(sb), axis=1) / 127.0
+    assert np.array_equal(xs, d.astype(np.float32))
+    assert np.array_equal(bs, xq.reshape(-1, sub).astype(np.int64).sum(axis=1))
+    q = xq.reshape(-1, 256).astype(np.float64)
+    nz = d > 0
+    assert np.all(np.abs(q[nz] * d[nz, None] - sb[nz]) <= d[nz, None] / 2 + 1e-12)
+    assert np.all(xq[:256] == 0)
