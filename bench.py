@@ -223,6 +223,55 @@ def int8_lines(torch, ctx):
     return lines
 
 
+class KquantCase:
+    """rq_qmatmul_q8k of a synthetic K-quant weight with q8_K activations
+    quantized once; `copies` weights rotated."""
+
+    def __init__(self, torch, ctx, fmt, m, k, n, copies=1, seed=0):
+        import raster_amd
+        from raster_amd import workloads as wl
+
+        if fmt == "q4k":
+            arrs = wl.q4k_weights(n, k, seed)
+            self.weights = [raster_amd.QWeight.q4k(*arrs, n, k, ctx) for _ in range(copies)]
+            self.bytes = n * k // 2 + n * (k // 256) * 8 + n * (k // 32) * 2
+        else:
+            arrs = wl.q6k_weights(n, k, seed)
+            self.weights = [raster_amd.QWeight.q6k(*arrs, n, k, ctx) for _ in range(copies)]
+            self.bytes = n * k + n * (k // 256) * 4 + n * (k // 16)
+        x = torch.randn(m * k, device="cuda")
+        self.xq = raster_amd.quantize_act_q8k(ctx, x, k, 32 if fmt == "q4k" else 16)
+        self.y = torch.empty((m, n), device="cuda")
+        self.i = 0
+
+    def step(self):
+        w = self.weights[self.i % len(self.weights)]
+        self.i += 1
+        w.matmul_q8k(*self.xq, y=self.y)
+
+    def destroy(self):
+        for w in self.weights:
+            w.destroy()
+        self.weights = []
+
+
+def kquant_lines(torch, ctx, m=1, k=4096, n=14336):
+    """The K-quant GEMV at the Q4 decode shape: cold / warm GB/s of weight bytes."""
+    lines = {}
+    for fmt in ("q4k", "q6k"):
+        one = KquantCase(torch, ctx, fmt, m, k, n)
+        wb = one.bytes
+        warm_ms, _ = time_graph(torch, one)
+        one.destroy()
+        c = KquantCase(torch, ctx, fmt, m, k, n, copies=copies_for_cold(wb))
+        cold_ms, _ = time_graph(torch, c)
+        c.destroy()
+        lines[f"{fmt}_m{m}_{n}x{k}"] = {"weight_bytes": wb, "cold_us": round(cold_ms * 1e3, 3),
+                                          "cold_GBs": round(wb / cold_ms / 1e6, 1),
+                                          "warm_us": round(warm_ms * 1e3, 3), "warm_GBs": round(wb / warm_ms / 1e6, 1)}
+    return lines
+
+
 def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
     c = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=1)
     ms = time_eager(torch, c, steps, warmup)
@@ -506,6 +555,9 @@ def main():
             f" {result['decoder']['unfused_us_per_step']} us/step unfused")
         log("int8-activation path")
         result["int8"] = i8 = int8_lines(torch, ctx)
+        log("K-quant GEMV")
+        result["kquant"] = kq = kquant_lines(torch, ctx)
+        log("kquant: " + "; ".join(f"{k} cold {v['cold_us']} us {v['cold_GBs']} GB/s" for k, v in kq.items()))
         log(f"int8: quantize {i8['quantize_act_i8']['us']} us {i8['quantize_act_i8']['GBs']} GB/s; "
             f"gemm {i8['gemm_i8_q8_C2_shape']['us']} us {i8['gemm_i8_q8_C2_shape']['TOPs']} TOP/s; "
             f"decode q8 cold {i8['decode_i8_q8_m1_4096x4096']['cold_us']} us, "

@@ -34,6 +34,27 @@ def q4_weights(out: int, in_: int, seed: int = 0):
     return packed, scales
 
 
+def q4k_weights(out: int, in_: int, seed: int = 0):
+    """Synthetic Q4_K arrays in Raster's layout: nibbles U{0..15}, aq U{0..63},
+    bq U{-32..31}, da / db U(0.0005, 0.002) per super-block."""
+    rng = np.random.default_rng(seed)
+    wq = rng.integers(0, 256, size=out * in_ // 2, dtype=np.uint8)
+    da = rng.uniform(0.0005, 0.002, out * (in_ // 256)).astype(np.float32)
+    db = rng.uniform(0.0005, 0.002, out * (in_ // 256)).astype(np.float32)
+    aq = rng.integers(0, 64, size=out * (in_ // 32), dtype=np.uint8)
+    bq = rng.integers(-32, 32, size=out * (in_ // 32), dtype=np.int8)
+    return wq, da, db, aq, bq
+
+
+def q6k_weights(out: int, in_: int, seed: int = 0):
+    """Synthetic Q6_K arrays: codes U{0..63}, sc U{0..127}, ds U(0.00002, 0.0001)."""
+    rng = np.random.default_rng(seed)
+    wq = rng.integers(0, 64, size=out * in_, dtype=np.uint8)
+    sc = rng.integers(0, 128, size=out * (in_ // 16), dtype=np.int8)
+    ds = rng.uniform(0.00002, 0.0001, out * (in_ // 256)).astype(np.float32)
+    return wq, sc, ds
+
+
 def activations(m: int, in_: int, seed: int = 1, dtype: str = "f32") -> np.ndarray:
     """x ~ N(0, 1); for "bf16" the values are rounded to bf16 (returned as f32 values
     that are exactly representable in bf16)."""
