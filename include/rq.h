@@ -282,6 +282,21 @@ int rq_dequant(rq_ctx ctx, rq_weight w, float* w_out, void* stream);
 int rq_qlinear_q8(rq_ctx ctx, const float* x, const int8_t* codes, const float* scales, int64_t m, int64_t in,
                   int64_t out, float* y);
 
+/* Backward-data of the quantized linear, qlinear-q8-dx
+ * (raster/quant/train.clj:110-137, the pullback of qlinear-q8,
+ * train.clj:143-155): dx[m, in] = dy[m, out] . dequant(W), i.e. dx[m, i] =
+ * sum_o scale[o, i/32] * code[o, i] * dy[m, o], each w = scale * code and
+ * w * dy rounded to f32 as Raster does, summed in f32 (Raster: double). Q8_0
+ * or Q4_0 (code = nibble - 8) weights; device f32 buffers, dx 16-byte aligned,
+ * fully overwritten. Splits the reduction over `out` into slices whose partial
+ * sums use per-stream scratch (grown outside capture only, like rq_qmatmul). */
+int rq_qmatmul_dx(rq_ctx ctx, rq_weight w, const float* dy, float* dx, int64_t m, void* stream);
+
+/* qlinear-q8-dx with its own argument list (dy codes scales m in out) on host
+ * arrays: uploads a temporary weight, runs rq_qmatmul_dx, downloads dx. */
+int rq_qlinear_q8_dx(rq_ctx ctx, const float* dy, const int8_t* codes, const float* scales, int64_t m, int64_t in,
+                     int64_t out, float* dx);
+
 #ifdef __cplusplus
 }
 #endif

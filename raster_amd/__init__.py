@@ -6,10 +6,11 @@ quantized-matmul call surface (quant.py).
 """
 from . import _lib
 from .quant import (RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q8_0, Context, QWeight, RqError, context,
-                    decode_attention, dequant_q8_dense, qlinear_q8, quantize_act_i8, quantize_act_q8k)
+                    decode_attention, dequant_q8_dense, qlinear_q8, qlinear_q8_dx, quantize_act_i8,
+                    quantize_act_q8k)
 
 __all__ = [
     "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "quantize_act_q8k",
-    "qlinear_q8", "dequant_q8_dense",
+    "qlinear_q8", "qlinear_q8_dx", "dequant_q8_dense",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]

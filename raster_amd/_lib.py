@@ -52,6 +52,8 @@ SIGNATURES = {
     "rq_decode_attention": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, C.c_double, C.c_double, _p, _p], _i),
     "rq_dequant": ([_p, _p, _p, _p], _i),
     "rq_qlinear_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
+    "rq_qmatmul_dx": ([_p, _p, _p, _p, _i64, _p], _i),
+    "rq_qlinear_q8_dx": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
 }
 
 

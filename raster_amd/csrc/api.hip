@@ -913,4 +913,56 @@ int rq_qlinear_q8(rq_ctx h, const float* x, const int8_t* codes, const float* sc
   return s;
 }
 
+int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m, void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (kquant(w)) return fail(RQ_ERR_DTYPE, "rq_qmatmul_dx supports Q8_0 and Q4_0 weights");
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
+  if (!dy || !dx) return fail(RQ_ERR_NULL, "dy or dx is NULL");
+  if (((uintptr_t)dy & 3) != 0) return fail(RQ_ERR_SHAPE, "dy must be 4-byte aligned");
+  if (((uintptr_t)dx & 15) != 0) return fail(RQ_ERR_SHAPE, "dx must be 16-byte aligned");
+  if (int s = set_device(c)) return s;
+  const hipStream_t st = (hipStream_t)stream;
+  const int slices = dx_slices(w.in, w.npad, c->cu_count);
+  float* part = nullptr;
+  if (slices > 1) {
+    int* cnt = nullptr;
+    if (int s = stream_split(c, st, 0, (size_t)slices * (size_t)m * (size_t)w.in * 4, &cnt, &part)) return s;
+  }
+  const auto ev = timing_pair(c, st);
+  if (ev.first) (void)hipEventRecord(ev.first, st);
+  hipError_t e = launch_dx(w, dy, dx, m, part, slices, st);
+  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, st);
+  timing_done(c, ev, e == hipSuccess);
+  if (e != hipSuccess) return hip_fail(e, "dx launch");
+  return RQ_OK;
+}
+
+int rq_qlinear_q8_dx(rq_ctx h, const float* dy, const int8_t* codes, const float* scales, int64_t m, int64_t in,
+                     int64_t out, float* dx) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!dy || !codes || !scales || !dx) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  rq_weight w = nullptr;
+  if (int s = rq_weight_create_q8(h, codes, scales, out, in, &w)) return s;
+  void *ddy = nullptr, *ddx = nullptr;
+  int s = rq_buf_alloc(h, (size_t)(m * out) * 4, &ddy);
+  if (!s) s = rq_buf_alloc(h, (size_t)(m * in) * 4, &ddx);
+  if (!s) s = rq_upload(h, ddy, dy, (size_t)(m * out) * 4, nullptr);
+  if (!s) s = rq_qmatmul_dx(h, w, static_cast<const float*>(ddy), static_cast<float*>(ddx), m, nullptr);
+  if (!s) s = rq_download(h, dx, ddx, (size_t)(m * in) * 4, nullptr);
+  std::string keep = s ? t_err : std::string();
+  if (ddy) rq_buf_free(h, ddy);
+  if (ddx) rq_buf_free(h, ddx);
+  rq_weight_destroy(w);
+  if (s) t_err = keep;
+  return s;
+}
+
 }  // extern "C"

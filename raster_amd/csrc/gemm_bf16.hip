@@ -524,12 +524,14 @@ static hipError_t launch_wl(const MatmulArgs& a) {
 // 256 x 64 tiles and 4-deep rings (two workgroups per CU) is 8 to 25% faster
 // than 128 x 128 per-wave weights, whose tile suits smaller M. (Deeper rings
 // make the compiler wait for every load and 6 or more shared fragments per
-// tile were slower still.)
+// tile were slower still.) For M <= 64 the weight stream is latency-bound:
+// 64 x 64 tiles (twice the workgroups of 64 x 128) measured 126 against
+// 151 us (Q4) and 68 against 81 us (Q8) at M = 32, K = 8192, N = 28672.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   (void)cu_count;
   if (a.m > 128) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
-  if (a.m <= 64) return launch_t<FMT, ST, 4, 2>(a);
+  if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);
   return launch_t<FMT, ST, 8, 2>(a);
 }
 

@@ -143,6 +143,11 @@ size_t kquant_gemv_lds(int format, int64_t k, int mt);
 hipError_t launch_kquant_gemv(const Weight& w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
                               int y_dtype, int64_t m, int cu_count, hipStream_t stream);
 hipError_t launch_kquant_dequant(const Weight& w, float* out, hipStream_t stream);
+// backward-data (dx.hip): row-group slices and the launch (part: slices * m * in
+// f32 when slices > 1)
+int dx_slices(int64_t in, int64_t npad, int cu_count);
+hipError_t launch_dx(const Weight& w, const float* dy, float* dx, int64_t m, float* part, int slices,
+                     hipStream_t stream);
 // RoPE + KV append + single-query attention for one decode step (attention.hip).
 size_t decode_attention_lds(int64_t pos, int64_t head_dim);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,

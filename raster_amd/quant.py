@@ -4,6 +4,7 @@ Names, argument order and result shapes follow the reference functions
 (paths inside replikativ/raster):
 
   qlinear_q8(x, codes, scales, m, in_, out) -> y[m*out]   raster/quant/train.clj:77-108
+  qlinear_q8_dx(dy, codes, scales, m, in_, out) -> dx[m*in]  raster/quant/train.clj:110-137
   dequant_q8_dense(codes, scales, in_, out) -> W[out*in]  raster/quant/train.clj:60-71
 
 plus the resident-weight object the GPU path needs (`QWeight`, the :constant
@@ -24,7 +25,7 @@ from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q4_K, RQ_Q6_K, RQ_Q8_0, R
 
 __all__ = [
     "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "quantize_act_q8k",
-    "qlinear_q8", "dequant_q8_dense",
+    "qlinear_q8", "qlinear_q8_dx", "dequant_q8_dense",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]
 
@@ -287,6 +288,23 @@ class QWeight:
              C.c_void_p(bsums.data_ptr()), C.c_void_p(y.data_ptr()), _dtype_code(y), m, _stream_ptr(stream))
         return y
 
+    def matmul_dx(self, dy, dx=None, stream=None):
+        """rq_qmatmul_dx (qlinear-q8-dx): dx[m, in] = dy[m, out] . dequant(W), f32."""
+        import torch
+
+        _need(dy.is_cuda and dy.is_contiguous() and dy.dtype == torch.float32 and dy.numel() % self.out == 0,
+              "dy must be a contiguous f32 CUDA tensor of m*out elements")
+        m = dy.numel() // self.out
+        if dx is None:
+            dx = torch.empty((m, self.in_), dtype=torch.float32, device=dy.device)
+        _need(dx.is_cuda and dx.is_contiguous() and dx.dtype == torch.float32 and dx.numel() == m * self.in_,
+              "dx must be a contiguous f32 [m, in] CUDA tensor")
+        if stream is None:
+            stream = torch.cuda.current_stream(dy.device)
+        call("rq_qmatmul_dx", self.ctx.handle, self.handle, C.c_void_p(dy.data_ptr()), C.c_void_p(dx.data_ptr()), m,
+             _stream_ptr(stream))
+        return dx
+
     def dequant(self, stream=None):
         """Dequantized f32 W[out, in] computed on the device."""
         import torch
@@ -400,6 +418,18 @@ def qlinear_q8(x, codes, scales, m: int, in_: int, out: int, ctx: Context | None
     y = np.empty(m * out, np.float32)
     call("rq_qlinear_q8", ctx.handle, _np_ptr(x), _np_ptr(codes), _np_ptr(scales), m, in_, out, _np_ptr(y))
     return y
+
+
+def qlinear_q8_dx(dy, codes, scales, m: int, in_: int, out: int, ctx: Context | None = None) -> np.ndarray:
+    """raster.quant.train/qlinear-q8-dx: dx[m*in] = dy[m*out] . dequant(codes, scales), on the GPU."""
+    ctx = ctx or context()
+    dy = np.ascontiguousarray(dy, np.float32)
+    codes, scales = np.ascontiguousarray(codes, np.int8), np.ascontiguousarray(scales, np.float32)
+    _need(dy.size == m * out and codes.size == out * in_ and scales.size == out * (in_ // 32),
+          "array sizes do not match m, in, out")
+    dx = np.empty(m * in_, np.float32)
+    call("rq_qlinear_q8_dx", ctx.handle, _np_ptr(dy), _np_ptr(codes), _np_ptr(scales), m, in_, out, _np_ptr(dx))
+    return dx
 
 
 def dequant_q8_dense(codes, scales, in_: int, out: int, ctx: Context | None = None) -> np.ndarray:
