@@ -745,6 +745,11 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
     if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
+  } else if (!plan.ok && x_dtype == kXtI8) {
+    // fragment-major int8 activations with their scales and sums: 640 B per
+    // 16-row tile and 32-block
+    const size_t bytes = (size_t)((m + 15) / 16) * (size_t)(w.in / 32) * 640;
+    if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
   }
   const auto ev = timing_pair(c, a.stream);
   a.ev_main[0] = ev.first;

@@ -10,14 +10,17 @@
 // (Raster adds in double; the f32 sum differs from it by rounding only).
 //
 // Operands: A = weights (16 rows o x 32 k, one chunk of the chunked layout,
-// 8 bytes per lane, one coalesced load), B = activations (32 k x 16 rows t,
-// 8 bytes per lane from row-major xq). Lane (t = lane % 16, q = lane / 16)
-// of the result holds y[t][o0 + 4q .. 4q + 3]: four outputs of one
-// activation row, stored together.
+// 8 bytes per lane, one coalesced load), B = activations (32 k x 16 rows t).
+// A packing pass first rewrites xq / xs / xsum fragment-major: per 16-row
+// tile and block, the 512 code bytes in operand-lane order, then the 16 rows'
+// xs and xsum (640 bytes), so every activation load is contiguous (row-major
+// fragments would touch 16 cache lines per load). Lane (t = lane % 16,
+// q = lane / 16) of the result holds y[t][o0 + 4q .. 4q + 3]: four outputs of
+// one activation row, stored together.
 //
-// Workgroup: 4 waves in a 2 x 2 arrangement over a 64 (o) x 64 (t) tile, each
-// wave 2 x 2 MFMA tiles; the next block's operands and scales are loaded
-// while the current block's MFMAs and scaling run.
+// Workgroup: 4 waves in a 2 x 2 arrangement, each wave TO x TT MFMA tiles
+// (16 rows each along o and t); a ring of R blocks keeps the loads of the next
+// R - 1 blocks in flight while a block's MFMAs and scaling run.
 #include "rq_internal.h"
 
 namespace rq {
@@ -25,18 +28,44 @@ namespace rq {
 namespace {
 
 constexpr int kI8Threads = 256;
+// per-wave tile (16-row MFMA tiles along o and t) and blocks in flight
+constexpr int kI8To = 4, kI8Tt = 2, kI8Ring = 4;
 
 typedef long i64x1;
 
 }  // namespace
 
-template <int FMT, typename ST>
+constexpr int kI8Frag = 640;  // packed bytes per (16-row tile, block)
+
+// Fragment-major copy of int8 activations: one thread per (tile, block, lane):
+// the 8 codes of row 16 tile + lane % 16, k group lane / 16, then (lanes < 16)
+// the row's xs and xsum. Rows past M are zero.
+__global__ __launch_bounds__(256) void pack_i8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                     const int32_t* __restrict__ xsum, uint8_t* __restrict__ xp,
+                                                     int M, int K, int64_t nfrag) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t f = i >> 6;
+  if (f >= nfrag) return;
+  const int lane = (int)(i & 63), nb = K / 32;
+  const int64_t tile = f / nb;
+  const int b = (int)(f % nb);
+  const int64_t t = tile * 16 + (lane & 15);
+  uint8_t* dst = xp + f * kI8Frag;
+  u32x2 v = u32x2{0u, 0u};
+  if (t < M) v = *reinterpret_cast<const u32x2*>(xq + t * K + 32 * b + 8 * (lane >> 4));
+  *reinterpret_cast<u32x2*>(dst + lane * 8) = v;
+  if (lane < 16) {
+    reinterpret_cast<float*>(dst + 512)[lane] = t < M ? xs[t * nb + b] : 0.0f;
+    reinterpret_cast<int32_t*>(dst + 576)[lane] = t < M && xsum ? xsum[t * nb + b] : 0;
+  }
+}
+
+template <int FMT, typename ST, int TO, int TT, int R>
 __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                            const int8_t* __restrict__ xq,
-                                                            const float* __restrict__ xs,
-                                                            const int32_t* __restrict__ xsum, void* __restrict__ y,
+                                                            const uint8_t* __restrict__ xp, void* __restrict__ y,
                                                             int M, int K, int N, int npad, int y_dtype,
                                                             int tiles_t) {
+  constexpr int BO = 2 * 16 * TO, BT = 2 * 16 * TT;  // workgroup tile: 2 x 2 waves
   const int nb = K / 32;
   // tile order: the activation tiles of one weight tile adjacent, and each
   // XCD (workgroups are dealt round-robin by id) given a contiguous run
@@ -48,27 +77,29 @@ __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __re
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, kg = lane >> 4;  // operand row / column, 8-element k group
   const int g_last = npad / 16 - 1;
-  // this wave's two weight groups and two activation tiles
-  int grp[2], trow[2];
+  const int o_base = to * BO + (wave & 1) * 16 * TO, t_base = tt * BT + (wave >> 1) * 16 * TT;
+  // this wave's weight groups and (clamped) packed activation tiles
+  const int t_last = (M + 15) / 16 - 1;
+  int grp[TO];
+  const uint8_t* xt[TT];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    grp[i] = min(to * 4 + (wave & 1) * 2 + i, g_last);
-    trow[i] = min(tt * 64 + (wave >> 1) * 32 + 16 * i + li, M - 1);  // B operand row of this lane
-  }
+  for (int i = 0; i < TO; i++) grp[i] = min(o_base / 16 + i, g_last);
+#pragma unroll
+  for (int j = 0; j < TT; j++) xt[j] = xp + (int64_t)min(t_base / 16 + j, t_last) * nb * kI8Frag;
   constexpr int CB = FMT == RQ_Q8_0 ? 32 : 16;  // code bytes per row and block
 
   struct Ops {
-    uint64_t a[2], b[2];
-    f32x4 ws[2];
-    float xs[2];
-    int xsum[2];
+    uint64_t a[TO], b[TT];
+    f32x4 ws[TO];
+    float xs[TT];
+    int xsum[TT];
   };
-  // block b's operands: weight rows of lane (li) for k group kg, activation
-  // row trow for k group kg; the scales of the 4 weight rows this lane's
-  // results cover (4 kg .. 4 kg + 3 of the group) and of its activation rows
+  // block b's operands: weight rows of lane li for k group kg, activation row
+  // trow for k group kg, the scales of the 4 weight rows this lane's results
+  // cover (4 kg .. 4 kg + 3 of the group) and of its activation rows
   auto load = [&](Ops& o, int b) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < TO; i++) {
       const uint8_t* ch = q + ((int64_t)grp[i] * nb + b) * (16 * CB) + li * CB;
       if (FMT == RQ_Q8_0) {
         o.a[i] = *reinterpret_cast<const uint64_t*>(ch + 8 * kg);
@@ -77,7 +108,6 @@ __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __re
         const uint64_t w = *reinterpret_cast<const uint64_t*>(ch + 8 * (kg & 1));
         o.a[i] = (w >> (4 * (kg >> 1))) & 0x0F0F0F0F0F0F0F0Full;
       }
-      o.b[i] = *reinterpret_cast<const uint64_t*>(xq + (int64_t)trow[i] * K + 32 * b + 8 * kg);
       const ST* s4 = sc + ((int64_t)grp[i] * nb + b) * 16 + 4 * kg;
       if (sizeof(ST) == 4) {
         o.ws[i] = *reinterpret_cast<const f32x4*>(s4);
@@ -86,21 +116,26 @@ __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __re
         o.ws[i] = f32x4{f16_bits_to_f32((uint16_t)(h[0] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(h[0] >> 16)),
                         f16_bits_to_f32((uint16_t)(h[1] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(h[1] >> 16))};
       }
-      o.xs[i] = xs[(int64_t)trow[i] * nb + b];
-      o.xsum[i] = FMT == RQ_Q4_0 ? xsum[(int64_t)trow[i] * nb + b] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < TT; j++) {
+      const uint8_t* fr = xt[j] + (int64_t)b * kI8Frag;
+      o.b[j] = *reinterpret_cast<const uint64_t*>(fr + lane * 8);
+      o.xs[j] = reinterpret_cast<const float*>(fr + 512)[li];
+      o.xsum[j] = FMT == RQ_Q4_0 ? reinterpret_cast<const int32_t*>(fr + 576)[li] : 0;
     }
   };
 
-  f32x4 acc[2][2];
+  f32x4 acc[TO][TT];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TO; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < TT; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](const Ops& o) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TO; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
+      for (int j = 0; j < TT; j++) {
         const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8((i64x1)o.a[i], (i64x1)o.b[j], i32x4{0, 0, 0, 0}, 0,
                                                               0, 0);
 #pragma unroll
@@ -111,24 +146,30 @@ __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __re
       }
   };
 
-  Ops op[2];
-  load(op[0], 0);
-  for (int b = 0; b < nb; b += 2) {
-    load(op[1], min(b + 1, nb - 1));
-    compute(op[0]);
-    if (b + 1 >= nb) break;
-    load(op[0], min(b + 2, nb - 1));
-    compute(op[1]);
+  // a ring of R blocks: block b computes from slot b % R while the loads of
+  // blocks b + 1 .. b + R - 1 are in flight (loads past the last block reread
+  // it and are not used)
+  Ops op[R];
+#pragma unroll
+  for (int u = 0; u < R - 1; u++) load(op[u], min(u, nb - 1));
+  for (int b0 = 0; b0 < nb; b0 += R) {
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int b = b0 + u;
+      if (b >= nb) break;
+      load(op[(u + R - 1) % R], min(b + R - 1, nb - 1));
+      compute(op[u]);
+    }
   }
 
-  // lane (li, kg) holds y[t = row of tile j][o = 16 grp_i + 4 kg + e]
+  // lane (li, kg) holds y[t = row li of tile j][o = 16 grp_i + 4 kg + e]
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int t = tt * 64 + (wave >> 1) * 32 + 16 * j + li;
+  for (int j = 0; j < TT; j++) {
+    const int t = t_base + 16 * j + li;
     if (t >= M) continue;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int o0 = (to * 4 + (wave & 1) * 2 + i) * 16 + 4 * kg;
+    for (int i = 0; i < TO; i++) {
+      const int o0 = o_base + 16 * i + 4 * kg;
       if (o0 >= N) continue;
       if (o0 + 3 < N && (N & 3) == 0) {
         if (y_dtype == RQ_F32) {
@@ -151,23 +192,30 @@ __global__ __launch_bounds__(kI8Threads) void gemm_i8_kernel(const uint8_t* __re
   }
 }
 
-template <int FMT, typename ST>
+template <int FMT, typename ST, int TO, int TT, int R>
 static hipError_t launch_i8_t(const MatmulArgs& a) {
-  const int tiles_t = (int)((a.m + 63) / 64), tiles_o = (int)((a.npad / 16 + 3) / 4);
+  constexpr int BO = 32 * TO, BT = 32 * TT;
+  const int tiles_t = (int)((a.m + BT - 1) / BT), tiles_o = (int)((a.npad + BO - 1) / BO);
   const int64_t grid = (int64_t)tiles_t * tiles_o;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
-  hipExtLaunchKernelGGL((gemm_i8_kernel<FMT, ST>), dim3((unsigned)grid), dim3(kI8Threads), 0, a.stream, a.ev_main[0],
-                        a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), static_cast<const int8_t*>(a.x),
-                        a.ops.act_scale, a.ops.act_sum, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype,
-                        tiles_t);
+  // pack (its end is the timing start: see the bf16 GEMM), then the GEMM
+  const int64_t nfrag = (a.m + 15) / 16 * (a.k / 32);
+  hipExtLaunchKernelGGL(pack_i8_kernel, dim3((unsigned)((nfrag * 64 + 255) / 256)), dim3(256), 0, a.stream, nullptr,
+                        a.ev_main[0], 0, static_cast<const int8_t*>(a.x), a.ops.act_scale, a.ops.act_sum,
+                        static_cast<uint8_t*>(a.scratch), (int)a.m, (int)a.k, nfrag);
+  if (hipError_t e = hipGetLastError()) return e;
+  hipExtLaunchKernelGGL((gemm_i8_kernel<FMT, ST, TO, TT, R>), dim3((unsigned)grid), dim3(kI8Threads), 0, a.stream,
+                        nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        static_cast<const uint8_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype, tiles_t);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count) {
   (void)cu_count;
-  if (a.format == RQ_Q8_0) return launch_i8_t<RQ_Q8_0, float>(a);
-  if (a.scale_dtype == RQ_F16) return launch_i8_t<RQ_Q4_0, uint16_t>(a);
-  return launch_i8_t<RQ_Q4_0, float>(a);
+  if (a.format == RQ_Q8_0) return launch_i8_t<RQ_Q8_0, float, kI8To, kI8Tt, kI8Ring>(a);
+  if (a.scale_dtype == RQ_F16) return launch_i8_t<RQ_Q4_0, uint16_t, kI8To, kI8Tt, kI8Ring>(a);
+  return launch_i8_t<RQ_Q4_0, float, kI8To, kI8Tt, kI8Ring>(a);
 }
 
 }  // namespace rq
