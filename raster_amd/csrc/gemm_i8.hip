@@ -28,8 +28,9 @@ namespace rq {
 namespace {
 
 constexpr int kI8Threads = 256;
-// per-wave tile (16-row MFMA tiles along o and t) and blocks in flight
-constexpr int kI8To = 4, kI8Tt = 2, kI8Ring = 4;
+// per-wave tile along t (16-row MFMA tiles) and blocks in flight; the tile
+// along o is chosen per shape (launch_gemm_i8)
+constexpr int kI8Tt = 4, kI8Ring = 4;
 
 typedef long i64x1;
 
@@ -211,11 +212,29 @@ static hipError_t launch_i8_t(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
+// The per-wave tile along o (TO 16-row tiles, TT = 4 along t): the kernel
+// holds two workgroups per CU, and a grid that needs a second, partial round
+// leaves CUs idle. TO in {2, 3, 4} minimizing rounds x TO (the time of a
+// round grows with TO). Measured at M = 512, K = 4096, N = 11008 (Q8):
+// 32 x 64 tiles 119-134 us (688 workgroups, two rounds), 48 x 64 101 us
+// (460, one round), 64 x 64 125 us (344); 64 x 32 and 32 x 32 were slower.
 hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count) {
-  (void)cu_count;
-  if (a.format == RQ_Q8_0) return launch_i8_t<RQ_Q8_0, float, kI8To, kI8Tt, kI8Ring>(a);
-  if (a.scale_dtype == RQ_F16) return launch_i8_t<RQ_Q4_0, uint16_t, kI8To, kI8Tt, kI8Ring>(a);
-  return launch_i8_t<RQ_Q4_0, float, kI8To, kI8Tt, kI8Ring>(a);
+  const int64_t slots = 2 * (int64_t)cu_count, tiles_t = (a.m + 32 * kI8Tt - 1) / (32 * kI8Tt);
+  int best = 2;
+  int64_t best_cost = INT64_MAX;
+  for (int to = 2; to <= 4; to++) {
+    const int64_t wgs = tiles_t * ((a.npad + 32 * to - 1) / (32 * to));
+    const int64_t cost = (wgs + slots - 1) / slots * to;
+    if (cost < best_cost) best_cost = cost, best = to;
+  }
+#define RQ_I8(FMT_, ST_)                                                               \
+  return best == 2 ? launch_i8_t<FMT_, ST_, 2, kI8Tt, kI8Ring>(a)                      \
+         : best == 3 ? launch_i8_t<FMT_, ST_, 3, kI8Tt, kI8Ring>(a)                    \
+                     : launch_i8_t<FMT_, ST_, 4, kI8Tt, kI8Ring>(a);
+  if (a.format == RQ_Q8_0) { RQ_I8(RQ_Q8_0, float) }
+  if (a.scale_dtype == RQ_F16) { RQ_I8(RQ_Q4_0, uint16_t) }
+  RQ_I8(RQ_Q4_0, float)
+#undef RQ_I8
 }
 
 }  // namespace rq
