@@ -745,6 +745,13 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
     if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
+    if (gemm_sm_takes(w.format, m)) {
+      a.slices = gemm_sm_slices(m, w.in, w.npad, c->cu_count);
+      if (a.slices > 1) {
+        if (int s = stream_split(c, a.stream, 0, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, &a.cnt, &a.part))
+          return s;
+      }
+    }
   } else if (!plan.ok && x_dtype == kXtI8) {
     // fragment-major int8 activations with their scales and sums: 640 B per
     // 16-row tile and 32-block
@@ -756,7 +763,8 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.ev_main[1] = ev.second;
   hipError_t e = plan.ok              ? launch_gemv(a, plan)
                  : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
-                 : x_dtype == RQ_BF16 ? launch_gemm_bf16(a, c->cu_count)
+                 : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m) ? launch_gemm_sm(a, a.slices)
+                                                                    : launch_gemm_bf16(a, c->cu_count))
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");

@@ -112,6 +112,7 @@ struct MatmulArgs {
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
   // and these events take that dispatch's own start and end timestamps
   hipEvent_t ev_main[2] = {nullptr, nullptr};
+  int slices = 1;  // K-slices of the small-m GEMM (partial sums in `part`)
 };
 
 // Decode kernel (m <= 16) launch plan: rows per MFMA group, waves per
@@ -129,6 +130,11 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
+// bf16 x, 16 < m <= 64, weight-stream GEMM with LDS-staged activations
+// (gemm_sm.hip); K-slices and whether it takes a call
+int gemm_sm_slices(int64_t m, int64_t k, int64_t npad, int cu_count);
+bool gemm_sm_takes(int format, int64_t m);
+hipError_t launch_gemm_sm(const MatmulArgs& a, int ks);
 // int8 activations (x_dtype kXtI8, scales / sums in a.ops), m > 16 (gemm_i8.hip)
 hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).

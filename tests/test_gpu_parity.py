@@ -233,6 +233,33 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
     assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
 
 
+@pytest.mark.parametrize("m,in_,out", [(17, 4096, 520), (32, 8192, 256), (48, 2080, 100), (64, 8192, 96),
+                                       (33, 256, 14336), (20, 96, 40)])
+@pytest.mark.parametrize("scale_kind", ["f16", "f32"])
+def test_gemm_small_m_q4_kslices(torch, ctx, orc, m, in_, out, scale_kind):
+    # Q4_0 with bf16 activations and 16 < m <= 64 takes the small-m GEMM: K is
+    # cut into up to 8 slices when the grid would be thin (narrow N, long K),
+    # their partial sums added in slice order, so two calls agree bit for bit.
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=7 * m + out, dtype="bf16")
+    packed, sc16 = wl.q4_weights(out, in_, seed=in_ + out)
+    note(f"gemm-sm q4 {scale_kind} m={m} {out}x{in_}")
+    scales = sc16.view(np.float16) if scale_kind == "f16" else orc.f16_bits_to_f32(sc16)
+    w = raster_amd.QWeight.q4(packed, scales, out, in_, ctx)
+    y32 = run(torch, w, x, m, "bf16", "f32")
+    y32b = run(torch, w, x, m, "bf16", "f32")
+    y16 = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    assert np.array_equal(y32, y32b)
+    assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
+    rows = rows_subset(out, 256)
+    pk = packed.reshape(out, in_ // 2)[rows].ravel()
+    ss = sc16.reshape(out, in_ // 32)[rows].ravel()
+    ref = orc.qlinear_q4(x, pk, ss, m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y32[:, rows], ref) < TOL_BF16
+
+
 # ---------------------------------------------------------------- decode kernel edges
 @pytest.mark.parametrize("m,in_,out", [(1, 32, 16), (3, 96, 40), (16, 160, 33), (5, 4096, 48), (16, 4096, 64)])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
