@@ -24,16 +24,14 @@ struct Ctx {
   int clock_khz;
   std::unordered_set<Weight*> weights;
   std::unordered_set<void*> buffers;
-  // Per-stream scratch, grow-only, freed with the context: the bf16 GEMM's
-  // packed activations, and the decode kernel's K-split counters (kept at zero
-  // between calls) and partial sums. Calls on one stream run in order, so a
-  // stream's buffers are never used by two kernels at once.
+  // Per-stream scratch, grow-only, freed with the context: packed
+  // activations, and the K-split partial sums. Calls on one stream run in
+  // order, so a stream's buffers are never used by two kernels at once.
   struct StreamScratch {
     void* pack = nullptr;
     size_t pack_bytes = 0;
-    void* red = nullptr;   // int counters[red_counters] (256-byte aligned), then partials
+    void* red = nullptr;  // K-split partial sums
     size_t red_bytes = 0;
-    int red_counters = 0;
   };
   std::unordered_map<hipStream_t, StreamScratch> scratch;
   // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
@@ -204,26 +202,15 @@ static int stream_pack(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
   return RQ_OK;
 }
 
-// The decode kernel's K-split buffers for `stream`: `counters` zeroed ints
-// and `part_bytes` of partial sums. A new buffer's counters are zeroed on the
-// stream before first use; every call leaves them at zero again.
-static int stream_split(Ctx* c, hipStream_t stream, int counters, size_t part_bytes, int** cnt, float** part) {
+// The K-split partial sums for `stream`: `part_bytes` (grow-only).
+static int stream_split(Ctx* c, hipStream_t stream, size_t part_bytes, float** part) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto& e = c->scratch[stream];
-  const size_t have_c = align256((size_t)e.red_counters * 4);
-  if (e.red_counters < counters || e.red_bytes < have_c + part_bytes) {
+  if (e.red_bytes < part_bytes) {
     if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
-    const int nc = std::max(counters, e.red_counters);
-    const size_t ncb = align256((size_t)nc * 4);
-    if (int s = regrow(stream, ncb + std::max(part_bytes, e.red_bytes > have_c ? e.red_bytes - have_c : 0),
-                       &e.red, &e.red_bytes))
-      return s;
-    e.red_counters = nc;
-    const hipError_t me = hipMemsetAsync(e.red, 0, ncb, stream);
-    if (me != hipSuccess) return hip_fail(me, "zeroing the decode counters");
+    if (int s = regrow(stream, part_bytes, &e.red, &e.red_bytes)) return s;
   }
-  *cnt = static_cast<int*>(e.red);
-  *part = reinterpret_cast<float*>(static_cast<uint8_t*>(e.red) + align256((size_t)e.red_counters * 4));
+  *part = static_cast<float*>(e.red);
   return RQ_OK;
 }
 
@@ -737,10 +724,9 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.stream = stream;
   a.scratch = nullptr;
   a.part = nullptr;
-  a.cnt = nullptr;
   a.ops = dops;
   if (plan.ok && plan.ksplit > 1) {
-    if (int s = stream_split(c, a.stream, plan.counters, plan.part_bytes, &a.cnt, &a.part)) return s;
+    if (int s = stream_split(c, a.stream, plan.part_bytes, &a.part)) return s;
   } else if (!plan.ok && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
@@ -748,7 +734,7 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     if (gemm_sm_takes(w.format, m)) {
       a.slices = gemm_sm_slices(m, w.in, w.npad, c->cu_count);
       if (a.slices > 1) {
-        if (int s = stream_split(c, a.stream, 0, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, &a.cnt, &a.part))
+        if (int s = stream_split(c, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, &a.part))
           return s;
       }
     }
@@ -942,8 +928,7 @@ int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m,
   const int slices = dx_slices(w.in, w.npad, c->cu_count);
   float* part = nullptr;
   if (slices > 1) {
-    int* cnt = nullptr;
-    if (int s = stream_split(c, st, 0, (size_t)slices * (size_t)m * (size_t)w.in * 4, &cnt, &part)) return s;
+    if (int s = stream_split(c, st, (size_t)slices * (size_t)m * (size_t)w.in * 4, &part)) return s;
   }
   const auto ev = timing_pair(c, st);
   if (ev.first) (void)hipEventRecord(ev.first, st);

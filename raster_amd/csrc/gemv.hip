@@ -225,13 +225,45 @@ __device__ __forceinline__ void quantize_item_a5(const float (&v)[4], bool valid
   store_int8_item(word, valid, mm, b, part, k, lstr, xstr, lev, xsf, xs, (float)d, sum8(s));
 }
 
+// The outputs of 16-row group g held by lane (r, g4) of one wave: v[mg] is
+// y[4 mg + g4][16 g + r] before the fused epilogue, rinv[mg] that row's
+// 1 / rms (input RMSNorm only). SwiGLU: lane r (even) holds the gate row,
+// lane r + 1 the up row; y has N / 2 columns.
+template <int MG>
+__device__ __forceinline__ void store_group(const float (&v)[MG], const float (&rinv)[MG], int g, int lane, void* y,
+                                            int M, int N, int y_dtype, const DecodeOps& ops) {
+  const int r = lane & 15, g4 = lane >> 4;
+  const int o = 16 * g + r;
+  const int ny = ops.swiglu ? N / 2 : N, oy = ops.swiglu ? o / 2 : o;
+#pragma unroll
+  for (int mg = 0; mg < MG; mg++) {
+    const int m = 4 * mg + g4;
+    float out = v[mg];
+    if (ops.norm_gain) out *= rinv[mg];
+    if (ops.swiglu) {
+      const float up = __shfl_down(out, 1, 64);
+      out = out / (1.0f + expf(-out)) * up;
+    }
+    const bool mine = m < M && o < N && (!ops.swiglu || (r & 1) == 0);
+    if (mine) {
+      if (ops.residual)
+        out += y_dtype == RQ_F32 ? static_cast<const float*>(ops.residual)[(int64_t)m * ny + oy]
+                                 : bf16_bits_to_f32(static_cast<const uint16_t*>(ops.residual)[(int64_t)m * ny + oy]);
+      if (y_dtype == RQ_F32)
+        static_cast<float*>(y)[(int64_t)m * ny + oy] = out;
+      else
+        static_cast<uint16_t*>(y)[(int64_t)m * ny + oy] = (uint16_t)f32_to_bf16_bits(out);
+    }
+  }
+}
+
 }  // namespace
 
 template <int FMT, typename ST, int XT, int MT, int WAVES, int NB, int RING>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                            const void* __restrict__ x, void* __restrict__ y, int M,
                                                            int K, int N, int npad, int y_dtype, int ksplit,
-                                                           float* __restrict__ part, int* __restrict__ cnt,
+                                                           float* __restrict__ part,
                                                            DecodeOps ops) {
   constexpr int MG = MT / 4;                 // MFMAs per window (4 activation rows each)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -494,11 +526,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     load_batch(slot, wbeg + (t % nbg) * NB, min(g, ngroups - 1));
   };
   // Combine the waves' partial sums of the group in wave order; lane (r, g4)
-  // of wave 0 owns y[4 mg + g4][16 g + r]. With one slice it stores y. With
-  // several, it stores the slice's partial sums, and the workgroup that
-  // finishes the group's last slice adds all slices' partials in slice order
-  // (a deterministic sum) and stores y. The group's counter is back at zero
-  // when the kernel ends.
+  // of wave 0 owns y[4 mg + g4][16 g + r]. With one slice it stores y; with
+  // several it stores the slice's partial sums, which skinny_reduce_kernel
+  // adds in slice order (workgroup 0 also leaves the rows' sums of squares
+  // there for the input RMSNorm).
   auto finish_group = [&](int t) {
     const int g = gfirst + (t / nbg) * gcols;
 #pragma unroll
@@ -508,61 +539,31 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
     }
     __syncthreads();
     if (wave == 0) {
-      const int o = 16 * g + r;
-      float v[MG];
+      float v[MG], rinv[MG];
 #pragma unroll
       for (int mg = 0; mg < MG; mg++) {
         v[mg] = 0.0f;
 #pragma unroll
         for (int wv = 0; wv < WAVES; wv++) v[mg] += red[(wv * MG + mg) * 64 + lane];
-      }
-      bool store = ksplit == 1;
-      if (!store) {
+        rinv[mg] = 1.0f;
+        const int m = 4 * mg + g4;
+        if (XT != kXtI8 && ops.norm_gain && m < M) {
+          float ssum = 0.0f;
 #pragma unroll
-        for (int mg = 0; mg < MG; mg++) part[((int64_t)s * ngroups + g) * (MG * 64) + mg * 64 + lane] = v[mg];
-        __threadfence();  // release: the partials before the count
-        int old = 0;
-        if (lane == 0) old = atomicAdd(cnt + g, 1);
-        old = __shfl(old, 0, 64);
-        if (old == ksplit - 1) {
-          __threadfence();  // acquire: every slice's partials are visible
-#pragma unroll
-          for (int mg = 0; mg < MG; mg++) {
-            float sum = 0.0f;
-            for (int sl = 0; sl < ksplit; sl++) sum += part[((int64_t)sl * ngroups + g) * (MG * 64) + mg * 64 + lane];
-            v[mg] = sum;
-          }
-          if (lane == 0) __hip_atomic_store(cnt + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          store = true;
+          for (int wv = 0; wv < WAVES; wv++) ssum += nss[wv * MT + m];
+          rinv[mg] = 1.0f / sqrtf(ssum / (float)K + ops.norm_eps);
         }
       }
-      if (store) {
-        // swiglu: lane r (even) holds the gate row, lane r + 1 the up row
-        const int ny = ops.swiglu ? N / 2 : N, oy = ops.swiglu ? o / 2 : o;
+      if (ksplit == 1) {
+        store_group<MG>(v, rinv, g, lane, y, M, N, y_dtype, ops);
+      } else {
 #pragma unroll
-        for (int mg = 0; mg < MG; mg++) {
-          const int m = 4 * mg + g4;
-          float out = v[mg];
-          if (ops.norm_gain && m < M) {
-            float t = 0.0f;
+        for (int mg = 0; mg < MG; mg++) part[((int64_t)s * ngroups + g) * (MG * 64) + mg * 64 + lane] = v[mg];
+        if (XT != kXtI8 && ops.norm_gain && blockIdx.x == 0 && lane < M) {
+          float ssum = 0.0f;
 #pragma unroll
-            for (int wv = 0; wv < WAVES; wv++) t += nss[wv * MT + m];
-            out *= 1.0f / sqrtf(t / (float)K + ops.norm_eps);
-          }
-          if (ops.swiglu) {
-            const float up = __shfl_down(out, 1, 64);
-            out = out / (1.0f + expf(-out)) * up;
-          }
-          const bool mine = m < M && o < N && (!ops.swiglu || (r & 1) == 0);
-          if (mine) {
-            if (ops.residual)
-              out += y_dtype == RQ_F32 ? static_cast<const float*>(ops.residual)[(int64_t)m * ny + oy]
-                                       : bf16_bits_to_f32(static_cast<const uint16_t*>(ops.residual)[(int64_t)m * ny + oy]);
-            if (y_dtype == RQ_F32)
-              static_cast<float*>(y)[(int64_t)m * ny + oy] = out;
-            else
-              static_cast<uint16_t*>(y)[(int64_t)m * ny + oy] = (uint16_t)f32_to_bf16_bits(out);
-          }
+          for (int wv = 0; wv < WAVES; wv++) ssum += nss[wv * MT + lane];
+          part[(int64_t)ksplit * ngroups * (MG * 64) + lane] = ssum;
         }
       }
     }
@@ -585,6 +586,29 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint8_t* __res
   }
 }
 
+// y from the K-slices' partial sums of the decode kernel, added in slice
+// order, then the fused epilogue; one wave per 16-row group
+template <int MT>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ part, void* __restrict__ y, int M,
+                                                            int K, int N, int ngroups, int ksplit, int y_dtype,
+                                                            DecodeOps ops) {
+  constexpr int MG = MT / 4;
+  const int lane = threadIdx.x & 63;
+  const int g = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  if (g >= ngroups) return;  // wave-uniform
+  const float* ss = part + (int64_t)ksplit * ngroups * (MG * 64);
+  float v[MG], rinv[MG];
+#pragma unroll
+  for (int mg = 0; mg < MG; mg++) {
+    float t = 0.0f;
+    for (int sl = 0; sl < ksplit; sl++) t += part[((int64_t)sl * ngroups + g) * (MG * 64) + mg * 64 + lane];
+    v[mg] = t;
+    const int m = 4 * mg + (lane >> 4);
+    rinv[mg] = ops.norm_gain && m < M ? 1.0f / sqrtf(ss[m] / (float)K + ops.norm_eps) : 1.0f;
+  }
+  store_group<MG>(v, rinv, g, lane, y, M, N, y_dtype, ops);
+}
+
 constexpr int kBatch = 4;  // windows per batch
 // batch slots in flight per wave
 template <int FMT>
@@ -601,9 +625,9 @@ constexpr int kRing = 2;
 //    activation decomposition (measured no faster at 6144 and 11264 x 2048).
 //  * A workgroup holds the activations of its K-range in LDS; when the whole
 //    K does not fit, each 16-row group is cut into ksplit K-slices handled by
-//    different workgroups, whose partial sums the last one to finish adds up.
-//    (Splitting only to create more workgroups does not pay: the
-//    cross-workgroup handoff costs more than it gains.)
+//    different workgroups; a second kernel adds their partial sums in slice
+//    order. (Splitting only to create more workgroups does not pay: the
+//    second launch and the partials' round trip cost more than they gain.)
 DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
   DecodePlan p{};
   if (m < 1 || m > 16) return p;
@@ -623,8 +647,8 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count) {
   p.ksplit = (int)ks;
   p.grid = (int)(gcols * ks);
   p.lds_bytes = lds;
-  p.part_bytes = ks > 1 ? (size_t)ks * (size_t)ngroups * (size_t)(p.mt * 16) * 4 : 0;
-  p.counters = ks > 1 ? (int)ngroups : 0;
+  // partial sums, then the rows' sums of squares (mt floats)
+  p.part_bytes = ks > 1 ? ((size_t)ks * (size_t)ngroups * (size_t)(p.mt * 16) + (size_t)p.mt) * 4 : 0;
   p.ok = true;
   return p;
 }
@@ -644,9 +668,17 @@ static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
+  const bool split = p.ksplit > 1;
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(64 * WAVES), (unsigned)p.lds_bytes, a.stream,
-                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales_rb), a.x, a.y, (int)a.m,
-                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.cnt, a.ops);
+                        a.ev_main[0], split ? nullptr : a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales_rb), a.x,
+                        a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.ops);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (split) {
+    const int ngroups = (int)(a.npad / 16);
+    hipExtLaunchKernelGGL(skinny_reduce_kernel<MT>, dim3((unsigned)((ngroups + 3) / 4)), dim3(256), 0, a.stream,
+                          nullptr, a.ev_main[1], 0, a.part, a.y, (int)a.m, (int)a.k, (int)a.n, ngroups, p.ksplit,
+                          a.y_dtype, a.ops);
+  }
   return hipGetLastError();
 }
 
@@ -664,7 +696,7 @@ static hipError_t launch_x(const MatmulArgs& a, const DecodePlan& p) {
 }
 
 hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p) {
-  if (!p.ok || (p.ksplit > 1 && (!a.part || !a.cnt))) return hipErrorInvalidValue;
+  if (!p.ok || (p.ksplit > 1 && !a.part)) return hipErrorInvalidValue;
   if (a.format == RQ_Q8_0) return launch_x<RQ_Q8_0, float>(a, p);
   if (a.scale_dtype == RQ_F16) return launch_x<RQ_Q4_0, uint16_t>(a, p);
   return launch_x<RQ_Q4_0, float>(a, p);

@@ -107,7 +107,6 @@ struct MatmulArgs {
   hipStream_t stream;
   void* scratch;    // bf16 GEMM: ceil(m/16)*16 * k bf16 for the fragment-major activations
   float* part;      // decode with K-split: partial sums, DecodePlan::part_bytes
-  int* cnt;         // decode with K-split: one zeroed counter per 16-row group
   DecodeOps ops = {nullptr, 0.0f, nullptr, 0, 0, nullptr, nullptr};
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
   // and these events take that dispatch's own start and end timestamps
@@ -122,7 +121,6 @@ struct DecodePlan {
   bool ok;
   int mt, waves, ksplit, grid, lds_bytes;
   size_t part_bytes;  // scratch for the slices' partial sums (ksplit > 1)
-  int counters;       // zero-initialised ints, one per 16-row group (ksplit > 1)
 };
 DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 

@@ -118,11 +118,13 @@ def test_fused_residual(torch, ctx, orc, m, in_, out, ydt):
     assert orc.normwise_relerr(y, ref) < (TOL_F32 if ydt == "f32" else TOL_BF16)
 
 
-@pytest.mark.parametrize("m,in_,ffn", [(1, 2048, 5632), (4, 128, 24), (16, 4096, 40), (1, 20480, 8)])
+@pytest.mark.parametrize("m,in_,ffn", [(1, 2048, 5632), (4, 128, 24), (16, 4096, 40), (1, 20480, 8),
+                                       (16, 5632, 24), (9, 14336, 40)])
 @pytest.mark.parametrize("norm", [False, True], ids=["plain", "norm"])
 def test_fused_swiglu(torch, ctx, orc, m, in_, ffn, norm):
     # gate row i and up row i stored as rows 2i / 2i+1; y[m, ffn] =
-    # silu(gate) * up, optionally of the RMSNorm of x
+    # silu(gate) * up, optionally of the RMSNorm of x; (1, 20480), (16, 5632)
+    # and (9, 14336) cut K into slices (the epilogue runs in the reduce kernel)
     import raster_amd
 
     eps = 1e-5

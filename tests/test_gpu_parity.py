@@ -320,10 +320,10 @@ def test_decode_special_activations(torch, ctx, orc):
     assert not np.any(np.isfinite(ref[3])) and not np.any(np.isfinite(ref[4]))
 
 
-@pytest.mark.parametrize("m,in_,out", [(2, 20480, 16), (16, 8192, 48), (9, 4096, 4096)])
+@pytest.mark.parametrize("m,in_,out", [(2, 20480, 16), (16, 8192, 48), (9, 4096, 4096), (16, 14336, 64)])
 def test_decode_k_split(torch, ctx, orc, m, in_, out):
-    # few 16-row groups, or activations too long for one workgroup's LDS: the
-    # decode kernel cuts K into slices whose partial sums one workgroup adds up
+    # activations too long for one workgroup's LDS: the decode kernel cuts K
+    # into slices whose partial sums a second kernel adds in slice order
     import raster_amd
 
     codes, scales = wl.q8_weights(out, in_, seed=8)
