@@ -701,8 +701,9 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
   return run_matmul(c, w, plan, x, x_dtype, y, y_dtype, m, dops, (hipStream_t)stream);
 }
 
-// Launches the matmul of a validated call: the decode kernel when the plan
-// allows it, else the GEMM for the activation dtype; per-stream scratch and
+// Launches the matmul of a validated call: for m <= 16 the int8 decode kernel
+// (for 8 < m <= 16 without fused options, f32 / bf16 x: the MFMA decode
+// kernel), else the GEMM for the activation dtype; per-stream scratch and
 // kernel timing around it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
                       int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream) {
@@ -725,7 +726,13 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.scratch = nullptr;
   a.part = nullptr;
   a.ops = dops;
-  if (plan.ok && plan.ksplit > 1) {
+  const bool plain = !dops.norm_gain && !dops.residual && !dops.swiglu && !dops.act_i8;
+  const MfPlan mf = plain && plan.ok ? plan_gemv_mf(m, w.in, w.npad, x_dtype, c->cu_count) : MfPlan{};
+  if (mf.ok) {
+    if (mf.ks > 1) {
+      if (int s = stream_split(c, a.stream, (size_t)mf.ks * (size_t)m * (size_t)w.out * 4, &a.part)) return s;
+    }
+  } else if (plan.ok && plan.ksplit > 1) {
     if (int s = stream_split(c, a.stream, plan.part_bytes, &a.part)) return s;
   } else if (!plan.ok && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows
@@ -747,7 +754,8 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   const auto ev = timing_pair(c, a.stream);
   a.ev_main[0] = ev.first;
   a.ev_main[1] = ev.second;
-  hipError_t e = plan.ok              ? launch_gemv(a, plan)
+  hipError_t e = mf.ok                ? launch_gemv_mf(a, mf)
+                 : plan.ok            ? launch_gemv(a, plan)
                  : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m) ? launch_gemm_sm(a, a.slices)
                                                                     : launch_gemm_bf16(a, c->cu_count))

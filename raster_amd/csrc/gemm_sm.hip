@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   }
 }
 
-// y = sum over K-slices of the partial sums, in slice order
+// y = sum over K-slices of the partial sums part[s * n + e], in slice order
 __global__ __launch_bounds__(256) void gemm_sm_reduce_kernel(const float* __restrict__ part, void* __restrict__ y,
                                                             int64_t n, int ks, int y_dtype) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -222,6 +222,13 @@ __global__ __launch_bounds__(256) void gemm_sm_reduce_kernel(const float* __rest
     static_cast<uint16_t*>(y)[e] = (uint16_t)f32_to_bf16_bits(t);
 }
 
+hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
+                               hipEvent_t stop) {
+  hipExtLaunchKernelGGL(gemm_sm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, nullptr, stop,
+                        0, part, y, n, ks, y_dtype);
+  return hipGetLastError();
+}
+
 template <int FMT, typename ST, int MT>
 static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
   constexpr int NTW = 1, KC = 8;
@@ -232,12 +239,8 @@ static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
                         static_cast<const uint16_t*>(a.scratch), a.y, a.part, (int)a.m, (int)a.k, (int)a.n,
                         (int)a.npad, a.y_dtype);
   if (hipError_t e = hipGetLastError()) return e;
-  if (ks > 1) {
-    const int64_t n = a.m * a.n;
-    hipExtLaunchKernelGGL(gemm_sm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, a.stream, nullptr,
-                          a.ev_main[1], 0, a.part, a.y, n, ks, a.y_dtype);
-  }
-  return hipGetLastError();
+  if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_main[1]);
+  return hipSuccess;
 }
 
 // K-slices: about 24 waves per CU at m <= 32 (12 above: the 4-tile kernel

@@ -124,6 +124,19 @@ struct DecodePlan {
 };
 DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 
+// Decode on bf16 MFMA with exact codes (gemv_mf.hip): plain calls, f32 / bf16
+// x, 8 < m <= 16 (the kernel takes m <= 16). kw x gw waves per workgroup,
+// wd-step weight ring, ks K-slices, gcols workgroup columns per slice.
+struct MfPlan {
+  bool ok;
+  int kw, gw, wd, ks, gcols;
+};
+MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int cu_count);
+hipError_t launch_gemv_mf(const MatmulArgs& a, const MfPlan& p);
+// y[e] = sum over s < ks of part[s * n + e] (f32 or bf16 y), in slice order
+hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
+                               hipEvent_t stop);
+
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
 hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p);
 hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
