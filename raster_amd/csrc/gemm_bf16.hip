@@ -40,7 +40,7 @@ namespace {
 //      so fg < 2 takes low nibbles and fg >= 2 high nibbles.
 struct WCodes {
   u32x2 v;
-  float s;
+  uint32_t s;  // scale bits, converted at dequantization
 };
 
 template <int FMT, typename ST>
@@ -50,13 +50,13 @@ __device__ __forceinline__ void load_wcodes(WCodes& c, const uint8_t* __restrict
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
   else
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + fr * 16 + 8 * (fg & 1));
-  c.s = load_scale<ST>(sc, chunk * 16 + fr);
+  c.s = load_scale_bits<ST>(sc, chunk * 16 + fr);
 }
 
 // Dequantized fragment (8 bf16): exact f32 scale * code, one RNE rounding to bf16.
-template <int FMT>
+template <int FMT, typename ST>
 __device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
-  const float s = c.s;
+  const float s = scale_from_bits<ST>(c.s);
   uint32_t d[2];
   float off;
   if (FMT == RQ_Q8_0) {
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   RQ_LOAD_A(0, 3);
   RQ_LOAD_A(1, 4);
 #pragma unroll
-  for (int j = 0; j < NTW; j++) wf[0][j] = dequant_frag<FMT>(wc[0][j], fg);
+  for (int j = 0; j < NTW; j++) wf[0][j] = dequant_frag<FMT, ST>(wc[0][j], fg);
   __syncthreads();
   RQ_READ_A(0, 0);
 
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
       _Pragma("unroll") for (int i = 0; i < MT; i++)                                      \
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[(u_) % 2][j], afr[(u_) % 2][i], \
                                                             acc[i][j], 0, 0, 0);          \
-      wf[((u_) + 1) % 2][j] = dequant_frag<FMT>(wc[((u_) + 1) % WD][j], fg);              \
+      wf[((u_) + 1) % 2][j] = dequant_frag<FMT, ST>(wc[((u_) + 1) % WD][j], fg);              \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
     __syncthreads();                                                                      \
@@ -293,10 +293,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
   }
 }
 
-// Workgroup-shared weights: the 4 waves stack along M (MT 16-row activation
-// fragments each, BM = 64 MT rows) and share NT dequantized 16-row weight
+// Workgroup-shared weights: the W waves stack along M (MT 16-row activation
+// fragments each, BM = 16 MT W rows) and share NT dequantized 16-row weight
 // fragments (BN = 16 NT columns) through LDS. Per k-step every weight element
-// is dequantized once per workgroup and each fragment feeds 4 MT MFMAs;
+// is dequantized once per workgroup and each fragment feeds W MT MFMAs;
 // activation fragments go from the fragment-major copy straight into
 // registers (no LDS), since no two waves use the same rows.
 // Pipeline per k-step s (unrolled by R so every ring index is compile-time):
@@ -309,11 +309,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint8_t* __restric
 //         whole turns of every ring)
 //   MFMA: step s, with the weight fragments read during step s-1
 //   one barrier
-template <int FMT, typename ST, int MT, int NT, int R, int WPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_wl_kernel(
+template <int FMT, typename ST, int MT, int NT, int R, int WPE, int W = 4>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_wl_kernel(
     const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
     int M, int K, int N, int npad, int y_dtype, int tiles_m) {
-  constexpr int CW = (NT + 3) / 4;  // weight fragments a wave dequantizes per step (at most)
+  constexpr int CW = (NT + W - 1) / W;  // weight fragments a wave dequantizes per step (at most)
   constexpr int L = R % 4 == 0 ? 4 : 3;
   static_assert(R >= 4 && R % L == 0 && R % 2 == 0, "ring depth: whole turns of the LDS and fragment rings");
   __shared__ __attribute__((aligned(16))) bf16x8 Bs[L][NT][64];
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
   const int nkb = K / 32;
-  const int m0 = tm * (64 * MT) + wave * (16 * MT);  // this wave's first row
+  const int m0 = tm * (16 * MT * W) + wave * (16 * MT);  // this wave's first row
   const int n0 = tn * (16 * NT);
 
   // activation fragment i of this wave (rows m0 + 16 i ..): clamped to the
@@ -340,11 +340,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
   const uint16_t* asrc[MT];
 #pragma unroll
   for (int i = 0; i < MT; i++) asrc[i] = xf + (int64_t)min(m0 / 16 + i, mt_last) * nkb * 512 + lane * 8;
-  // weight fragments this wave dequantizes: c = wave + 4 j < NT
+  // weight fragments this wave dequantizes: c = wave + W j < NT
   const int g_last = npad / 16 - 1;
   int64_t wchunk[CW];
 #pragma unroll
-  for (int j = 0; j < CW; j++) wchunk[j] = (int64_t)min(n0 / 16 + min(wave + 4 * j, NT - 1), g_last) * nkb;
+  for (int j = 0; j < CW; j++) wchunk[j] = (int64_t)min(n0 / 16 + min(wave + W * j, NT - 1), g_last) * nkb;
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -371,8 +371,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
 #define WL_DEQUANT(kb_)                                                                           \
   do {                                                                                            \
     _Pragma("unroll") for (int j = 0; j < CW; j++) {                                              \
-      const bf16x8 d_ = dequant_frag<FMT>(wc[(kb_) % R][j], fg);                                  \
-      if (wave + 4 * j < NT) Bs[(kb_) % L][wave + 4 * j][lane] = d_;                              \
+      const bf16x8 d_ = dequant_frag<FMT, ST>(wc[(kb_) % R][j], fg);                                  \
+      if (wave + W * j < NT) Bs[(kb_) % L][wave + W * j][lane] = d_;                              \
     }                                                                                             \
   } while (0)
 #define WL_READ_B(kb_)                                                                            \
@@ -507,12 +507,12 @@ static hipError_t launch_t(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-template <int FMT, typename ST, int MT, int NT, int R, int WPE>
+template <int FMT, typename ST, int MT, int NT, int R, int WPE, int W = 4>
 static hipError_t launch_wl(const MatmulArgs& a) {
-  const int tiles_m = (int)((a.m + 64 * MT - 1) / (64 * MT));
+  const int tiles_m = (int)((a.m + 16 * MT * W - 1) / (16 * MT * W));
   const int tiles_n = (int)((a.npad / 16 + NT - 1) / NT);
   if (hipError_t e = launch_pack_x(a)) return e;
-  hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R, WPE>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
+  hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R, WPE, W>), dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * W), 0,
                         a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m);
@@ -521,16 +521,37 @@ static hipError_t launch_wl(const MatmulArgs& a) {
 
 // Kernel and tile by M, measured with random data at M = 256, 512, 1024
 // (K 4096 / 8192, N 11008 / 28672): for M > 128 the shared-weight kernel with
-// 256 x 64 tiles and 4-deep rings (two workgroups per CU) is 8 to 25% faster
-// than 128 x 128 per-wave weights, whose tile suits smaller M. (Deeper rings
-// make the compiler wait for every load and 6 or more shared fragments per
-// tile were slower still.) For M <= 64 the weight stream is latency-bound:
-// 64 x 64 tiles (twice the workgroups of 64 x 128) measured 126 against
-// 151 us (Q4) and 68 against 81 us (Q8) at M = 32, K = 8192, N = 28672.
+// 4-deep rings and two waves per SIMD is 8 to 25% faster than 128 x 128
+// per-wave weights, whose tile suits smaller M. (Deeper rings make the
+// compiler wait for every load.) Its tile comes from a cost model: a CU works
+// through ceil(tiles / CUs) tiles on its critical path, whether side by side
+// or one after another, so a tiling costs that count times the tile area.
+// Candidates, ties to the first: 8 waves x 512 x 48 (one workgroup per CU),
+// 4 waves x 256 x 64 and 4 waves x 256 x 48 (two per CU). Measured (Q8, clocks
+// settled): M = 512, K = 4096, N = 11008: 54.2 / 56.7 / 54.5 us; M = 256,
+// K = 8192, N = 28672: 256 x 64 144 us, 256 x 48 197 us; M = 1024, K = 4096,
+// N = 11008: 512 x 48 105.4 us, 256 x 64 108.3 us; the model ranks them the
+// same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
+// (twice the workgroups of 64 x 128) measured 126 against 151 us (Q4) and 68
+// against 81 us (Q8) at M = 32, K = 8192, N = 28672.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
-  (void)cu_count;
-  if (a.m > 128) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
+  if (a.m > 128) {
+    const int64_t bm[3] = {512, 256, 256}, bn[3] = {48, 64, 48};
+    int best = 0;
+    int64_t best_cost = INT64_MAX;
+    for (int i = 0; i < 3; i++) {
+      const int64_t tiles = (a.m + bm[i] - 1) / bm[i] * ((a.npad + bn[i] - 1) / bn[i]);
+      const int64_t cost = (tiles + cu_count - 1) / std::max(cu_count, 1) * bm[i] * bn[i];
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = i;
+      }
+    }
+    if (best == 0) return launch_wl<FMT, ST, 4, 3, 4, 2, 8>(a);
+    if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
+    return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
+  }
   if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);
   return launch_t<FMT, ST, 8, 2>(a);
 }

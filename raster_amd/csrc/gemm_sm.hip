@@ -26,7 +26,7 @@ namespace {
 
 struct WCodesSm {
   u32x2 v;
-  float s;
+  uint32_t s;  // scale bits, converted at dequantization
 };
 
 template <int FMT, typename ST>
@@ -36,14 +36,14 @@ __device__ __forceinline__ void load_wc(WCodesSm& c, const uint8_t* __restrict__
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
   else
     c.v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + fr * 16 + 8 * (fg & 1));
-  c.s = load_scale<ST>(sc, chunk * 16 + fr);
+  c.s = load_scale_bits<ST>(sc, chunk * 16 + fr);
 }
 
 // 8 bf16 of the lane's fragment share: exact f32 scale * code, one RNE
 // rounding (the dequant of gemm_bf16.hip)
-template <int FMT>
+template <int FMT, typename ST>
 __device__ __forceinline__ bf16x8 dequant_sm(const WCodesSm& c, int fg) {
-  const float s = c.s;
+  const float s = scale_from_bits<ST>(c.s);
   uint32_t d[2];
   float off;
   if (FMT == RQ_Q8_0) {
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
       const int slot = buf * KC + u;
       bf16x8 wf[NTW];
 #pragma unroll
-      for (int j = 0; j < NTW; j++) wf[j] = dequant_sm<FMT>(wc[slot][j], fg);
+      for (int j = 0; j < NTW; j++) wf[j] = dequant_sm<FMT, ST>(wc[slot][j], fg);
       load_w(slot, s + WD);
       bf16x8 af[MT];
 #pragma unroll

@@ -195,6 +195,23 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// A block scale as loaded (f32 bits, or f16 bits zero-extended) and its value.
+// Register rings of weights in flight keep the bits and convert when the step
+// is computed: converting at load time makes the compiler wait for the load
+// right there.
+template <typename ST>
+__device__ __forceinline__ uint32_t load_scale_bits(const ST* s, int64_t i);
+template <>
+__device__ __forceinline__ uint32_t load_scale_bits<float>(const float* s, int64_t i) { return __float_as_uint(s[i]); }
+template <>
+__device__ __forceinline__ uint32_t load_scale_bits<uint16_t>(const uint16_t* s, int64_t i) { return s[i]; }
+template <typename ST>
+__device__ __forceinline__ float scale_from_bits(uint32_t b);
+template <>
+__device__ __forceinline__ float scale_from_bits<float>(uint32_t b) { return __uint_as_float(b); }
+template <>
+__device__ __forceinline__ float scale_from_bits<uint16_t>(uint32_t b) { return f16_bits_to_f32((uint16_t)b); }
+
 template <typename ST>
 __device__ __forceinline__ float load_scale(const ST* s, int64_t i);
 template <>

@@ -233,6 +233,35 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
     assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
 
 
+@pytest.mark.parametrize("m,in_,out", [(500, 96, 12004), (300, 416, 12000), (512, 1024, 11008)])
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_gemm_bf16_wide_tiles(torch, ctx, orc, m, in_, out, fmt):
+    # wide N near m = 512: the tile cost model picks the 8-wave 512 x 48 tile
+    # (one workgroup per CU); ragged M and N, 3 and 13 K-blocks
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=m + in_, dtype="bf16")
+    note(f"gemm wide {fmt} bf16 m={m} {out}x{in_}")
+    rows = rows_subset(out, 384)
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=out)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        cs = codes.reshape(out, in_)[rows].ravel()
+        ss = scales.reshape(out, in_ // 32)[rows].ravel()
+        ref = orc.qlinear_q8(x, cs, ss, m, in_, len(rows))
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=out)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+        pk = packed.reshape(out, in_ // 2)[rows].ravel()
+        ss = sc16.reshape(out, in_ // 32)[rows].ravel()
+        ref = orc.qlinear_q4(x, pk, ss, m, in_, len(rows))
+    y32 = run(torch, w, x, m, "bf16", "f32")
+    y16 = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    assert orc.normwise_relerr(y32[:, rows], ref.reshape(m, len(rows))) < TOL_BF16
+    assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
+
+
 @pytest.mark.parametrize("m,in_,out", [(17, 4096, 520), (32, 8192, 256), (48, 2080, 100), (64, 8192, 96),
                                        (33, 256, 14336), (20, 96, 40)])
 @pytest.mark.parametrize("scale_kind", ["f16", "f32"])
