@@ -526,18 +526,19 @@ static hipError_t launch_wl(const MatmulArgs& a) {
 // compiler wait for every load.) Its tile comes from a cost model: a CU works
 // through ceil(tiles / CUs) tiles on its critical path, whether side by side
 // or one after another, so a tiling costs that count times the tile area.
-// Candidates, ties to the first: 8 waves x 512 x 48 (one workgroup per CU),
-// 4 waves x 256 x 64 and 4 waves x 256 x 48 (two per CU). Measured (Q8, clocks
-// settled): M = 512, K = 4096, N = 11008: 54.2 / 56.7 / 54.5 us; M = 256,
-// K = 8192, N = 28672: 256 x 64 144 us, 256 x 48 197 us; M = 1024, K = 4096,
-// N = 11008: 512 x 48 105.4 us, 256 x 64 108.3 us; the model ranks them the
-// same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
+// Candidates, ties to the first: 8 waves x 256 x 96 (two fragments of rows
+// each, one workgroup per CU), 4 waves x 256 x 64 and 4 waves x 256 x 48 (two
+// per CU). Measured (Q8, clocks settled): M = 512, K = 4096, N = 11008:
+// 52.6 / 56.1 / 54.5 us (8 waves x 512 x 48, the same area: 54.8 us, its
+// activation traffic from L2 twice that of 256 x 96); M = 256, K = 8192,
+// N = 28672: 256 x 64 144 us, 256 x 48 197 us, 8 x 256 x 96 191 us; M = 1024:
+// 256 x 96 103 us, 256 x 64 106 to 108 us. The model ranks them the same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
 // (twice the workgroups of 64 x 128) measured 126 against 151 us (Q4) and 68
 // against 81 us (Q8) at M = 32, K = 8192, N = 28672.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   if (a.m > 128) {
-    const int64_t bm[3] = {512, 256, 256}, bn[3] = {48, 64, 48};
+    const int64_t bm[3] = {256, 256, 256}, bn[3] = {96, 64, 48};
     int best = 0;
     int64_t best_cost = INT64_MAX;
     for (int i = 0; i < 3; i++) {
@@ -548,7 +549,7 @@ static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
         best = i;
       }
     }
-    if (best == 0) return launch_wl<FMT, ST, 4, 3, 4, 2, 8>(a);
+    if (best == 0) return launch_wl<FMT, ST, 2, 6, 4, 2, 8>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
     return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
   }
