@@ -88,26 +88,37 @@ __device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
 // multiple of 16 are zero. Row-major fragment loads hit 16 rows one row
 // stride apart (K*2 bytes, which aliases in L1) and use half of each cache
 // line; from xf every fragment is one contiguous kilobyte.
-// One workgroup moves a 16-row x 128-element region (4 k-blocks): it reads
-// 256 contiguous bytes per row (whole cache lines), transposes through LDS
-// (rows padded to 17 pieces against bank conflicts) and writes 4 KB
-// contiguously.
+// One workgroup moves a 16-row x 512-element region (16 k-blocks, 16 KB):
+// each thread reads four 16-byte pieces (16 threads cover 256 contiguous
+// bytes of a row per round), the tile is transposed through LDS (rows padded
+// to 65 pieces against bank conflicts) and written back as 16 contiguous
+// kilobytes, four pieces per thread.
+constexpr int kPackBlocks = 16;  // k-blocks per pack workgroup
 __global__ __launch_bounds__(256) void pack_x_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xf, int M,
                                                     int K) {
-  __shared__ uint4 t[16 * 17];
-  const int nb = K / 32, nq = (nb + 3) / 4;
-  const int tile = blockIdx.x / nq, b0 = (blockIdx.x % nq) * 4;
+  __shared__ uint4 t[16 * (4 * kPackBlocks + 1)];
+  constexpr int PR = 4 * kPackBlocks + 1;  // LDS pieces per row
+  const int nb = K / 32, nq = (nb + kPackBlocks - 1) / kPackBlocks;
+  const int tile = blockIdx.x / nq, b0 = (blockIdx.x % nq) * kPackBlocks;
   const int i = threadIdx.x;
-  {
-    const int r = i >> 4, pp = i & 15;  // row, 16-byte piece of the row's 256 bytes
-    const int m = tile * 16 + r, b = b0 + (pp >> 2);
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (m < M && b < nb) v = *reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * b0 + 8 * pp);
-    t[r * 17 + pp] = v;
+  const int r = i >> 4, pp = i & 15;  // row, piece within a 256-byte round
+  const int m = tile * 16 + r;
+  uint4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int p = pp + 16 * j, b = b0 + (p >> 2);  // piece p of the row's 64
+    v[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (m < M && b < nb) v[j] = *reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * b0 + 8 * p);
   }
+#pragma unroll
+  for (int j = 0; j < 4; j++) t[r * PR + pp + 16 * j] = v[j];
   __syncthreads();
-  const int b = b0 + (i >> 6), l = i & 63, r = l & 15, fg = l >> 4;
-  if (b < nb) *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = t[r * 17 + (i >> 6) * 4 + fg];
+  const int l = i & 63, lr = l & 15, fg = l >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int bb = (i >> 6) + 4 * j, b = b0 + bb;  // block of this store
+    if (b < nb) *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = t[lr * PR + bb * 4 + fg];
+  }
 }
 
 template <int FMT, typename ST, int MT, int NTW, int WD = 6>
@@ -488,7 +499,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
 // microseconds, in front of the GEMM; the GEMM follows the packing pass
 // directly, so its duration is the span between the two end events.
 hipError_t launch_pack_x(const MatmulArgs& a) {
-  const int64_t pack_blocks = (a.m + 15) / 16 * ((a.k / 32 + 3) / 4);
+  const int64_t pack_blocks = (a.m + 15) / 16 * ((a.k / 32 + kPackBlocks - 1) / kPackBlocks);
   hipExtLaunchKernelGGL(pack_x_kernel, dim3((unsigned)pack_blocks), dim3(256), 0, a.stream, nullptr, a.ev_main[0], 0,
                         static_cast<const uint16_t*>(a.x), static_cast<uint16_t*>(a.scratch), (int)a.m, (int)a.k);
   return hipGetLastError();
