@@ -145,11 +145,15 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * m == 0 is a no-op.
  *
  * Numerics (all accumulation in f32):
- *  - m <= 16: int8 MFMA on the raw weight codes. Each 32-block of each
+ *  - m <= 8: int8 MFMA on the raw weight codes. Each 32-block of each
  *    activation row is held as a 16-bit block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
  *    exponent, |X| < 2^15, so the per-element error is <= 2^(e-16) (below
  *    1.6e-5 relative to the block maximum). An inf or NaN activation makes its
  *    row's outputs NaN.
+ *  - 8 < m <= 16: bf16 MFMA on the exact codes (offset so that every code is
+ *    a small integer in bf16), the block scale applied in f32 to each block's
+ *    dot; f32 x split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|). A
+ *    non-finite activation makes its row's outputs non-finite.
  *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
  *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
@@ -159,10 +163,11 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * rq_ctx_destroy; calls on one stream are ordered, calls on different streams
  * do not share it):
  *  - bf16 x with m > 16: the packed activation tile, ceil(m/16)*16*in*2 bytes;
- *  - m <= 16 with activations too long for one workgroup's LDS (in above
- *    17472 at m <= 4, 8704 at m <= 8, 4288 at m <= 16): per-group counters and
- *    the K-slices' partial sums. The counters are zeroed when allocated and every
- *    call leaves them at zero.
+ *  - K-slices' partial sums, m * out * 4 bytes per slice, added in slice
+ *    order by a second kernel: m <= 8 with activations too long for one
+ *    workgroup's LDS (in above 17472 at m <= 4, 8704 at m <= 8); 8 < m <= 16
+ *    when in exceeds about 600 (f32 x; 1200 bf16), up to in / 32 slices;
+ *    Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to 8 slices).
  * Under HIP graph capture nothing can be allocated: run the same (or a
  * larger) shape once on the capturing stream before capturing, otherwise the
  * call fails with RQ_ERR_SHAPE and a message saying so.
