@@ -166,7 +166,8 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *  - K-slices' partial sums, m * out * 4 bytes per slice, added in slice
  *    order by a second kernel: m <= 8 with activations too long for one
  *    workgroup's LDS (in above 17472 at m <= 4, 8704 at m <= 8); 8 < m <= 16
- *    when in exceeds about 600 (f32 x; 1200 bf16), up to in / 32 slices;
+ *    when a slice of x no longer fits two workgroups' LDS (in above 1216 at
+ *    m = 16 with f32 x, up to 4096 at m = 9 with bf16 x), up to in / 32 slices;
  *    Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to 8 slices).
  * Under HIP graph capture nothing can be allocated: run the same (or a
  * larger) shape once on the capturing stream before capturing, otherwise the
