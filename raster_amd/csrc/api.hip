@@ -702,9 +702,9 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
 }
 
 // Launches the matmul of a validated call: for m <= 16 the int8 decode kernel
-// (for 8 < m <= 16 without fused options, f32 / bf16 x: the MFMA decode
-// kernel), else the GEMM for the activation dtype; per-stream scratch and
-// kernel timing around it.
+// (without fused options, f32 / bf16 x: for m = 1 with Q4_0 weights the sdot4
+// GEMV, for 8 < m <= 16 the MFMA decode kernel), else the GEMM for the
+// activation dtype; per-stream scratch and kernel timing around it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
                       int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream) {
   if (int s = set_device(c)) return s;
@@ -728,7 +728,10 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.ops = dops;
   const bool plain = !dops.norm_gain && !dops.residual && !dops.swiglu && !dops.act_i8;
   const MfPlan mf = plain && plan.ok ? plan_gemv_mf(m, w.in, w.npad, x_dtype, c->cu_count) : MfPlan{};
-  if (mf.ok) {
+  const G1Plan g1 = plain && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};
+  if (g1.ok) {
+    // the m = 1 GEMV uses no scratch
+  } else if (mf.ok) {
     if (mf.ks > 1) {
       if (int s = stream_split(c, a.stream, (size_t)mf.ks * (size_t)m * (size_t)w.out * 4, &a.part)) return s;
     }
@@ -754,7 +757,8 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   const auto ev = timing_pair(c, a.stream);
   a.ev_main[0] = ev.first;
   a.ev_main[1] = ev.second;
-  hipError_t e = mf.ok                ? launch_gemv_mf(a, mf)
+  hipError_t e = g1.ok                ? launch_gemv1(a, g1)
+                 : mf.ok              ? launch_gemv_mf(a, mf)
                  : plan.ok            ? launch_gemv(a, plan)
                  : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m) ? launch_gemm_sm(a, a.slices)

@@ -77,50 +77,6 @@ struct SkinnyLds {
   }
 };
 
-template <int XT>
-__device__ __forceinline__ void load_x4(const void* x, int64_t off, bool ok, float (&v)[4]) {
-  if (!ok) {
-    v[0] = v[1] = v[2] = v[3] = 0.0f;
-  } else if (XT == kXtI8) {
-    // four int8 codes, carried as the bits of v[0]
-    v[0] = __uint_as_float(*reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(x) + off));
-    v[1] = v[2] = v[3] = 0.0f;
-  } else if (XT == RQ_F32) {
-    const f32x4 t = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + off);
-    v[0] = t[0];
-    v[1] = t[1];
-    v[2] = t[2];
-    v[3] = t[3];
-  } else {
-    const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(x) + off);
-    v[0] = __uint_as_float(t[0] << 16);
-    v[1] = __uint_as_float(t[0] & 0xFFFF0000u);
-    v[2] = __uint_as_float(t[1] << 16);
-    v[3] = __uint_as_float(t[1] & 0xFFFF0000u);
-  }
-}
-
-// Reductions over the 8 lanes that share a block (lanes 8j..8j+7): swap
-// neighbours, then pairs, then the two quads of the row half (DPP moves, no
-// LDS traffic).
-__device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
-__device__ __forceinline__ int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
-__device__ __forceinline__ int dpp_half_mirror(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
-__device__ __forceinline__ float max8(float v) {
-  v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
-  v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
-  return fmaxf(v, __int_as_float(dpp_half_mirror(__float_as_int(v))));
-}
-__device__ __forceinline__ int or8(int v) {
-  v |= dpp_xor1(v);
-  v |= dpp_xor2(v);
-  return v | dpp_half_mirror(v);
-}
-__device__ __forceinline__ int sum8(int v) {
-  v += dpp_xor1(v);
-  v += dpp_xor2(v);
-  return v + dpp_half_mirror(v);
-}
 
 // A row's 8 block scales of one batch of the row-batched scales.
 template <typename ST>

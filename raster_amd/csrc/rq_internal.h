@@ -133,6 +133,15 @@ struct MfPlan {
 };
 MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int cu_count);
 hipError_t launch_gemv_mf(const MatmulArgs& a, const MfPlan& p);
+// m = 1 decode on v_dot4_i32_i8 for Q4_0 weights (gemv1.hip): plain calls,
+// f32 / bf16 x. waves per workgroup, ring depth, workgroups.
+struct G1Plan {
+  bool ok;
+  int waves, ring, gcols;
+};
+G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count);
+hipError_t launch_gemv1(const MatmulArgs& a, const G1Plan& p);
+
 // y[e] = sum over s < ks of part[s * n + e] (f32 or bf16 y), in slice order
 hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
                                hipEvent_t stop);
@@ -212,6 +221,9 @@ __device__ __forceinline__ float scale_from_bits<float>(uint32_t b) { return __u
 template <>
 __device__ __forceinline__ float scale_from_bits<uint16_t>(uint32_t b) { return f16_bits_to_f32((uint16_t)b); }
 
+__device__ __forceinline__ float scale_value(float s) { return s; }
+__device__ __forceinline__ float scale_value(uint16_t s) { return f16_bits_to_f32(s); }
+
 template <typename ST>
 __device__ __forceinline__ float load_scale(const ST* s, int64_t i);
 template <>
@@ -219,6 +231,53 @@ __device__ __forceinline__ float load_scale<float>(const float* s, int64_t i) { 
 template <>
 __device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* s, int64_t i) {
   return f16_bits_to_f32(s[i]);
+}
+
+// Four consecutive activations of a row as f32 (x_dtype f32 or bf16; for int8
+// x the four codes travel as the bits of v[0]); zeros when !ok.
+template <int XT>
+__device__ __forceinline__ void load_x4(const void* x, int64_t off, bool ok, float (&v)[4]) {
+  if (!ok) {
+    v[0] = v[1] = v[2] = v[3] = 0.0f;
+  } else if (XT == kXtI8) {
+    // four int8 codes, carried as the bits of v[0]
+    v[0] = __uint_as_float(*reinterpret_cast<const uint32_t*>(static_cast<const int8_t*>(x) + off));
+    v[1] = v[2] = v[3] = 0.0f;
+  } else if (XT == RQ_F32) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + off);
+    v[0] = t[0];
+    v[1] = t[1];
+    v[2] = t[2];
+    v[3] = t[3];
+  } else {
+    const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(x) + off);
+    v[0] = __uint_as_float(t[0] << 16);
+    v[1] = __uint_as_float(t[0] & 0xFFFF0000u);
+    v[2] = __uint_as_float(t[1] << 16);
+    v[3] = __uint_as_float(t[1] & 0xFFFF0000u);
+  }
+}
+
+// Reductions over the 8 lanes that share a block (lanes 8j..8j+7): swap
+// neighbours, then pairs, then the two quads of the row half (DPP moves, no
+// LDS traffic).
+__device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_half_mirror(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
+  return fmaxf(v, __int_as_float(dpp_half_mirror(__float_as_int(v))));
+}
+__device__ __forceinline__ int or8(int v) {
+  v |= dpp_xor1(v);
+  v |= dpp_xor2(v);
+  return v | dpp_half_mirror(v);
+}
+__device__ __forceinline__ int sum8(int v) {
+  v += dpp_xor1(v);
+  v += dpp_xor2(v);
+  return v + dpp_half_mirror(v);
 }
 
 // Math/round of a double clamped to [-127, 127] (the int8 quantizers'
