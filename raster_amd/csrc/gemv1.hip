@@ -1,5 +1,6 @@
-// gemv1.hip — decode GEMV for m = 1 (plain rq_qmatmul calls, f32 or bf16 x)
-// on v_dot4_i32_i8, with the numerics of the int8-level decode kernel
+// gemv1.hip — decode GEMV (MR activation rows, planned for m = 1; plain
+// rq_qmatmul calls, f32 or bf16 x) on v_dot4_i32_i8, with the numerics of the
+// int8-level decode kernel
 // (gemv.hip): each 32-block of x is a 16-bit block fixed point X =
 // rint(x * 2^(15-e)) split into two int8 levels X = 256 L0 + L1, and the
 // weight codes enter the integer dots exactly (Q4_0 nibbles 0..15 with the
@@ -39,22 +40,24 @@ struct G1Codes {
 
 }  // namespace
 
-// LDS: levels [nb][64] (L0 then L1, 32 bytes each), factor [nb] f32,
-// level sum [nb] i32, partial sums [2][W][16] f32
-__host__ __device__ inline int g1_lds_bytes(int nb, int waves) { return nb * 72 + 2 * waves * 16 * 4; }
+// LDS: levels [mr][nb][64] (L0 then L1, 32 bytes each), factor [mr][nb] f32,
+// level sum [mr][nb] i32, partial sums [2][W][mr][16] f32
+__host__ __device__ inline int g1_lds_bytes(int nb, int waves, int mr) {
+  return mr * nb * 72 + 2 * waves * mr * 16 * 4;
+}
 
-template <int FMT, typename ST, int XT, int W, int D>
+template <int FMT, typename ST, int XT, int W, int D, int MR>
 __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                      const void* __restrict__ x, void* __restrict__ y, int K, int N,
-                                                      int npad, int y_dtype) {
+                                                      const void* __restrict__ x, void* __restrict__ y, int M, int K,
+                                                      int N, int npad, int y_dtype) {
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;  // blocks per load instruction
   constexpr int CB = FMT == RQ_Q4_0 ? 256 : 512;  // chunk bytes
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int nb = K / 32, ngroups = npad / 16;
   int8_t* lev = reinterpret_cast<int8_t*>(smem);
-  float* fac = reinterpret_cast<float*>(smem + nb * 64);
-  int* sx = reinterpret_cast<int*>(smem + nb * 68);
-  float* red = reinterpret_cast<float*>(smem + nb * 72);
+  float* fac = reinterpret_cast<float*>(smem + MR * nb * 64);
+  int* sx = reinterpret_cast<int*>(smem + MR * nb * 68);
+  float* red = reinterpret_cast<float*>(smem + MR * nb * 72);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15;
@@ -88,16 +91,18 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
     }
   };
 
-  // ---- x into LDS (first round of loads before the weight ring's)
+  // ---- x into LDS (first round of loads before the weight ring's). Item it:
+  // row it / (8 nb), 4 elements; rows past M decompose as zeros.
   constexpr int XI = 4;
-  const int nitems = nb * 8, stride = 64 * W;
+  const int nitems = MR * nb * 8, stride = 64 * W;
   float xv[XI][4];
   auto load_items = [&](int base) {
 #pragma unroll
     for (int i = 0; i < XI; i++) {
       if (base + stride * i >= nitems) break;  // workgroup-uniform
       const int it = min(base + tid + stride * i, nitems - 1);
-      load_x4<XT>(x, (int64_t)it * 4, true, xv[i]);
+      const int mr = it / (nb * 8), rem = it - mr * nb * 8;
+      load_x4<XT>(x, (int64_t)mr * K + rem * 4, mr < M, xv[i]);
     }
   };
   auto convert_items = [&](int base) {
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
       if (base + stride * i >= nitems) break;
       const int it0 = base + tid + stride * i;
       const int it = min(it0, nitems - 1);
-      const int b = it >> 3, part = it & 7;
+      const int b = it >> 3, part = it & 7;  // b counts the rows' blocks in turn: mr * nb + block
       const float* v = xv[i];
       float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
       int bad = !(fabsf(v[0]) <= 3.402823466e38f && fabsf(v[1]) <= 3.402823466e38f &&
@@ -153,7 +158,9 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
   __syncthreads();
 
   // ---- the stream
-  float acc = 0.0f;
+  float acc[MR];
+#pragma unroll
+  for (int mr = 0; mr < MR; mr++) acc[mr] = 0.0f;
   for (int gi = 0; gi < ng; gi++) {
     for (int u0 = 0; u0 < spp; u0 += D) {
 #pragma unroll
@@ -169,65 +176,81 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
           // a short tail load (shifted back to stay inside the row) rereads
           // blocks of the previous step: count each block once
           const bool fresh = st * BPL <= nb - BPL || b >= st * BPL;
-          int c0 = 0, c1 = 0;
-          if (FMT == RQ_Q4_0) {
-            const i32x4 a0 = *reinterpret_cast<const i32x4*>(lev + b * 64);
-            const i32x4 a1 = *reinterpret_cast<const i32x4*>(lev + b * 64 + 16);
-            const i32x4 a2 = *reinterpret_cast<const i32x4*>(lev + b * 64 + 32);
-            const i32x4 a3 = *reinterpret_cast<const i32x4*>(lev + b * 64 + 48);
+          int lo[4], hi[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-              const int lo = (int)(w[k] & 0x0F0F0F0Fu), hi = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
-              c0 = __builtin_amdgcn_sdot4(lo, a0[k], c0, false);
-              c0 = __builtin_amdgcn_sdot4(hi, a1[k], c0, false);
-              c1 = __builtin_amdgcn_sdot4(lo, a2[k], c1, false);
-              c1 = __builtin_amdgcn_sdot4(hi, a3[k], c1, false);
-            }
-            c1 -= 8 * sx[b];
-          } else {
-            const i32x4 a0 = *reinterpret_cast<const i32x4*>(lev + b * 64 + 16 * h);
-            const i32x4 a2 = *reinterpret_cast<const i32x4*>(lev + b * 64 + 32 + 16 * h);
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-              c0 = __builtin_amdgcn_sdot4((int)w[k], a0[k], c0, false);
-              c1 = __builtin_amdgcn_sdot4((int)w[k], a2[k], c1, false);
-            }
+          for (int k = 0; k < 4; k++) {
+            lo[k] = FMT == RQ_Q4_0 ? (int)(w[k] & 0x0F0F0F0Fu) : (int)w[k];
+            hi[k] = (int)((w[k] >> 4) & 0x0F0F0F0Fu);
           }
-          const float t = (float)((c0 << 8) + c1);  // |256 C0 + C1| < 2^24: exact in f32
-          if (fresh) acc = fmaf(t, fac[b] * s, acc);
+#pragma unroll
+          for (int mr = 0; mr < MR; mr++) {
+            const int bb = mr * nb + b;
+            int c0 = 0, c1 = 0;
+            if (FMT == RQ_Q4_0) {
+              const i32x4 a0 = *reinterpret_cast<const i32x4*>(lev + bb * 64);
+              const i32x4 a1 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 16);
+              const i32x4 a2 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 32);
+              const i32x4 a3 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 48);
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
+                c0 = __builtin_amdgcn_sdot4(hi[k], a1[k], c0, false);
+                c1 = __builtin_amdgcn_sdot4(lo[k], a2[k], c1, false);
+                c1 = __builtin_amdgcn_sdot4(hi[k], a3[k], c1, false);
+              }
+              c1 -= 8 * sx[bb];
+            } else {
+              const i32x4 a0 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 16 * h);
+              const i32x4 a2 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 32 + 16 * h);
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
+                c1 = __builtin_amdgcn_sdot4(lo[k], a2[k], c1, false);
+              }
+            }
+            const float t = (float)((c0 << 8) + c1);  // |256 C0 + C1| < 2^24: exact in f32
+            if (fresh) acc[mr] = fmaf(t, fac[bb] * s, acc[mr]);
+          }
         }
       }
     }
     // ---- group gi: the row's lanes, then the waves (in wave order)
-    acc += __shfl_xor(acc, 16, 64);
-    acc += __shfl_xor(acc, 32, 64);
-    float* rb = red + (gi & 1) * W * 16;
-    if (lane < 16) rb[wave * 16 + lane] = acc;
-    acc = 0.0f;
+    float* rb = red + (gi & 1) * W * MR * 16;
+#pragma unroll
+    for (int mr = 0; mr < MR; mr++) {
+      float t = acc[mr];
+      t += __shfl_xor(t, 16, 64);
+      t += __shfl_xor(t, 32, 64);
+      if (lane < 16) rb[(wave * MR + mr) * 16 + lane] = t;
+      acc[mr] = 0.0f;
+    }
     __syncthreads();
     if (wave == 0 && lane < 16) {
-      float t = rb[lane];
-#pragma unroll
-      for (int ww = 1; ww < W; ww++) t += rb[ww * 16 + lane];
       const int o = 16 * ((int)blockIdx.x + gi * (int)gridDim.x) + lane;
-      if (o < N) {
-        if (y_dtype == RQ_F32)
-          static_cast<float*>(y)[o] = t;
-        else
-          static_cast<uint16_t*>(y)[o] = (uint16_t)f32_to_bf16_bits(t);
+#pragma unroll
+      for (int mr = 0; mr < MR; mr++) {
+        float t = rb[mr * 16 + lane];
+#pragma unroll
+        for (int ww = 1; ww < W; ww++) t += rb[(ww * MR + mr) * 16 + lane];
+        if (mr < M && o < N) {
+          if (y_dtype == RQ_F32)
+            static_cast<float*>(y)[(int64_t)mr * N + o] = t;
+          else
+            static_cast<uint16_t*>(y)[(int64_t)mr * N + o] = (uint16_t)f32_to_bf16_bits(t);
+        }
       }
     }
   }
 }
 
 // One configuration (the lab and the dispatcher): gcols workgroups.
-template <int FMT, typename ST, int XT, int W, int D>
+template <int FMT, typename ST, int XT, int W, int D, int MR>
 hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
-  auto kernel = &gemv1_kernel<FMT, ST, XT, W, D>;
+  auto kernel = &gemv1_kernel<FMT, ST, XT, W, D, MR>;
   const int nb = (int)(a.k / 32);
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;
-  if (a.m != 1 || nb < BPL || gcols < 1) return hipErrorInvalidValue;
-  const int lds = g1_lds_bytes(nb, W);
+  if (a.m < 1 || a.m > MR || nb < BPL || gcols < 1) return hipErrorInvalidValue;
+  const int lds = g1_lds_bytes(nb, W, MR);
   if (lds > 163840) return hipErrorInvalidValue;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
@@ -241,8 +264,8 @@ hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
   }
   const int ngroups = (int)(a.npad / 16);
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)std::min(gcols, ngroups)), dim3(64 * W), (unsigned)lds, a.stream,
-                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.k,
-                        (int)a.n, (int)a.npad, a.y_dtype);
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m,
+                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
   return hipGetLastError();
 }
 
@@ -257,7 +280,9 @@ namespace rq {
 // 5.8 us; K = 14336, N = 4096: 10.3 against 14.1 us. 8 waves (16 from
 // K = 12288: 10.3 against 10.8 us), a 2-step ring while a wave has at most 4
 // steps per group, else 4 (deeper rings measured slower), and up to two
-// workgroups per CU (one with 16 waves).
+// workgroups per CU (one with 16 waves). The dot work grows with the rows:
+// at K = 4096, N = 14336, m = 2 took 12.1 against 12.9 us and m = 4 17.2 to
+// 19.4 against 14.5 us, so m > 1 stays with the int8-level kernel.
 G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count) {
   G1Plan p{};
   if (m != 1 || format != RQ_Q4_0 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0) return p;
@@ -265,7 +290,7 @@ G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, i
   if (nb < 4) return p;
   const int64_t nsteps = (nb + 3) / 4;
   p.waves = nsteps >= 96 ? 16 : 8;
-  if (g1_lds_bytes((int)nb, p.waves) > 163840) return p;
+  if (g1_lds_bytes((int)nb, p.waves, 1) > 163840) return p;
   const int64_t spw = (nsteps + p.waves - 1) / p.waves;
   p.ring = spw <= 4 ? 2 : 4;
   p.gcols = (int)std::min<int64_t>(ngroups, (int64_t)cu_count * (p.waves == 16 ? 1 : 2));
@@ -275,10 +300,10 @@ G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, i
 
 template <typename ST, int XT>
 static hipError_t launch_g1_x(const MatmulArgs& a, const G1Plan& p) {
-  if (p.waves == 8 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 2>(a, p.gcols);
-  if (p.waves == 8 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 4>(a, p.gcols);
-  if (p.waves == 16 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 2>(a, p.gcols);
-  if (p.waves == 16 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 4>(a, p.gcols);
+  if (p.waves == 8 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 2, 1>(a, p.gcols);
+  if (p.waves == 8 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 4, 1>(a, p.gcols);
+  if (p.waves == 16 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 2, 1>(a, p.gcols);
+  if (p.waves == 16 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 4, 1>(a, p.gcols);
   return hipErrorInvalidValue;
 }
 
