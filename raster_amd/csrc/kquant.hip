@@ -92,7 +92,7 @@ hipError_t launch_quantize_act_q8k(const float* x, int64_t m, int64_t in, int su
 
 // ---- K-quant GEMV: y[t][o] for MT activation rows t. FMT RQ_Q4_K / RQ_Q6_K.
 // LDS: xq[MT][K] codes, bsums[MT][K/SUB], xs[MT][K/256].
-template <int FMT, int MT>
+template <int FMT, int MT, int D>
 __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
     const uint8_t* __restrict__ wq, const void* __restrict__ sup, const void* __restrict__ subsc,
     const int8_t* __restrict__ xq, const float* __restrict__ xs, const int32_t* __restrict__ bsums,
@@ -116,65 +116,129 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
   for (int i = tid; i < MT * nsb; i += kKqThreads) ls[i] = i / nsb < M ? xs[(int64_t)i] : 0.0f;
   __syncthreads();
 
+  // ---- this wave's work: row groups gi = 0 .. ng-1 (rows o0 = 4 (gw + gi
+  // nwaves) ..), each swept in nit steps (lane: sub-block lane + 64 si). The
+  // steps stream through a D-step register ring of raw code and scale bits
+  // across row groups (steps padded to whole ring turns); nothing converts or
+  // tests loaded bits before the step computes, and refills are unconditional
+  // at clamped addresses, so the compiler keeps D steps of loads in flight.
+  // D = 1 measured best (14336 x 4096, m = 1: Q4_K 11.7 / 12.2 / 13.5 /
+  // 15.5 us and Q6_K 16.9 / 17.4 / 18.9 / 19.0 us at D = 1 .. 4; before this
+  // stream, loading each step only when it was computed: 15.0 and 16.3 us).
   const int gw = (int)blockIdx.x * (kKqThreads / 64) + wave, nwaves = (int)gridDim.x * (kKqThreads / 64);
-  for (int o0 = gw * kKqRows; o0 < N; o0 += nwaves * kKqRows) {
-    float acc[kKqRows][MT];
+  const int ngrp = (N + kKqRows - 1) / kKqRows;
+  const int ng = gw < ngrp ? (ngrp - 1 - gw) / nwaves + 1 : 0;
+  if (ng == 0) return;  // wave-uniform; no barrier follows
+  const int nit = (nsub + 63) / 64, nitp = (nit + D - 1) / D * D;
+  constexpr int CODE_ROW = FMT == RQ_Q4_K ? 1 : 2;  // K * CODE_ROW / 2 code bytes per row
+  struct Slot {
+    u32x4 w[kKqRows];
+    uint32_t a[kKqRows], b[kKqRows], c[kKqRows];  // Q4_K: da, db bits, aq | bq << 8; Q6_K: ds bits, sc
+  };
+  Slot ring[D];
+  auto load = [&](int slot, int gi, int si) {
+    if (gi >= ng) {  // past the end: the last step again
+      gi = ng - 1;
+      si = nitp - 1;
+    }
+    const int o0 = (gw + gi * nwaves) * kKqRows;
+    const int sb = min(lane + 64 * min(si, nit - 1), nsub - 1);
 #pragma unroll
-    for (int r = 0; r < kKqRows; r++)
-#pragma unroll
-      for (int t = 0; t < MT; t++) acc[r][t] = 0.0f;
-    for (int s = lane; s < nsub; s += 64) {
-      // the loads of all rows first, then the math
-      u32x4 w[kKqRows];
-      float f0[kKqRows], f1[kKqRows];
-#pragma unroll
-      for (int r = 0; r < kKqRows; r++) {
-        const int o = min(o0 + r, N - 1);
-        w[r] = *reinterpret_cast<const u32x4*>(wq + (int64_t)o * (K * (FMT == RQ_Q4_K ? 1 : 2) / 2) + s * 16);
-        if (FMT == RQ_Q4_K) {
-          const f32x2 d2 = static_cast<const f32x2*>(sup)[(int64_t)o * nsb + s / 8];
-          const uint32_t ab = static_cast<const uint16_t*>(subsc)[(int64_t)o * nsub + s];
-          f0[r] = d2[0] * (float)(int)(ab & 0xFFu);        // da * aq
-          f1[r] = d2[1] * (float)(int)(int8_t)(ab >> 8);   // db * bq
-        } else {
-          f0[r] = static_cast<const float*>(sup)[(int64_t)o * nsb + s / 16] *
-                  (float)static_cast<const int8_t*>(subsc)[(int64_t)o * nsub + s];  // ds * sc
-          f1[r] = 0.0f;
-        }
+    for (int r = 0; r < kKqRows; r++) {
+      const int o = min(o0 + r, N - 1);
+      ring[slot].w[r] = *reinterpret_cast<const u32x4*>(wq + (int64_t)o * (K * CODE_ROW / 2) + sb * 16);
+      if (FMT == RQ_Q4_K) {
+        const u32x2 d2 = static_cast<const u32x2*>(sup)[(int64_t)o * nsb + sb / 8];
+        ring[slot].a[r] = d2[0];
+        ring[slot].b[r] = d2[1];
+        ring[slot].c[r] = static_cast<const uint16_t*>(subsc)[(int64_t)o * nsub + sb];
+      } else {
+        ring[slot].a[r] = static_cast<const uint32_t*>(sup)[(int64_t)o * nsb + sb / 16];
+        ring[slot].c[r] = (uint32_t)(uint8_t)static_cast<const int8_t*>(subsc)[(int64_t)o * nsub + sb];
       }
+    }
+  };
+  int lg = 0, ls_ = 0;
+  auto advance = [&](int& gi, int& si) {
+    if (++si == nitp) {
+      si = 0;
+      ++gi;
+    }
+  };
 #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        const u32x4 xa = reinterpret_cast<const u32x4*>(lx + t * K)[s * SUB / 16];
-        const int bs = lb[t * nsub + s];
-        const float dact = ls[t * nsb + s * SUB / 256];
-        if (FMT == RQ_Q4_K) {
-          const u32x4 xb = reinterpret_cast<const u32x4*>(lx + t * K)[s * 2 + 1];
+  for (int i = 0; i < D; i++) {
+    load(i, lg, ls_);
+    advance(lg, ls_);
+  }
+
+  float acc[kKqRows][MT];
+#pragma unroll
+  for (int r = 0; r < kKqRows; r++)
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[r][t] = 0.0f;
+  for (int gi = 0; gi < ng; gi++) {
+    for (int si0 = 0; si0 < nitp; si0 += D) {
+#pragma unroll
+      for (int i = 0; i < D; i++) {
+        const int si = si0 + i;
+        const Slot cur = ring[i];
+        load(i, lg, ls_);
+        advance(lg, ls_);
+        const int sraw = lane + 64 * si;
+        if (si < nit) {  // wave-uniform: padding steps compute nothing
+          const bool live = sraw < nsub;
+          const int s = min(sraw, nsub - 1);
+          float f0[kKqRows], f1[kKqRows];
 #pragma unroll
           for (int r = 0; r < kKqRows; r++) {
-            int dp = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              dp = __builtin_amdgcn_sdot4((int)(w[r][i] & 0x0F0F0F0Fu), (int)xa[i], dp, false);
-              dp = __builtin_amdgcn_sdot4((int)((w[r][i] >> 4) & 0x0F0F0F0Fu), (int)xb[i], dp, false);
+            if (FMT == RQ_Q4_K) {
+              f0[r] = __uint_as_float(cur.a[r]) * (float)(int)(cur.c[r] & 0xFFu);        // da * aq
+              f1[r] = __uint_as_float(cur.b[r]) * (float)(int)(int8_t)(cur.c[r] >> 8);   // db * bq
+            } else {
+              f0[r] = __uint_as_float(cur.a[r]) * (float)(int)(int8_t)cur.c[r];          // ds * sc
+              f1[r] = 0.0f;
             }
-            acc[r][t] = fmaf(dact, f0[r] * (float)dp + f1[r] * (float)bs, acc[r][t]);
           }
-        } else {
 #pragma unroll
-          for (int r = 0; r < kKqRows; r++) {
-            int dp = 0;
+          for (int t = 0; t < MT; t++) {
+            const u32x4 xa = reinterpret_cast<const u32x4*>(lx + t * K)[s * SUB / 16];
+            const int bs = lb[t * nsub + s];
+            const float dact = ls[t * nsb + s * SUB / 256];
+            if (FMT == RQ_Q4_K) {
+              const u32x4 xb = reinterpret_cast<const u32x4*>(lx + t * K)[s * 2 + 1];
 #pragma unroll
-            for (int i = 0; i < 4; i++) dp = __builtin_amdgcn_sdot4((int)w[r][i], (int)xa[i], dp, false);
-            acc[r][t] = fmaf(dact * f0[r], (float)(dp - 32 * bs), acc[r][t]);
+              for (int r = 0; r < kKqRows; r++) {
+                int dp = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                  dp = __builtin_amdgcn_sdot4((int)(cur.w[r][k] & 0x0F0F0F0Fu), (int)xa[k], dp, false);
+                  dp = __builtin_amdgcn_sdot4((int)((cur.w[r][k] >> 4) & 0x0F0F0F0Fu), (int)xb[k], dp, false);
+                }
+                const float v = fmaf(dact, f0[r] * (float)dp + f1[r] * (float)bs, acc[r][t]);
+                acc[r][t] = live ? v : acc[r][t];
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < kKqRows; r++) {
+                int dp = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) dp = __builtin_amdgcn_sdot4((int)cur.w[r][k], (int)xa[k], dp, false);
+                const float v = fmaf(dact * f0[r], (float)(dp - 32 * bs), acc[r][t]);
+                acc[r][t] = live ? v : acc[r][t];
+              }
+            }
           }
         }
       }
     }
+    // ---- row group gi: sum the lanes, store
+    const int o0 = (gw + gi * nwaves) * kKqRows;
 #pragma unroll
     for (int r = 0; r < kKqRows; r++)
 #pragma unroll
       for (int t = 0; t < MT; t++) {
         const float v = wave_sum64(acc[r][t]);
+        acc[r][t] = 0.0f;
         const int o = o0 + r;
         if (lane == 0 && o < N && t < M) {
           if (y_dtype == RQ_F32)
@@ -185,16 +249,15 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
       }
   }
 }
-
 size_t kquant_gemv_lds(int format, int64_t k, int mt) {
   const int64_t sub = format == RQ_Q4_K ? 32 : 16;
   return (size_t)mt * (size_t)(k + 4 * (k / sub) + 4 * (k / 256));
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, int D = 1>
 static hipError_t launch_kq_t(const Weight& w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
                               int y_dtype, int64_t m, int cu_count, hipStream_t stream) {
-  auto kernel = &kquant_gemv_kernel<FMT, MT>;
+  auto kernel = &kquant_gemv_kernel<FMT, MT, D>;
   const size_t lds = kquant_gemv_lds(FMT, w.in, MT);
   if (lds > 65536) {
     static std::atomic<uint64_t> attr_set{0};
