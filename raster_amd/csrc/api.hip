@@ -702,9 +702,10 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
 }
 
 // Launches the matmul of a validated call: for m <= 16 the int8 decode kernel
-// (without fused options, f32 / bf16 x: for m = 1 with Q4_0 weights the sdot4
-// GEMV, for 8 < m <= 16 the MFMA decode kernel), else the GEMM for the
-// activation dtype; per-stream scratch and kernel timing around it.
+// (for m = 1 with Q4_0 weights the sdot4 GEMV instead, unless a norm,
+// residual or SwiGLU is fused; for 8 < m <= 16 without fused options, f32 /
+// bf16 x, the MFMA decode kernel), else the GEMM for the activation dtype;
+// per-stream scratch and kernel timing around it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
                       int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream) {
   if (int s = set_device(c)) return s;
@@ -728,7 +729,9 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.ops = dops;
   const bool plain = !dops.norm_gain && !dops.residual && !dops.swiglu && !dops.act_i8;
   const MfPlan mf = plain && plan.ok ? plan_gemv_mf(m, w.in, w.npad, x_dtype, c->cu_count) : MfPlan{};
-  const G1Plan g1 = plain && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};
+  // the m = 1 GEMV also quantizes to int8 blocks itself (act_i8)
+  const bool plain_g1 = !dops.norm_gain && !dops.residual && !dops.swiglu;
+  const G1Plan g1 = plain_g1 && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};
   if (g1.ok) {
     // the m = 1 GEMV uses no scratch
   } else if (mf.ok) {

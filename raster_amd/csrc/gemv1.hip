@@ -5,7 +5,11 @@
 // rint(x * 2^(15-e)) split into two int8 levels X = 256 L0 + L1, and the
 // weight codes enter the integer dots exactly (Q4_0 nibbles 0..15 with the
 // zero point folded as -8 * sum X). Per block: the int32 dot 256 C0 + C1
-// (- 8 sum X), then f32 (2^(e-15) * scale) times it.
+// (- 8 sum X), then f32 (2^(e-15) * scale) times it. Int8 activations
+// (rq_qmatmul_i8: Raster's quantize-act-i8 blocks) are the single level L1,
+// with their block scale as the factor and their code sum as sum X; with
+// act_i8 the kernel makes those blocks itself from f32 / bf16 x, by the math
+// of quantize_act_i8_kernel (bitwise its codes, scales and sums).
 //
 // Memory: one load instruction moves 1 KB of codes. A Q4_0 lane takes the
 // 16-byte row r of one chunk (4 consecutive chunks per wave, lane
@@ -48,8 +52,10 @@ __host__ __device__ inline int g1_lds_bytes(int nb, int waves, int mr) {
 
 template <int FMT, typename ST, int XT, int W, int D, int MR>
 __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                      const void* __restrict__ x, void* __restrict__ y, int M, int K,
-                                                      int N, int npad, int y_dtype) {
+                                                      const void* __restrict__ x, const float* __restrict__ axs,
+                                                      const int32_t* __restrict__ axsum, int act_i8,
+                                                      void* __restrict__ y, int M, int K, int N, int npad,
+                                                      int y_dtype) {
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;  // blocks per load instruction
   constexpr int CB = FMT == RQ_Q4_0 ? 256 : 512;  // chunk bytes
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -103,6 +109,12 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
       const int it = min(base + tid + stride * i, nitems - 1);
       const int mr = it / (nb * 8), rem = it - mr * nb * 8;
       load_x4<XT>(x, (int64_t)mr * K + rem * 4, mr < M, xv[i]);
+      if (XT == kXtI8) {
+        // the block's scale and code sum ride along in v[1], v[2], loaded
+        // with the codes (not at the conversion, one more round trip)
+        xv[i][1] = mr < M ? axs[it >> 3] : 0.0f;
+        xv[i][2] = __int_as_float(mr < M && axsum ? axsum[it >> 3] : 0);
+      }
     }
   };
   auto convert_items = [&](int base) {
@@ -112,7 +124,41 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
       const int it0 = base + tid + stride * i;
       const int it = min(it0, nitems - 1);
       const int b = it >> 3, part = it & 7;  // b counts the rows' blocks in turn: mr * nb + block
+      if (XT == kXtI8) {
+        if (it0 < nitems) {
+          *reinterpret_cast<uint32_t*>(lev + b * 64 + part * 4) = 0u;
+          *reinterpret_cast<uint32_t*>(lev + b * 64 + 32 + part * 4) = __float_as_uint(xv[i][0]);
+          if (part == 0) {
+            fac[b] = xv[i][1];
+            sx[b] = __float_as_int(xv[i][2]);
+          }
+        }
+        continue;
+      }
       const float* v = xv[i];
+      if (act_i8) {
+        const float qmax = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const double d = (double)qmax / 127.0;
+        const double id = d == 0.0 ? 0.0 : 1.0 / d;
+        uint32_t word = 0u;
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int qv = java_round_clamp127((double)v[k] * id);
+          word |= (uint32_t)(qv & 0xFF) << (8 * k);
+          s += qv;
+        }
+        s = sum8(s);
+        if (it0 < nitems) {
+          *reinterpret_cast<uint32_t*>(lev + b * 64 + part * 4) = 0u;
+          *reinterpret_cast<uint32_t*>(lev + b * 64 + 32 + part * 4) = word;
+          if (part == 0) {
+            fac[b] = (float)d;
+            sx[b] = s;
+          }
+        }
+        continue;
+      }
       float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
       int bad = !(fabsf(v[0]) <= 3.402823466e38f && fabsf(v[1]) <= 3.402823466e38f &&
                   fabsf(v[2]) <= 3.402823466e38f && fabsf(v[3]) <= 3.402823466e38f);
@@ -193,8 +239,10 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
               const i32x4 a3 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 48);
 #pragma unroll
               for (int k = 0; k < 4; k++) {
-                c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
-                c0 = __builtin_amdgcn_sdot4(hi[k], a1[k], c0, false);
+                if (XT != kXtI8) {  // int8 activations: level 0 is zero
+                  c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
+                  c0 = __builtin_amdgcn_sdot4(hi[k], a1[k], c0, false);
+                }
                 c1 = __builtin_amdgcn_sdot4(lo[k], a2[k], c1, false);
                 c1 = __builtin_amdgcn_sdot4(hi[k], a3[k], c1, false);
               }
@@ -204,7 +252,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
               const i32x4 a2 = *reinterpret_cast<const i32x4*>(lev + bb * 64 + 32 + 16 * h);
 #pragma unroll
               for (int k = 0; k < 4; k++) {
-                c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
+                if (XT != kXtI8) c0 = __builtin_amdgcn_sdot4(lo[k], a0[k], c0, false);
                 c1 = __builtin_amdgcn_sdot4(lo[k], a2[k], c1, false);
               }
             }
@@ -250,6 +298,7 @@ hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
   const int nb = (int)(a.k / 32);
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;
   if (a.m < 1 || a.m > MR || nb < BPL || gcols < 1) return hipErrorInvalidValue;
+  if (XT == kXtI8 && !a.ops.act_scale) return hipErrorInvalidValue;
   const int lds = g1_lds_bytes(nb, W, MR);
   if (lds > 163840) return hipErrorInvalidValue;
   static std::atomic<uint64_t> attr_set{0};
@@ -264,8 +313,8 @@ hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
   }
   const int ngroups = (int)(a.npad / 16);
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)std::min(gcols, ngroups)), dim3(64 * W), (unsigned)lds, a.stream,
-                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.y, (int)a.m,
-                        (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.ops.act_scale,
+                        a.ops.act_sum, a.ops.act_i8, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
   return hipGetLastError();
 }
 
@@ -285,7 +334,8 @@ namespace rq {
 // 19.4 against 14.5 us, so m > 1 stays with the int8-level kernel.
 G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count) {
   G1Plan p{};
-  if (m != 1 || format != RQ_Q4_0 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0) return p;
+  if (m != 1 || format != RQ_Q4_0 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16 && x_dtype != kXtI8) || k % 32 != 0)
+    return p;
   const int64_t nb = k / 32, ngroups = npad / 16;
   if (nb < 4) return p;
   const int64_t nsteps = (nb + 3) / 4;
@@ -307,11 +357,15 @@ static hipError_t launch_g1_x(const MatmulArgs& a, const G1Plan& p) {
   return hipErrorInvalidValue;
 }
 
+template <typename ST>
+static hipError_t launch_g1_s(const MatmulArgs& a, const G1Plan& p) {
+  if (a.x_dtype == kXtI8) return launch_g1_x<ST, kXtI8>(a, p);
+  return a.x_dtype == RQ_F32 ? launch_g1_x<ST, RQ_F32>(a, p) : launch_g1_x<ST, RQ_BF16>(a, p);
+}
+
 hipError_t launch_gemv1(const MatmulArgs& a, const G1Plan& p) {
   if (!p.ok || a.format != RQ_Q4_0) return hipErrorInvalidValue;
-  if (a.scale_dtype == RQ_F16)
-    return a.x_dtype == RQ_F32 ? launch_g1_x<uint16_t, RQ_F32>(a, p) : launch_g1_x<uint16_t, RQ_BF16>(a, p);
-  return a.x_dtype == RQ_F32 ? launch_g1_x<float, RQ_F32>(a, p) : launch_g1_x<float, RQ_BF16>(a, p);
+  return a.scale_dtype == RQ_F16 ? launch_g1_s<uint16_t>(a, p) : launch_g1_s<float>(a, p);
 }
 
 }  // namespace rq

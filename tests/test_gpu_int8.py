@@ -140,7 +140,8 @@ def run_i8(torch, ctx, orc, fmt, m, in_, out, seed, ydt="f32"):
     return y, r
 
 
-@pytest.mark.parametrize("m,in_,out", [(1, 4096, 4096), (3, 96, 40), (16, 4096, 64), (2, 20480, 32), (5, 160, 33)])
+@pytest.mark.parametrize("m,in_,out", [(1, 4096, 4096), (3, 96, 40), (16, 4096, 64), (2, 20480, 32), (5, 160, 33),
+                                       (1, 160, 33), (1, 14336, 64), (1, 416, 520)])
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q4f32"])
 def test_qmatmul_i8_decode(torch, ctx, orc, m, in_, out, fmt):
     note(f"qmatmul-i8 decode {fmt} m={m} {out}x{in_}")
@@ -162,8 +163,8 @@ def test_qmatmul_i8_bf16_out(torch, ctx, orc, m):
     assert orc.normwise_relerr(y, r) < TOL_BF16
 
 
-@pytest.mark.parametrize("m,in_,out", [(1, 2048, 2048), (4, 4096, 96), (2, 20480, 16)])
-@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("m,in_,out", [(1, 2048, 2048), (4, 4096, 96), (2, 20480, 16), (1, 160, 33), (1, 14336, 48)])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q4f32"])
 def test_fused_act_i8_equals_two_step(torch, ctx, orc, m, in_, out, fmt):
     # quantizing inside the decode kernel gives the quantizer's codes, so the
     # fused call equals rq_quantize_act_i8 + rq_qmatmul_i8 bit for bit
@@ -180,6 +181,23 @@ def test_fused_act_i8_equals_two_step(torch, ctx, orc, m, in_, out, fmt):
     assert torch.equal(y1, y2)
     r = ref(xq.cpu().numpy().ravel(), xs.cpu().numpy().ravel(), xsum.cpu().numpy().ravel(), m)
     assert orc.normwise_relerr(y1.cpu().numpy(), r) < TOL_I8
+
+
+@pytest.mark.parametrize("m,in_,out", [(1, 4096, 256), (3, 416, 40)])
+def test_fused_act_i8_bf16_x(torch, ctx, orc, m, in_, out):
+    # bf16 activations widen exactly to f32: the fused quantization of bf16 x
+    # equals rq_quantize_act_i8 of the widened rows, then rq_qmatmul_i8
+    import raster_amd
+
+    x = special_activations(m, in_, seed=in_ - m)
+    w, _ = make(raster_amd, ctx, orc, "q4", out, in_, seed=out + 1)
+    xb = dev(torch, x).reshape(m, in_).to(torch.bfloat16)
+    y1 = w.matmul_fused(xb, act_i8=True)
+    xq, xs, xsum = raster_amd.quantize_act_i8(ctx, xb.float().reshape(-1), in_)
+    y2 = w.matmul_i8(xq, xs, xsum)
+    torch.cuda.synchronize()
+    w.destroy()
+    assert torch.equal(y1, y2)
 
 
 def test_fused_norm_act_i8(torch, ctx, orc):
