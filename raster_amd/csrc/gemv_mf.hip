@@ -20,6 +20,14 @@
 //   ring: A = the activation fragment from LDS (lane (r, q): row r, k = 8q ..
 //   8q+7; rows past m read a zero slot), B = the 16 x 32 chunk in the same
 //   lane order, so lane (r, q) ends up holding y[4q + v][16 g + r], v < 4.
+//   Q4_0 chunks come in fours: lane (r, q) loads the 16-byte row r of the
+//   q-th chunk of a quad (a wave's load moves 1 KB, against 256 B of 8-byte
+//   loads that two lanes share), and two lane-swap rounds across the 16-lane
+//   rows (v_permlane32_swap, v_permlane16_swap) hand lane (r, q) dword q of
+//   row r of each of the four chunks: bytes 4q .. 4q+3, i.e. k = 4q .. 4q+3
+//   (low nibbles) and 4q+16 .. 4q+19 (high nibbles). The activation
+//   fragments in LDS are laid out in that k order; the scales of the four
+//   chunks are broadcast the same way.
 //   The KW waves of a column split the slice's steps and add their partial
 //   sums through LDS in wave order; with ks > 1 the slices' partial sums go
 //   to `part` and gemm_sm_reduce_kernel adds them in slice order.
@@ -41,32 +49,66 @@ struct MfCodes {
   ST s;     // its row's block scale, as stored
 };
 
+// One ring slot of the Q4_0 quad stream: the lane's 16 loaded bytes (row r
+// of chunk q of the quad) and that chunk's scale for row r, as stored.
+template <typename ST>
+struct MfQuad {
+  u32x4 v;
+  ST s;
+};
+
+// Lane (r, a) holds d[b] = dword b of row r of chunk a; afterwards d[j] =
+// dword a of row r of chunk j. Swaps between the lane rows (16 lanes each):
+// rows {2, 3} of d[0] with rows {0, 1} of d[2] (likewise d[1], d[3]), then
+// rows {1, 3} of one with rows {0, 2} of the other.
+__device__ __forceinline__ void mf_xpose4(uint32_t (&d)[4]) {
+  const auto p02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+  const auto p13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+  const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+  const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+  d[0] = q01[0];
+  d[1] = q01[1];
+  d[2] = q23[0];
+  d[3] = q23[1];
+}
+
+// Lane row a holds s (of chunk a); afterwards b[j] = lane row j's s, in
+// every row.
+__device__ __forceinline__ void mf_bcast4(uint32_t s, uint32_t (&b)[4]) {
+  const auto p = __builtin_amdgcn_permlane32_swap(s, s, false, false);
+  const auto b01 = __builtin_amdgcn_permlane16_swap(p[0], p[0], false, false);
+  const auto b23 = __builtin_amdgcn_permlane16_swap(p[1], p[1], false, false);
+  b[0] = b01[0];
+  b[1] = b01[1];
+  b[2] = b23[0];
+  b[3] = b23[1];
+}
+
+// Dword a of a Q4_0 row (bytes 4a .. 4a+3) as the bf16 of 128 + nibble, in
+// the k order k = 4a .. 4a+3, 4a+16 .. 4a+19
+__device__ __forceinline__ bf16x8 mf_q4_dword(uint32_t d) {
+  const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+  return __builtin_bit_cast(bf16x8, u32x4{__builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u),
+                                          __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u),
+                                          __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u),
+                                          __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u)});
+}
+
 __device__ __forceinline__ float mf_scale(float s) { return s; }
 __device__ __forceinline__ float mf_scale(uint16_t s) { return f16_bits_to_f32(s); }
 
-// the lane's 8 codes as bf16 of code + OFF
-template <int FMT, typename ST>
-__device__ __forceinline__ bf16x8 mf_codes(const MfCodes<ST>& c, int qd) {
+// the lane's 8 Q8_0 codes as bf16 of code + 128 (v_cvt_f32_ubyte of c ^ 0x80;
+// the bf16 of an integer below 256 is the high half of its f32)
+template <typename ST>
+__device__ __forceinline__ bf16x8 mf_q8_codes(const MfCodes<ST>& c) {
   uint32_t o[4];
-  if (FMT == RQ_Q4_0) {
-    // k = 8q .. 8q+7: low nibbles of bytes 8q.. (q < 2), high nibbles of
-    // bytes 8(q-2).. (q >= 2); bytes n | 0x43 << 8 are the bf16 128 + n
-    const uint32_t sh = qd >= 2 ? 4u : 0u;
-    const uint32_t d0 = (c.v[0] >> sh) & 0x0F0F0F0Fu, d1 = (c.v[1] >> sh) & 0x0F0F0F0Fu;
-    o[0] = __builtin_amdgcn_perm(0x43434343u, d0, 0x04010400u);
-    o[1] = __builtin_amdgcn_perm(0x43434343u, d0, 0x04030402u);
-    o[2] = __builtin_amdgcn_perm(0x43434343u, d1, 0x04010400u);
-    o[3] = __builtin_amdgcn_perm(0x43434343u, d1, 0x04030402u);
-  } else {
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t u = c.v[h] ^ 0x80808080u;  // c + 128 per byte
-      const float f0 = (float)(u & 0xFFu), f1 = (float)((u >> 8) & 0xFFu);
-      const float f2 = (float)((u >> 16) & 0xFFu), f3 = (float)(u >> 24);
-      // the bf16 of an integer below 256 is the high half of its f32
-      o[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-      o[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
-    }
+  for (int h = 0; h < 2; h++) {
+    const uint32_t u = c.v[h] ^ 0x80808080u;
+    const float f0 = (float)(u & 0xFFu), f1 = (float)((u >> 8) & 0xFFu);
+    const float f2 = (float)((u >> 16) & 0xFFu), f3 = (float)(u >> 24);
+    o[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    o[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   }
   return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -157,9 +199,21 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
       sum += __shfl_xor(sum, 1, 64);
       sum += __shfl_xor(sum, 2, 64);
       if (idx0 < nitems) {
-        *reinterpret_cast<u32x4*>(smem + ((u * P) * M + m) * 64 + qq * 16) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        if (P == 2)
-          *reinterpret_cast<u32x4*>(smem + ((u * P + 1) * M + m) * 64 + qq * 16) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        uint8_t* f = smem + ((u * P) * M + m) * 64;
+        if (FMT == RQ_Q4_0) {
+          // k = 8qq .. 8qq+3 to lane group 2(qq&1), 8qq+4 .. 8qq+7 to the
+          // next; the high half of the block to the upper 8 bytes of each
+          const int o0 = 32 * (qq & 1) + 8 * (qq >> 1);
+          *reinterpret_cast<u32x2*>(f + o0) = u32x2{hi[0], hi[1]};
+          *reinterpret_cast<u32x2*>(f + o0 + 16) = u32x2{hi[2], hi[3]};
+          if (P == 2) {
+            *reinterpret_cast<u32x2*>(f + M * 64 + o0) = u32x2{lo[0], lo[1]};
+            *reinterpret_cast<u32x2*>(f + M * 64 + o0 + 16) = u32x2{lo[2], lo[3]};
+          }
+        } else {
+          *reinterpret_cast<u32x4*>(f + qq * 16) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+          if (P == 2) *reinterpret_cast<u32x4*>(f + M * 64 + qq * 16) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        }
         if (qq == 0) *reinterpret_cast<float*>(smem + xs_off + (u * 16 + m) * 4) = OFF * sum;
       }
     }
@@ -177,7 +231,24 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
   const int spp = (spw + WD - 1) / WD * WD;
   const int nunits = (ngroups + gcols * GW - 1) / (gcols * GW);
   const int T = nunits * spp;
-  MfCodes<ST> wc[WD];
+  static_assert(WD % 4 == 0, "the Q4_0 ring holds whole quads");
+  MfCodes<ST> wc[FMT == RQ_Q4_0 ? 1 : WD];
+  MfQuad<ST> wq[FMT == RQ_Q4_0 ? WD / 4 : 1];
+  // Q4_0: quad slot of steps u .. u+3 (u a multiple of 4); lane (r, qd)
+  // loads step u + qd, clamped to the wave's share (steps past it compute
+  // nothing)
+  auto load_q = [&](int slot, int j, int u) {
+    if (j >= nunits) {  // past the end: the last quad again
+      j = nunits - 1;
+      u = spp - 4;
+    }
+    const int g = min(col * GW + gw + j * gcols * GW, ngroups - 1);
+    const int kb = kb0 + min(kw * spw + min(u + qd, spw - 1), nst - 1);
+    const int64_t chunk = (int64_t)g * nkb + kb;
+    wq[slot].v = *reinterpret_cast<const u32x4*>(q + chunk * 256 + r * 16);
+    wq[slot].s = sc[chunk * 16 + r];
+  };
+  // Q8_0: slot of step u, lane (r, qd) loading codes 8qd .. 8qd+7 of row r
   auto load_w = [&](int slot, int j, int u) {
     if (j >= nunits) {  // past the end: the last step again
       j = nunits - 1;
@@ -186,10 +257,7 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
     const int g = min(col * GW + gw + j * gcols * GW, ngroups - 1);
     const int kb = kb0 + min(kw * spw + min(u, spw - 1), nst - 1);
     const int64_t chunk = (int64_t)g * nkb + kb;
-    if (FMT == RQ_Q8_0)
-      wc[slot].v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + r * 32 + 8 * qd);
-    else
-      wc[slot].v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + r * 16 + 8 * (qd & 1));
+    wc[slot].v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + r * 32 + 8 * qd);
     wc[slot].s = sc[chunk * 16 + r];
   };
   int lj = 0, lu = 0;  // next step to load
@@ -200,15 +268,31 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
     }
   };
 
+  auto advance4 = [&](int& j, int& u) {
+    u += 4;
+    if (u == spp) {
+      u = 0;
+      ++j;
+    }
+  };
+
   load_items(0);
   __builtin_amdgcn_sched_barrier(0);
   // the ring's first WD steps, unconditionally (addresses are clamped; a
   // conditional here would leave the ring's indices to run time and put it
   // in scratch memory)
+  if constexpr (FMT == RQ_Q4_0) {
 #pragma unroll
-  for (int i = 0; i < WD; i++) {
-    load_w(i, lj, lu);
-    advance(lj, lu);
+    for (int t = 0; t < WD / 4; t++) {
+      load_q(t, lj, lu);
+      advance4(lj, lu);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WD; i++) {
+      load_w(i, lj, lu);
+      advance(lj, lu);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   for (int base = 0; base < nitems; base += stride * XI) {
@@ -258,12 +342,55 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
   };
 
   const int aoff = r < M ? r * 64 + qd * 16 : -1;
+  // one step's MFMAs and block epilogue
+  auto step = [&](int su, const bf16x8& bw, float sv) {
+    const int ab = su * P * M * 64;
+    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + aoff : zero_off));
+    f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    if (P == 2) {
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + M * 64 + aoff : zero_off));
+      blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, blk, 0, 0, 0);
+    }
+    const f32x4 xo = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] = fmaf(sv, blk[e] - xo[e], acc[e]);
+  };
+  if constexpr (FMT == RQ_Q4_0) {
+    for (int j = 0; j < nunits; j++) {
+      for (int u0 = 0; u0 < spp; u0 += WD) {
+#pragma unroll
+        for (int t = 0; t < WD / 4; t++) {
+          uint32_t d[4] = {wq[t].v[0], wq[t].v[1], wq[t].v[2], wq[t].v[3]};
+          uint32_t sb;
+          if constexpr (sizeof(ST) == 2)
+            sb = wq[t].s;
+          else
+            sb = __builtin_bit_cast(uint32_t, wq[t].s);
+          // unconditional refill (past the end it rereads the last quad): a
+          // conditional load leaves the compiler unsure how many loads are in
+          // flight, and its waits then drain the ring once per turn
+          load_q(t, lj, lu);
+          advance4(lj, lu);
+          mf_xpose4(d);
+          uint32_t s4[4];
+          mf_bcast4(sb, s4);
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int u = u0 + 4 * t + jj;
+            const int su = kw * spw + u;
+            if (u < spw && su < nst) step(su, mf_q4_dword(d[jj]), scale_from_bits<ST>(s4[jj]));
+          }
+        }
+      }
+      finish(j);
+    }
+  } else {
   for (int j = 0; j < nunits; j++) {
     for (int u0 = 0; u0 < spp; u0 += WD) {
 #pragma unroll
       for (int i = 0; i < WD; i++) {
         const int u = u0 + i;
-        const bf16x8 bw = mf_codes<FMT>(wc[i], qd);
+        const bf16x8 bw = mf_q8_codes(wc[i]);
         const float sv = mf_scale(wc[i].s);
         // unconditional refill (past the end it rereads the last step): a
         // conditional load leaves the compiler unsure how many loads are in
@@ -271,22 +398,11 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
         load_w(i, lj, lu);
         advance(lj, lu);
         const int su = kw * spw + u;
-        if (u < spw && su < nst) {
-          const int ab = su * P * M * 64;
-          const bf16x8 ah = *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + aoff : zero_off));
-          f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-          if (P == 2) {
-            const bf16x8 al =
-                *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + M * 64 + aoff : zero_off));
-            blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, blk, 0, 0, 0);
-          }
-          const f32x4 xo = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
-#pragma unroll
-          for (int e = 0; e < 4; e++) acc[e] = fmaf(sv, blk[e] - xo[e], acc[e]);
-        }
+        if (u < spw && su < nst) step(su, bw, sv);
       }
     }
     finish(j);
+  }
   }
 }
 
