@@ -16,6 +16,13 @@
 // waves of a workgroup cover 64 NTW columns and all of m (MT 16-row tiles).
 // K may be cut into ks slices (grid.y) whose f32 partial sums a second kernel
 // adds in slice order (deterministic), for more waves in flight.
+//
+// Q4_0 weights stream in quads of chunks: lane (r, q) loads the 16-byte row r
+// of chunk q of the quad (1 KB per wave load; 8-byte loads would have two
+// lanes per address), and two rounds of lane-row swaps (v_permlane32_swap,
+// v_permlane16_swap) hand lane (r, q) dword q of row r of each of the four
+// chunks, k = 4q .. 4q+3 (low nibbles) and 4q+16 .. 4q+19 (high nibbles). The
+// activation fragments are staged into LDS in that k order.
 #include <algorithm>
 
 #include "rq_internal.h"
@@ -29,33 +36,65 @@ struct WCodesSm {
   uint32_t s;  // scale bits, converted at dequantization
 };
 
-template <int FMT, typename ST>
-__device__ __forceinline__ void load_wc(WCodesSm& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                        int64_t chunk, int fr, int fg) {
-  if (FMT == RQ_Q8_0)
-    c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
-  else
-    c.v = *reinterpret_cast<const u32x2*>(q + chunk * 256 + fr * 16 + 8 * (fg & 1));
+struct WQuadSm {
+  u32x4 v;     // row r of chunk q of the quad
+  uint32_t s;  // that chunk's scale bits for row r
+};
+
+// Lane (r, a) holds d[b] = dword b of row r of chunk a; afterwards d[j] =
+// dword a of row r of chunk j (swaps between the 16-lane rows: rows {2, 3}
+// of d[0] with rows {0, 1} of d[2], likewise d[1], d[3]; then rows {1, 3} of
+// one with rows {0, 2} of the other).
+__device__ __forceinline__ void xpose4_rows(uint32_t (&d)[4]) {
+  const auto p02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+  const auto p13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+  const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+  const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+  d[0] = q01[0];
+  d[1] = q01[1];
+  d[2] = q23[0];
+  d[3] = q23[1];
+}
+
+// Lane row a holds s (of chunk a); afterwards b[j] = lane row j's s in every
+// row.
+__device__ __forceinline__ void bcast4_rows(uint32_t s, uint32_t (&b)[4]) {
+  const auto p = __builtin_amdgcn_permlane32_swap(s, s, false, false);
+  const auto b01 = __builtin_amdgcn_permlane16_swap(p[0], p[0], false, false);
+  const auto b23 = __builtin_amdgcn_permlane16_swap(p[1], p[1], false, false);
+  b[0] = b01[0];
+  b[1] = b01[1];
+  b[2] = b23[0];
+  b[3] = b23[1];
+}
+
+// Dword a of a Q4_0 row (bytes 4a .. 4a+3) dequantized to bf16 in the k order
+// k = 4a .. 4a+3, 4a+16 .. 4a+19: exact f32 scale * (n - 8), one RNE rounding
+template <typename ST>
+__device__ __forceinline__ bf16x8 dequant_q4_dword(uint32_t d, uint32_t sbits) {
+  const float s = scale_from_bits<ST>(sbits), off = -8.0f * s;
+  const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+  auto two = [&](uint32_t v, int b) {
+    return pack2_bf16(fmaf((float)((v >> (8 * b)) & 0xFFu), s, off), fmaf((float)((v >> (8 * b + 8)) & 0xFFu), s, off));
+  };
+  return __builtin_bit_cast(bf16x8, u32x4{two(lo, 0), two(lo, 2), two(hi, 0), two(hi, 2)});
+}
+
+// Q8_0: lane (fr, fg) takes codes 8fg .. 8fg+7 of row fr
+template <typename ST>
+__device__ __forceinline__ void load_wc_q8(WCodesSm& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
+                                           int64_t chunk, int fr, int fg) {
+  c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
   c.s = load_scale_bits<ST>(sc, chunk * 16 + fr);
 }
 
-// 8 bf16 of the lane's fragment share: exact f32 scale * code, one RNE
+// 8 bf16 of the lane's Q8_0 fragment share: exact f32 scale * code, one RNE
 // rounding (the dequant of gemm_bf16.hip)
-template <int FMT, typename ST>
-__device__ __forceinline__ bf16x8 dequant_sm(const WCodesSm& c, int fg) {
+template <typename ST>
+__device__ __forceinline__ bf16x8 dequant_sm_q8(const WCodesSm& c) {
   const float s = scale_from_bits<ST>(c.s);
-  uint32_t d[2];
-  float off;
-  if (FMT == RQ_Q8_0) {
-    d[0] = c.v[0] ^ 0x80808080u;
-    d[1] = c.v[1] ^ 0x80808080u;
-    off = -128.0f * s;
-  } else {
-    const int sh = fg >= 2 ? 4 : 0;
-    d[0] = (c.v[0] >> sh) & 0x0F0F0F0Fu;
-    d[1] = (c.v[1] >> sh) & 0x0F0F0F0Fu;
-    off = -8.0f * s;
-  }
+  const uint32_t d[2] = {c.v[0] ^ 0x80808080u, c.v[1] ^ 0x80808080u};
+  const float off = -128.0f * s;
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
@@ -106,14 +145,39 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int p = tid + 256 * i;
-      reinterpret_cast<u32x4*>(&As[buf][0][0][0])[p] = areg[i];
+      if (FMT == RQ_Q4_0) {
+        // the piece of lane (r, g) holds k = 8g .. 8g+7: k = 8g .. 8g+3 go
+        // to lane group 2 (g & 1), 8g+4 .. 8g+7 to the next one, the upper
+        // half of the block (g >= 2) to the upper 8 bytes of each
+        const int l = p & 63, r = l & 15, g = l >> 4;
+        uint8_t* base = reinterpret_cast<uint8_t*>(&As[buf][0][0][0]) + (p >> 6) * 1024;
+        const int o0 = ((2 * (g & 1)) * 16 + r) * 16 + 8 * (g >> 1);
+        *reinterpret_cast<u32x2*>(base + o0) = u32x2{areg[i][0], areg[i][1]};
+        *reinterpret_cast<u32x2*>(base + o0 + 256) = u32x2{areg[i][2], areg[i][3]};
+      } else {
+        reinterpret_cast<u32x4*>(&As[buf][0][0][0])[p] = areg[i];
+      }
     }
   };
-  WCodesSm wc[WD][NTW];
+  static_assert(KC % 4 == 0, "chunks of whole Q4_0 quads");
+  WCodesSm wc[FMT == RQ_Q4_0 ? 1 : WD][NTW];
+  WQuadSm wq[FMT == RQ_Q4_0 ? WD / 4 : 1][NTW];
   auto load_w = [&](int slot, int s) {  // step s of the slice (clamped)
-    const int kb = min(kb0 + min(s, max(nst - 1, 0)), nkb - 1);
+    if constexpr (FMT == RQ_Q4_0) {
+      // quad slot / 4 of steps s .. s+3 (slot, s multiples of 4): lane
+      // (fr, fg) loads step s + fg
+      const int kb = min(kb0 + min(s + fg, max(nst - 1, 0)), nkb - 1);
 #pragma unroll
-    for (int j = 0; j < NTW; j++) load_wc<FMT, ST>(wc[slot][j], q, sc, wchunk[j] + kb, fr, fg);
+      for (int j = 0; j < NTW; j++) {
+        const int64_t ch = wchunk[j] + kb;
+        wq[slot / 4][j].v = *reinterpret_cast<const u32x4*>(q + ch * 256 + fr * 16);
+        wq[slot / 4][j].s = load_scale_bits<ST>(sc, ch * 16 + fr);
+      }
+    } else {
+      const int kb = min(kb0 + min(s, max(nst - 1, 0)), nkb - 1);
+#pragma unroll
+      for (int j = 0; j < NTW; j++) load_wc_q8<ST>(wc[slot][j], q, sc, wchunk[j] + kb, fr, fg);
+    }
   };
 
   f32x4 acc[MT][NTW];
@@ -127,7 +191,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   load_a(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int s = 0; s < WD; s++) load_w(s, s);
+  for (int s = 0; s < WD; s += FMT == RQ_Q4_0 ? 4 : 1) load_w(s, s);
   __builtin_amdgcn_sched_barrier(0);
   store_a(0);
   if (nch > 1) load_a(1);
@@ -143,15 +207,35 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
       store_a(buf ^ 1);
       if (c + 2 < nch) load_a(c + 2);
     }
+    uint32_t dq[NTW][4], sq[NTW][4];  // the current quad, after the swaps
 #pragma unroll
     for (int u = 0; u < KC; u++) {
       const int s = c * KC + u;
       if (s >= nst) break;
       const int slot = buf * KC + u;
       bf16x8 wf[NTW];
+      if constexpr (FMT == RQ_Q4_0) {
+        if (u % 4 == 0) {
 #pragma unroll
-      for (int j = 0; j < NTW; j++) wf[j] = dequant_sm<FMT, ST>(wc[slot][j], fg);
-      load_w(slot, s + WD);
+          for (int j = 0; j < NTW; j++) {
+#pragma unroll
+            for (int b = 0; b < 4; b++) dq[j][b] = wq[slot / 4][j].v[b];
+            sq[j][0] = wq[slot / 4][j].s;
+          }
+          load_w(slot, s + WD);
+#pragma unroll
+          for (int j = 0; j < NTW; j++) {
+            xpose4_rows(dq[j]);
+            bcast4_rows(sq[j][0], sq[j]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NTW; j++) wf[j] = dequant_q4_dword<ST>(dq[j][u % 4], sq[j][u % 4]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NTW; j++) wf[j] = dequant_sm_q8<ST>(wc[slot][j]);
+        load_w(slot, s + WD);
+      }
       bf16x8 af[MT];
 #pragma unroll
       for (int i = 0; i < MT; i++) af[i] = As[buf][u][i][lane];

@@ -50,10 +50,10 @@ __host__ __device__ inline int g1_lds_bytes(int nb, int waves, int mr) {
   return mr * nb * 72 + 2 * waves * mr * 16 * 4;
 }
 
-template <int FMT, typename ST, int XT, int W, int D, int MR>
+template <int FMT, typename ST, int XT, int W, int D, int MR, bool AQ>
 __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
                                                       const void* __restrict__ x, const float* __restrict__ axs,
-                                                      const int32_t* __restrict__ axsum, int act_i8,
+                                                      const int32_t* __restrict__ axsum,
                                                       void* __restrict__ y, int M, int K, int N, int npad,
                                                       int y_dtype) {
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;  // blocks per load instruction
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
         continue;
       }
       const float* v = xv[i];
-      if (act_i8) {
+      if (AQ) {
         const float qmax = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
         const double d = (double)qmax / 127.0;
         const double id = d == 0.0 ? 0.0 : 1.0 / d;
@@ -292,9 +292,12 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
 }
 
 // One configuration (the lab and the dispatcher): gcols workgroups.
-template <int FMT, typename ST, int XT, int W, int D, int MR>
+// AQ: quantize x to int8 blocks in the kernel (rq_fused_ops.act_i8; a
+// template parameter, as a run-time switch costs the plain path ~0.4 us)
+template <int FMT, typename ST, int XT, int W, int D, int MR, bool AQ = false>
 hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
-  auto kernel = &gemv1_kernel<FMT, ST, XT, W, D, MR>;
+  static_assert(!(AQ && XT == kXtI8), "int8 input is quantized already");
+  auto kernel = &gemv1_kernel<FMT, ST, XT, W, D, MR, AQ>;
   const int nb = (int)(a.k / 32);
   constexpr int BPL = FMT == RQ_Q4_0 ? 4 : 2;
   if (a.m < 1 || a.m > MR || nb < BPL || gcols < 1) return hipErrorInvalidValue;
@@ -314,7 +317,7 @@ hipError_t launch_gemv1_t(const MatmulArgs& a, int gcols) {
   const int ngroups = (int)(a.npad / 16);
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)std::min(gcols, ngroups)), dim3(64 * W), (unsigned)lds, a.stream,
                         a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), a.x, a.ops.act_scale,
-                        a.ops.act_sum, a.ops.act_i8, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
+                        a.ops.act_sum, a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
   return hipGetLastError();
 }
 
@@ -348,19 +351,24 @@ G1Plan plan_gemv1(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, i
   return p;
 }
 
-template <typename ST, int XT>
+template <typename ST, int XT, bool AQ>
 static hipError_t launch_g1_x(const MatmulArgs& a, const G1Plan& p) {
-  if (p.waves == 8 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 2, 1>(a, p.gcols);
-  if (p.waves == 8 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 4, 1>(a, p.gcols);
-  if (p.waves == 16 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 2, 1>(a, p.gcols);
-  if (p.waves == 16 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 4, 1>(a, p.gcols);
+  if (p.waves == 8 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 2, 1, AQ>(a, p.gcols);
+  if (p.waves == 8 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 8, 4, 1, AQ>(a, p.gcols);
+  if (p.waves == 16 && p.ring == 2) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 2, 1, AQ>(a, p.gcols);
+  if (p.waves == 16 && p.ring == 4) return launch_gemv1_t<RQ_Q4_0, ST, XT, 16, 4, 1, AQ>(a, p.gcols);
   return hipErrorInvalidValue;
+}
+
+template <typename ST, int XT>
+static hipError_t launch_g1_q(const MatmulArgs& a, const G1Plan& p) {
+  return a.ops.act_i8 ? launch_g1_x<ST, XT, true>(a, p) : launch_g1_x<ST, XT, false>(a, p);
 }
 
 template <typename ST>
 static hipError_t launch_g1_s(const MatmulArgs& a, const G1Plan& p) {
-  if (a.x_dtype == kXtI8) return launch_g1_x<ST, kXtI8>(a, p);
-  return a.x_dtype == RQ_F32 ? launch_g1_x<ST, RQ_F32>(a, p) : launch_g1_x<ST, RQ_BF16>(a, p);
+  if (a.x_dtype == kXtI8) return launch_g1_x<ST, kXtI8, false>(a, p);
+  return a.x_dtype == RQ_F32 ? launch_g1_q<ST, RQ_F32>(a, p) : launch_g1_q<ST, RQ_BF16>(a, p);
 }
 
 hipError_t launch_gemv1(const MatmulArgs& a, const G1Plan& p) {
