@@ -728,7 +728,7 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   a.part = nullptr;
   a.ops = dops;
   const bool plain = !dops.norm_gain && !dops.residual && !dops.swiglu && !dops.act_i8;
-  const MfPlan mf = plain && plan.ok ? plan_gemv_mf(m, w.in, w.npad, x_dtype, c->cu_count) : MfPlan{};
+  const MfPlan mf = plain && plan.ok ? plan_gemv_mf(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : MfPlan{};
   // the m = 1 GEMV also quantizes to int8 blocks itself (act_i8)
   const bool plain_g1 = !dops.norm_gain && !dops.residual && !dops.swiglu;
   const G1Plan g1 = plain_g1 && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};

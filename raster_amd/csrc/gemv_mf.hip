@@ -446,20 +446,23 @@ namespace rq {
 
 // Plan: taken for 8 < m <= 16 only. There the int8 decode kernel spends most
 // of its time forming its activation levels and in its per-window epilogue
-// (38 us at m = 16, K = 4096, N = 14336 Q4, f32 x; this kernel 26 us); for
-// m <= 8 it stays ahead (m = 1 / 4: 11.6 / 14.6 us against 23 / 27 us).
-// Eight waves per workgroup take different groups (GW = 8; splitting K
-// between a workgroup's waves measured slower at m = 16); ks is the fewest
-// K-slices whose LDS fits two workgroups per CU (ks = 4 at K = 4096: 26 us,
-// against 36 at ks = 2 and 32 at ks = 8); a 16-step ring (32 steps: 30 us).
-MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int cu_count) {
+// (38 us at m = 16, K = 4096, N = 14336 Q4, f32 x; this kernel 18 us); for
+// m <= 8 it stays ahead (m = 1 / 4: 11.6 / 14.6 us against 23 / 27 us with
+// 8-byte Q4 loads). The waves of a workgroup take different groups
+// (splitting K between them measured slower at m = 16): Q4_0 16 waves with
+// an 8-step ring (two quads; at that shape 17.9 us against 18.8 for 8 waves
+// and 16 steps, and at K = 8192, N = 28672, bf16 x, 40.6 against 45.8),
+// Q8_0 8 waves with a 16-step ring (32 steps: 30 us with 8-byte Q4 loads);
+// ks is the fewest K-slices whose LDS fits two workgroups per CU (ks = 4 at
+// K = 4096: 18 us, against 20 at ks = 2 and 22 at ks = 8).
+MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count) {
   MfPlan p{};
   if (m <= 8 || m > 16 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0 || k < 32) return p;
   const int parts = x_dtype == RQ_F32 ? 2 : 1;
   const int64_t nkb = k / 32, ngroups = npad / 16;
   p.kw = 1;
-  p.gw = 8;
-  p.wd = 16;
+  p.gw = format == RQ_Q4_0 ? 16 : 8;
+  p.wd = format == RQ_Q4_0 ? 8 : 16;
   int64_t ks = 1;
   while (mf_lds_bytes((int)m, (int)((nkb + ks - 1) / ks), parts, p.kw, p.gw) > 81920 ||
          (ks - 1) * ((nkb + ks - 1) / ks) >= nkb) {
@@ -475,7 +478,11 @@ MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int cu_coun
 
 template <int FMT, typename ST, int XT>
 static hipError_t launch_mf_x(const MatmulArgs& a, const MfPlan& p) {
-  if (p.kw == 1 && p.gw == 8 && p.wd == 16) return launch_gemv_mf_t<FMT, ST, XT, 1, 8, 16>(a, p.ks, p.gcols);
+  if constexpr (FMT == RQ_Q4_0) {
+    if (p.kw == 1 && p.gw == 16 && p.wd == 8) return launch_gemv_mf_t<FMT, ST, XT, 1, 16, 8>(a, p.ks, p.gcols);
+  } else {
+    if (p.kw == 1 && p.gw == 8 && p.wd == 16) return launch_gemv_mf_t<FMT, ST, XT, 1, 8, 16>(a, p.ks, p.gcols);
+  }
   return hipErrorInvalidValue;
 }
 

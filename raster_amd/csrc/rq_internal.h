@@ -131,7 +131,7 @@ struct MfPlan {
   bool ok;
   int kw, gw, wd, ks, gcols;
 };
-MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int cu_count);
+MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count);
 hipError_t launch_gemv_mf(const MatmulArgs& a, const MfPlan& p);
 // m = 1 decode on v_dot4_i32_i8 for Q4_0 weights (gemv1.hip): plain calls,
 // f32 / bf16 x. waves per workgroup, ring depth, workgroups.
