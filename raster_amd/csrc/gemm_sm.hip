@@ -313,9 +313,15 @@ hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, in
   return hipGetLastError();
 }
 
+// Two weight fragments per wave (128 columns per workgroup) and chunks of 4
+// k-steps (an 8-step weight ring): with the Q4_0 quads, at M = 32 / 64,
+// K = 8192, N = 28672 51.5 / 69.1 us against 55.7 / 78.1 us for one fragment
+// and 8-step chunks.
+constexpr int kSmNTW = 2, kSmKC = 4;
+
 template <int FMT, typename ST, int MT>
 static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
-  constexpr int NTW = 1, KC = 8;
+  constexpr int NTW = kSmNTW, KC = kSmKC;
   if (hipError_t e = launch_pack_x(a)) return e;
   const dim3 grid((unsigned)((a.npad / 16 + 4 * NTW - 1) / (4 * NTW)), (unsigned)ks);
   hipExtLaunchKernelGGL((gemm_sm_kernel<FMT, ST, MT, NTW, KC>), grid, dim3(256), 0, a.stream, nullptr,
@@ -328,14 +334,15 @@ static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
 }
 
 // K-slices: about 24 waves per CU at m <= 32 (12 above: the 4-tile kernel
-// holds fewer per CU), 4 per 64 output columns times the slices; each slice
-// keeps at least 8 chunks of K. Measured (Q4, bf16 x): M = 32, K = 8192,
-// N = 28672: 1 / 2 / 4 slices 66.8 / 60.4 / 58.7 us; M = 64: 1 / 2 slices
-// 83.6 / 90.6 us; M = 17, K = 4096, N = 14336: 1 / 2 slices 27.1 / 20.8 us.
+// holds fewer per CU), 4 per 64 NTW output columns times the slices; each
+// slice keeps at least 8 chunks of K. Measured (Q4, bf16 x, two fragments per
+// wave, 4-step chunks): M = 32, K = 8192, N = 28672: 3 / 4 / 6 / 8 slices
+// 52.5 / 53.2 / 52.3 / 51.5 us; M = 64: 1 / 2 slices 82.9 / 69.1 us;
+// M = 17, K = 4096, N = 14336: 2 / 4 slices 21.1 / 19.2 us.
 int gemm_sm_slices(int64_t m, int64_t k, int64_t npad, int cu_count) {
-  const int64_t waves = (npad / 64) * 4, want = (int64_t)cu_count * (m <= 32 ? 24 : 12);
+  const int64_t waves = (npad / (64 * kSmNTW)) * 4, want = (int64_t)cu_count * (m <= 32 ? 24 : 12);
   int64_t ks = std::max<int64_t>(1, want / std::max<int64_t>(waves, 1));
-  ks = std::min<int64_t>(ks, std::max<int64_t>(1, (k / 32) / 64));
+  ks = std::min<int64_t>(ks, std::max<int64_t>(1, (k / 32) / (8 * kSmKC)));
   return (int)std::min<int64_t>(ks, 8);
 }
 
