@@ -145,12 +145,13 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * m == 0 is a no-op.
  *
  * Numerics (all accumulation in f32):
- *  - m <= 8: int8 MFMA on the raw weight codes. Each 32-block of each
+ *  - m <= 8 (Q4_0: m <= 4; every fused call): int8 MFMA (m = 1 with Q4_0:
+ *    v_dot4_i32_i8) on the raw weight codes. Each 32-block of each
  *    activation row is held as a 16-bit block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
  *    exponent, |X| < 2^15, so the per-element error is <= 2^(e-16) (below
  *    1.6e-5 relative to the block maximum). An inf or NaN activation makes its
  *    row's outputs NaN.
- *  - 8 < m <= 16: bf16 MFMA on the exact codes (offset so that every code is
+ *  - 8 < m <= 16 (Q4_0: 4 < m <= 16): bf16 MFMA on the exact codes (offset so that every code is
  *    a small integer in bf16), the block scale applied in f32 to each block's
  *    dot; f32 x split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|). A
  *    non-finite activation makes its row's outputs non-finite.

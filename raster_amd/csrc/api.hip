@@ -703,7 +703,8 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
 
 // Launches the matmul of a validated call: for m <= 16 the int8 decode kernel
 // (for m = 1 with Q4_0 weights the sdot4 GEMV instead, unless a norm,
-// residual or SwiGLU is fused; for 8 < m <= 16 without fused options, f32 /
+// residual or SwiGLU is fused; for 4 < m <= 16 (Q4_0) or 8 < m <= 16 (Q8_0)
+// without fused options, f32 /
 // bf16 x, the MFMA decode kernel), else the GEMM for the activation dtype;
 // per-stream scratch and kernel timing around it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,

@@ -1,4 +1,5 @@
-// gemv_mf.hip — decode matmul (m <= 16; planned for 8 < m <= 16) of plain
+// gemv_mf.hip — decode matmul (m <= 16; planned for 4 < m <= 16 with Q4_0
+// weights, 8 < m <= 16 with Q8_0) of plain
 // rq_qmatmul calls with f32 or bf16 activations, on bf16 MFMA with exact
 // codes.
 //
@@ -444,20 +445,23 @@ hipError_t launch_gemv_mf_t(const MatmulArgs& a, int ks, int gcols) {
 
 namespace rq {
 
-// Plan: taken for 8 < m <= 16 only. There the int8 decode kernel spends most
-// of its time forming its activation levels and in its per-window epilogue
-// (38 us at m = 16, K = 4096, N = 14336 Q4, f32 x; this kernel 18 us); for
-// m <= 8 it stays ahead (m = 1 / 4: 11.6 / 14.6 us against 23 / 27 us with
-// 8-byte Q4 loads). The waves of a workgroup take different groups
+// Plan: taken for 4 < m <= 16 with Q4_0 weights, 8 < m <= 16 with Q8_0. There
+// the int8 decode kernel spends most of its time forming its activation levels
+// and in its per-window epilogue (K = 4096, N = 14336 Q4, f32 x: m = 6 / 8 /
+// 16 21.4 / 23.6 / 38 us, this kernel 16.3 / 16.7 / 18 us); below it stays
+// ahead (m = 2 / 4: 12.3 / 14.9 us against 15.6 / 16.0 us). The waves of a workgroup take different groups
 // (splitting K between them measured slower at m = 16): Q4_0 16 waves with
 // an 8-step ring (two quads; at that shape 17.9 us against 18.8 for 8 waves
 // and 16 steps, and at K = 8192, N = 28672, bf16 x, 40.6 against 45.8),
 // Q8_0 8 waves with a 16-step ring (32 steps: 30 us with 8-byte Q4 loads);
-// ks is the fewest K-slices whose LDS fits two workgroups per CU (ks = 4 at
-// K = 4096: 18 us, against 20 at ks = 2 and 22 at ks = 8).
+// ks: at least the fewest K-slices whose LDS fits two workgroups per CU, and
+// enough workgroups for ~85% of the CUs (slices of at least 8 steps): at
+// K = 4096, m = 16 both give 4 (18 us, against 20 at ks = 2 and 22 at 8); at
+// m = 6 the LDS alone would allow 2 (23.3 us against 16.3 at 4).
 MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int format, int cu_count) {
   MfPlan p{};
-  if (m <= 8 || m > 16 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0 || k < 32) return p;
+  const int64_t m_min = format == RQ_Q4_0 ? 5 : 9;
+  if (m < m_min || m > 16 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0 || k < 32) return p;
   const int parts = x_dtype == RQ_F32 ? 2 : 1;
   const int64_t nkb = k / 32, ngroups = npad / 16;
   p.kw = 1;
@@ -468,10 +472,14 @@ MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int format,
          (ks - 1) * ((nkb + ks - 1) / ks) >= nkb) {
     if (++ks > nkb) return p;
   }
-  p.ks = (int)ks;
   p.gcols = (int)((ngroups + p.gw - 1) / p.gw);
+  const int64_t fill = std::min<int64_t>(((int64_t)cu_count * 85 / 100 + p.gcols - 1) / p.gcols,
+                                         std::max<int64_t>(1, nkb / 8));
+  int64_t kf = std::max(ks, fill);
+  while (kf > ks && (kf - 1) * ((nkb + kf - 1) / kf) >= nkb) --kf;  // no empty slice
+  ks = kf;
+  p.ks = (int)ks;
   if ((int64_t)p.gcols * ks > INT32_MAX) return p;
-  (void)cu_count;
   p.ok = true;
   return p;
 }

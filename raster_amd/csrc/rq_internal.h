@@ -125,7 +125,8 @@ struct DecodePlan {
 DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 
 // Decode on bf16 MFMA with exact codes (gemv_mf.hip): plain calls, f32 / bf16
-// x, 8 < m <= 16 (the kernel takes m <= 16). kw x gw waves per workgroup,
+// x, 4 < m <= 16 (Q4_0) or 8 < m <= 16 (Q8_0) (the kernel takes m <= 16).
+// kw x gw waves per workgroup,
 // wd-step weight ring, ks K-slices, gcols workgroup columns per slice.
 struct MfPlan {
   bool ok;

@@ -123,6 +123,26 @@ def test_mf_bf16(torch, ctx, orc, m, in_, out, fmt):
     assert orc.normwise_relerr(y, ro) < TOL_F32
 
 
+@pytest.mark.parametrize("m,in_,out", [(5, 4096, 520), (6, 416, 33), (8, 14336, 48), (7, 8192, 100)])
+@pytest.mark.parametrize("fmt", ["q4", "q4f32"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_mf_q4_small_m(torch, ctx, orc, m, in_, out, fmt, xdt):
+    # Q4_0 plain calls with 4 < m <= 8 take the MFMA decode kernel as well
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=m * 17 + in_, dtype=xdt).reshape(m, in_)
+    note(f"mf {fmt} {xdt} m={m} {out}x{in_}")
+    w, dense, s, off = make(raster_amd, ctx, orc, fmt, out, in_, seed=out + 2 * in_)
+    y = run(torch, w, x, xdt, "f32")
+    y2 = run(torch, w, x, xdt, "f32")
+    w.destroy()
+    assert np.array_equal(y, y2), "the K-slices are added in a fixed order"
+    rows = np.unique(np.linspace(0, out - 1, min(out, 256)).astype(np.int64))
+    ref = x.astype(np.float64) @ dense[rows].astype(np.float64).T
+    assert orc.normwise_relerr(y[:, rows], ref) < (TOL_F32 if xdt == "f32" else TOL_BF16)
+    assert np.all(np.abs(y[:, rows] - ref) <= mf_bound(x, dense[rows], s[rows], off))
+
+
 def test_mf_special_activations(torch, ctx, orc):
     # one block holding 1e30 and 1e-30, a zero row, an inf row, a NaN row and
     # a row near the bottom of the normal range: finite rows stay inside the
