@@ -462,6 +462,10 @@ MfPlan plan_gemv_mf(int64_t m, int64_t k, int64_t npad, int x_dtype, int format,
   MfPlan p{};
   const int64_t m_min = format == RQ_Q4_0 ? 5 : 9;
   if (m < m_min || m > 16 || (x_dtype != RQ_F32 && x_dtype != RQ_BF16) || k % 32 != 0 || k < 32) return p;
+  // Q8_0 (8-byte loads, no quads) only for small weights: at 4096 x 4096
+  // m = 12 / 16 15.1 / 15.4 us against 26.9 for the int8-level kernel, at
+  // K = 8192, N = 28672 81 / 90 / 101 us against 62 / 66 / 70 (m = 9 / 12 / 16)
+  if (format == RQ_Q8_0 && npad * k > (int64_t(32) << 20)) return p;
   const int parts = x_dtype == RQ_F32 ? 2 : 1;
   const int64_t nkb = k / 32, ngroups = npad / 16;
   p.kw = 1;
