@@ -304,6 +304,61 @@ int rq_qmatmul_dx(rq_ctx ctx, rq_weight w, const float* dy, float* dx, int64_t m
 int rq_qlinear_q8_dx(rq_ctx ctx, const float* dy, const int8_t* codes, const float* scales, int64_t m, int64_t in,
                      int64_t out, float* dx);
 
+/* ---- ingestion helpers and the int8 linear op ------------------------------ */
+
+/* nextpad (raster/quant/pack.clj:30-33): *inp = in rounded up to a multiple of
+ * 256, the K-quant super-block. q4k-of (pack.clj:45-53) zero-pads each row of
+ * W to that width before quantize-weight-q4k and reports it as the weight's
+ * `in`, so its buffer set goes to rq_weight_create_q4k with in = *inp; the
+ * caller zero-pads x to the same width, and the padded columns then add
+ * nothing (their q8_K codes and sums are 0). Host-only, no device work. */
+int rq_nextpad(int64_t in, int64_t* inp);
+
+/* q8-quantize (raster/quant/train.clj:34-58) on the device: a row-major f32
+ * W[out*in] (device, 16-byte aligned, in % 32 == 0) to signed Q8_0 codes
+ * int8[out*in] and scales f32[out*in/32] (device, 4-byte aligned): per row and
+ * 32-block d = max|w| / 127 in double, code = clamp(Math/round(w / d), -127,
+ * 127) (0 when d == 0), scale = (float) d. Bitwise equal to the reference on
+ * finite input; the outputs feed rq_weight_create_q8 after a download, or
+ * stay on the device. Asynchronous on `stream`. */
+int rq_q8_quantize(rq_ctx ctx, const float* W, int64_t out, int64_t in, int8_t* codes, float* scales,
+                   void* stream);
+
+/* q4k-of (raster/quant/pack.clj:45-53) on the device: W f32[out*in]
+ * (row-major, device) with each row zero-padded to *inp = nextpad(in), then
+ * quantize-weight-q4k (raster/compiler/backend/cpu/quant.clj:92-137) over the
+ * out * *inp values. Outputs (device): wq u8[out*inp/2] (16-byte aligned; the
+ * bytes q4k-of reads as little-endian int32 words), da, db f32[out*inp/256],
+ * aq u8[out*inp/32], bq i8[out*inp/32] -- the arrays rq_weight_create_q4k
+ * takes with in = *inp. With in % 256 == 0 this is quantize-weight-q4k of W.
+ * The reference's double arithmetic step for step (only maxima cross lanes):
+ * bitwise equal on finite input. Asynchronous on `stream`; *inp is set on
+ * return. */
+int rq_q4k_of(rq_ctx ctx, const float* W, int64_t out, int64_t in, uint8_t* wq, float* da, float* db, uint8_t* aq,
+              int8_t* bq, int64_t* inp, void* stream);
+
+/* quantize-weight-q6k (raster/compiler/backend/cpu/quant.clj:214-239) on the
+ * device over a row-major W f32[out*in] (in % 256 == 0, 16-byte aligned):
+ * wq u8[out*in] (16-byte aligned), sc i8[out*in/16], ds f32[out*in/256], the
+ * arrays rq_weight_create_q6k takes. Bitwise equal on finite input. */
+int rq_quantize_weight_q6k(rq_ctx ctx, const float* W, int64_t out, int64_t in, uint8_t* wq, int8_t* sc, float* ds,
+                           void* stream);
+
+/* qlinear-i8! / qlinear-i8-q8! (raster/quant/op.clj:43-51,81-90) with their
+ * argument list (x wqi wsi y in out) on host arrays: x f32[in], the x8
+ * repack-stream weight (wqi, wsi as for rq_weight_create_x8; nibble = 1 for
+ * the Q4_0 op qlinear-i8!, 0 for the zero-point-128 Q8 op qlinear-i8-q8!), y
+ * f32[out] fully overwritten (:overwrite 3, op.clj:75-79). x is quantized
+ * inside the kernel by quantize-act-i8's math (as quantize-act-i8-par,
+ * cpu/quant.clj:399-415) and the exact int8 block dots are scaled and summed
+ * in f32, which is the reference's numerics (qmatmul-q4-x8! / qmatmul-q8-x8!,
+ * raster/quant/kernels.clj:216-247,308-333, sum their f32 lanes in another
+ * order). Uploads a temporary weight per call and syncs; callers that call
+ * again with the same weight keep it resident instead (rq_weight_create_x8
+ * once, then rq_qmatmul_fused with act_i8 = 1 per call). */
+int rq_qlinear_i8(rq_ctx ctx, const float* x, const uint8_t* wqi, const float* wsi, int nibble, float* y,
+                  int64_t in, int64_t out);
+
 #ifdef __cplusplus
 }
 #endif

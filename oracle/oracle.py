@@ -89,7 +89,6 @@ def _declare(L):
         "rqo_qlinear_q4": ([p, p, p, p, i64, i64, i64, p], None),
         "rqo_quantize_act_i8": ([p, i64, i64, p, p, p], None),
         "rqo_qmatmul_q4_composable": ([p, p, p, p, p, p, i64, i64, i64, i64], None),
-        "rqo_qmatmul_q8_composable": ([p, p, p, p, p, i64, i64], None),
         "rqo_repack_x8": ([p, p, i64, i64, C.c_int, p, p], C.c_int),
         "rqo_wi8_dot_q4_x8": ([p, i64, p, i64, p], None),
         "rqo_wi8_dot_q8_x8": ([p, i64, p, i64, p], None),
@@ -101,6 +100,8 @@ def _declare(L):
         "rqo_i8gemv_dp4a": ([p, p, p, i64, i64], None),
         "rqo_dense_matmul_nt_f64": ([p, p, i64, i64, i64, p], None),
         "rqo_quantize_weight_q4k": ([p, i64, p, p, p, p, p], None),
+        "rqo_nextpad": ([i64], C.c_int64),
+        "rqo_q4k_of": ([p, i64, i64, p, p, p, p, p], C.c_int64),
         "rqo_dequant_q4k": ([p, p, p, p, p, i64, p], None),
         "rqo_quantize_weight_q6k": ([p, i64, p, p, p], None),
         "rqo_dequant_q6k": ([p, p, p, i64, p], None),
@@ -286,14 +287,6 @@ def qmatmul_q4_composable(xq, xs, xsum, wq, ws, in_: int, out: int) -> np.ndarra
     return y
 
 
-def qmatmul_q8_composable(xq, xs, codes, ws, in_: int, out: int) -> np.ndarray:
-    xq, xs = _c(xq, np.int8), _c(xs, np.float32)
-    codes, ws = _c(codes, np.int8), _c(ws, np.float32)
-    y = np.zeros(out, np.float32)
-    lib().rqo_qmatmul_q8_composable(_ptr(xq), _ptr(xs), _ptr(codes), _ptr(ws), _ptr(y), in_, out)
-    return y
-
-
 def repack_x8(wq, ws, out: int, in_: int, nibble: bool):
     """raster.compiler.core.layout/repack (NC=8) -> (wqi, wsi)."""
     wq, ws = _c(wq, np.uint8), _c(ws, np.float32)
@@ -439,6 +432,27 @@ def quantize_weight_q4k(w):
     aq, bq = np.empty(n // 32, np.uint8), np.empty(n // 32, np.int8)
     lib().rqo_quantize_weight_q4k(_ptr(w), n, _ptr(wq), _ptr(da), _ptr(db), _ptr(aq), _ptr(bq))
     return wq, da, db, aq, bq
+
+
+def nextpad(in_: int) -> int:
+    """raster.quant.pack/nextpad: in rounded up to a multiple of 256."""
+    return int(lib().rqo_nextpad(in_))
+
+
+def q4k_of(W, out: int, in_: int):
+    """raster.quant.pack/q4k-of -> (wq, da, db, aq, bq, inp): rows zero-padded to
+    inp = nextpad(in), then quantize-weight-q4k; wq is the nibble bytes (the
+    reference reinterprets them as little-endian int32 words)."""
+    W = _c(W, np.float32)
+    inp = nextpad(in_)
+    n = out * inp
+    wq = np.empty(n // 2, np.uint8)
+    da, db = np.empty(n // 256, np.float32), np.empty(n // 256, np.float32)
+    aq, bq = np.empty(n // 32, np.uint8), np.empty(n // 32, np.int8)
+    got = lib().rqo_q4k_of(_ptr(W), out, in_, _ptr(wq), _ptr(da), _ptr(db), _ptr(aq), _ptr(bq))
+    if got != inp:
+        raise MemoryError("rqo_q4k_of failed")
+    return wq, da, db, aq, bq, inp
 
 
 def dequant_q4k(wq, da, db, aq, bq, n: int) -> np.ndarray:

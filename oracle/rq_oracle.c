@@ -12,6 +12,7 @@
 #include "rq_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------------- */
@@ -392,20 +393,6 @@ void rqo_qmatmul_q4_composable(const int8_t* xq, const float* xs, const int32_t*
   }
 }
 
-void rqo_qmatmul_q8_composable(const int8_t* xq, const float* xs, const int8_t* codes, const float* ws,
-                               float* y, int64_t in, int64_t out) {
-  int64_t nb = in / 32;
-  for (int64_t o = 0; o < out; o++) {
-    double a = 0.0;
-    for (int64_t b = 0; b < nb; b++) {
-      int64_t dot = 0;
-      for (int k = 0; k < 32; k++) dot += (int64_t)codes[o * in + b * 32 + k] * (int64_t)xq[b * 32 + k];
-      a += ((double)xs[b] * (double)ws[o * nb + b]) * (double)dot;
-    }
-    y[o] = (float)a;
-  }
-}
-
 /* ------------------------------------------------------------------------- */
 /* x8 column-interleaved layout                                               */
 /* ------------------------------------------------------------------------- */
@@ -633,6 +620,25 @@ void rqo_quantize_weight_q4k(const float* w, int64_t len, uint8_t* wq, float* da
       }
     }
   }
+}
+
+/* nextpad: raster/quant/pack.clj:30-33, 256 * ceil(in / 256.0) in double. */
+int64_t rqo_nextpad(int64_t in) { return (int64_t)(256.0 * ceil((double)in / 256.0)); }
+
+/* q4k-of: raster/quant/pack.clj:35-53. Each row of the row-major [out x in] W
+ * is copied into a zero row of inp = nextpad(in) (padw, pack.clj:35-43), and the
+ * padded matrix is quantized by quantize-weight-q4k as one array. The outputs
+ * are sized for out * inp; wq holds the nibble bytes that q4k-of reinterprets
+ * as little-endian int32 words (pack.clj:20-28), which are the same bytes. */
+int64_t rqo_q4k_of(const float* W, int64_t out, int64_t in, uint8_t* wq, float* da, float* db, uint8_t* aq,
+                   int8_t* bq) {
+  const int64_t inp = rqo_nextpad(in);
+  float* Wp = (float*)calloc((size_t)(out * inp), sizeof(float));
+  if (!Wp) return -1;
+  for (int64_t o = 0; o < out; o++) memcpy(Wp + o * inp, W + o * in, (size_t)in * sizeof(float));
+  rqo_quantize_weight_q4k(Wp, out * inp, wq, da, db, aq, bq);
+  free(Wp);
+  return inp;
 }
 
 /* dequant-q4k: quant.clj:139-156 */

@@ -97,9 +97,6 @@ void rqo_quantize_act_i8(const float* x, int64_t M, int64_t in, int8_t* xq, floa
 void rqo_qmatmul_q4_composable(const int8_t* xq, const float* xs, const int32_t* xsum,
                                const uint8_t* wq, const float* ws, float* y,
                                int64_t in, int64_t out, int64_t o_start, int64_t o_count);
-/* Row-major Q8 (signed codes) twin of the composable fold: y[o] = sum_b xs*ws*dot. */
-void rqo_qmatmul_q8_composable(const int8_t* xq, const float* xs, const int8_t* codes,
-                               const float* ws, float* y, int64_t in, int64_t out);
 
 /* ---- column-interleaved x8 layout (CPU stream-gemv layout) ---- */
 /* repack: raster/compiler/core/layout.clj:246-286 (tile 8, k-group 4).
@@ -160,6 +157,12 @@ void rqo_decoder_layer(float* x, const int8_t* const* w, const float* const* s, 
  * (0..63), bq[len/32] (-32..31). */
 void rqo_quantize_weight_q4k(const float* w, int64_t len, uint8_t* wq, float* da, float* db, uint8_t* aq,
                              int8_t* bq);
+/* nextpad (raster/quant/pack.clj:30-33): in rounded up to a multiple of 256 */
+int64_t rqo_nextpad(int64_t in);
+/* q4k-of (raster/quant/pack.clj:45-53): rows zero-padded to inp = nextpad(in),
+ * then quantize-weight-q4k over out * inp values. Returns inp (-1: no memory). */
+int64_t rqo_q4k_of(const float* W, int64_t out, int64_t in, uint8_t* wq, float* da, float* db, uint8_t* aq,
+                   int8_t* bq);
 /* dequant-q4k (quant.clj:139-156): x = (da*aq)*q + (db*bq), in double, one narrowing */
 void rqo_dequant_q4k(const uint8_t* wq, const float* da, const float* db, const uint8_t* aq, const int8_t* bq,
                      int64_t len, float* out);

@@ -54,6 +54,11 @@ SIGNATURES = {
     "rq_qlinear_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
     "rq_qmatmul_dx": ([_p, _p, _p, _p, _i64, _p], _i),
     "rq_qlinear_q8_dx": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
+    "rq_nextpad": ([_i64, C.POINTER(_i64)], _i),
+    "rq_q8_quantize": ([_p, _p, _i64, _i64, _p, _p, _p], _i),
+    "rq_qlinear_i8": ([_p, _p, _p, _p, _i, _p, _i64, _i64], _i),
+    "rq_q4k_of": ([_p, _p, _i64, _i64, _p, _p, _p, _p, _p, C.POINTER(_i64), _p], _i),
+    "rq_quantize_weight_q6k": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
 }
 
 

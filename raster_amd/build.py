@@ -1,11 +1,14 @@
 """Builds raster_amd/librq.so (gfx950 HIP kernels + the C ABI of include/rq.h).
 
-    python -m raster_amd.build
+    python -m raster_amd.build [--force]
 
-One hipcc invocation over every .hip file in raster_amd/csrc. Packed-FP32
-instruction selection is switched off (-packed-fp32-ops) for every device
-compile; hipcc's host pass warns that it does not know that feature, which is
-harmless. MFMA accumulators are kept in VGPRs (-amdgpu-mfma-vgpr-form).
+Each .hip file in raster_amd/csrc is compiled to an object under
+raster_amd/_build/ (in parallel), then the objects are linked into librq.so.
+Without --force only objects older than their source or a shared header are
+rebuilt. Packed-FP32 instruction selection is switched off
+(-packed-fp32-ops) for every device compile; hipcc's host pass warns that it
+does not know that feature, which is harmless. MFMA accumulators are kept in
+VGPRs (-amdgpu-mfma-vgpr-form).
 """
 from __future__ import annotations
 
@@ -14,11 +17,22 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librq.so")
+HEADERS = [os.path.join(CSRC, "rq_internal.h"), os.path.join(os.path.dirname(HERE), "include", "rq.h")]
 ARCH = "gfx950"
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: without it the register allocator copies
+    # accumulator tiles between AGPRs around every MFMA
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-Wall", "-Wno-unused-function",
+]
 
 
 def hipcc() -> str:
@@ -32,28 +46,47 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    cmd = [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # MFMA accumulators in VGPRs: without it the register allocator copies
-        # accumulator tiles between AGPRs around every MFMA
-        "-mllvm", "-amdgpu-mfma-vgpr-form",
-        "-Wall", "-Wno-unused-function",
-        "-o", tmp, *sources(),
-    ]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
+def _stale(src: str, obj: str) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(p) > t for p in [src, *HEADERS])
+
+
+def _compile(src: str, obj: str) -> tuple[str, int, list[str]]:
+    tmp = obj + ".tmp"
+    r = subprocess.run([hipcc(), *FLAGS, "-c", "-o", tmp, src], capture_output=True, text=True)
     errs = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
-    if r.returncode != 0:
-        raise RuntimeError("librq build failed:\n" + "\n".join(errs))
-    if verbose and errs:
-        print("\n".join(errs), file=sys.stderr)
-    os.replace(tmp, LIB)
+    if r.returncode == 0:
+        os.replace(tmp, obj)
+    return src, r.returncode, errs
+
+
+def build(verbose: bool = False, force: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    pairs = [(s, os.path.join(OBJ, os.path.basename(s)[:-4] + ".o")) for s in sources()]
+    todo = [(s, o) for s, o in pairs if force or _stale(s, o)]
+    jobs = jobs or max(1, min(len(todo), os.cpu_count() or 1, 8))
+    failed = []
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for src, rc, errs in ex.map(lambda so: _compile(*so), todo):
+            if rc != 0:
+                failed.append(f"{os.path.basename(src)}:\n" + "\n".join(errs))
+            elif verbose and errs:
+                print("\n".join(errs), file=sys.stderr)
+    if failed:
+        raise RuntimeError("librq build failed:\n" + "\n\n".join(failed))
+    if todo or force or not os.path.exists(LIB):
+        tmp = LIB + ".tmp"
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for _, o in pairs]]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("librq link failed:\n" + r.stderr)
+        os.replace(tmp, LIB)
+    if verbose:
+        print(f"compiled {len(todo)} of {len(pairs)} sources", file=sys.stderr)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, force="--force" in sys.argv))

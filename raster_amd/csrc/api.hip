@@ -955,6 +955,84 @@ int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m,
   return RQ_OK;
 }
 
+int rq_nextpad(int64_t in, int64_t* inp) {
+  if (!inp) return fail(RQ_ERR_NULL, "inp is NULL");
+  if (in <= 0 || in > ((int64_t)1 << 40)) return fail(RQ_ERR_SHAPE, "in must be in 1 .. 2^40");
+  *inp = (in + 255) / 256 * 256;
+  return RQ_OK;
+}
+
+int rq_q8_quantize(rq_ctx h, const float* W, int64_t out, int64_t in, int8_t* codes, float* scales, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!W || !codes || !scales) return fail(RQ_ERR_NULL, "W, codes or scales is NULL");
+  if (int s = check_shape(out, in)) return s;
+  if (((uintptr_t)W & 15) != 0) return fail(RQ_ERR_SHAPE, "W must be 16-byte aligned");
+  if (((uintptr_t)codes & 3) != 0 || ((uintptr_t)scales & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "codes and scales must be 4-byte aligned");
+  if (int s = set_device(c)) return s;
+  // q8-quantize's per-block math is quantize-act-i8's (d = max|w| / 127 in
+  // double, Math/round, clamp to +-127): the same kernel over out rows of in
+  hipError_t e = launch_quantize_act_i8(W, out, in, codes, scales, nullptr, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "quantizer launch");
+  return RQ_OK;
+}
+
+int rq_q4k_of(rq_ctx h, const float* W, int64_t out, int64_t in, uint8_t* wq, float* da, float* db, uint8_t* aq,
+              int8_t* bq, int64_t* inp, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!W || !wq || !da || !db || !aq || !bq || !inp) return fail(RQ_ERR_NULL, "NULL argument");
+  if (out <= 0 || in <= 0) return fail(RQ_ERR_SHAPE, "out and in must be positive");
+  if (in > (int64_t)1 << 30 || out > (int64_t)1 << 30) return fail(RQ_ERR_SHAPE, "dimension too large");
+  if (((uintptr_t)wq & 15) != 0 || ((uintptr_t)da & 3) != 0 || ((uintptr_t)db & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "wq must be 16-byte aligned, da and db 4-byte aligned");
+  if (int s = rq_nextpad(in, inp)) return s;
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_q4k_encode(W, out, in, *inp, wq, da, db, aq, bq, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "encoder launch");
+  return RQ_OK;
+}
+
+int rq_quantize_weight_q6k(rq_ctx h, const float* W, int64_t out, int64_t in, uint8_t* wq, int8_t* sc, float* ds,
+                           void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!W || !wq || !sc || !ds) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  if (in % 256 != 0) return fail(RQ_ERR_SHAPE, "quantize-weight-q6k needs in % 256 == 0 (super-blocks of 256)");
+  if (((uintptr_t)W & 15) != 0 || ((uintptr_t)wq & 15) != 0 || ((uintptr_t)ds & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "W and wq must be 16-byte aligned, ds 4-byte aligned");
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_q6k_encode(W, out, in, wq, sc, ds, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "encoder launch");
+  return RQ_OK;
+}
+
+int rq_qlinear_i8(rq_ctx h, const float* x, const uint8_t* wqi, const float* wsi, int nibble, float* y, int64_t in,
+                  int64_t out) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!x || !wqi || !wsi || !y) return fail(RQ_ERR_NULL, "NULL argument");
+  if (int s = check_shape(out, in)) return s;
+  if (out % 8 != 0) return fail(RQ_ERR_SHAPE, "x8 layout needs out % 8 == 0");
+  rq_weight w = nullptr;
+  if (int s = rq_weight_create_x8(h, wqi, wsi, nibble ? 1 : 0, out, in, &w)) return s;
+  void *dx = nullptr, *dy = nullptr;
+  int s = rq_buf_alloc(h, (size_t)in * 4, &dx);
+  if (!s) s = rq_buf_alloc(h, (size_t)out * 4, &dy);
+  if (!s) s = rq_upload(h, dx, x, (size_t)in * 4, nullptr);
+  rq_fused_ops ops = {nullptr, 0.0f, nullptr, 0, 1};  // act_i8: quantize-act-i8 in the kernel
+  if (!s) s = rq_qmatmul_fused(h, w, dx, RQ_F32, dy, RQ_F32, 1, &ops, nullptr);
+  if (!s) s = rq_download(h, y, dy, (size_t)out * 4, nullptr);
+  std::string keep = s ? t_err : std::string();
+  if (dx) rq_buf_free(h, dx);
+  if (dy) rq_buf_free(h, dy);
+  rq_weight_destroy(w);
+  if (s) t_err = keep;
+  return s;
+}
+
 int rq_qlinear_q8_dx(rq_ctx h, const float* dy, const int8_t* codes, const float* scales, int64_t m, int64_t in,
                      int64_t out, float* dx) {
   Ctx* c = reinterpret_cast<Ctx*>(h);

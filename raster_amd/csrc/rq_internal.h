@@ -180,6 +180,12 @@ size_t decode_attention_lds(int64_t pos, int64_t head_dim);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
                                    double scale, float* out, hipStream_t stream);
+// Weight encoders (encode.hip): q4k-of (rows zero-padded from in to inp) and
+// quantize-weight-q6k (in % 256 == 0), device arrays in, device arrays out.
+hipError_t launch_q4k_encode(const float* W, int64_t out, int64_t in, int64_t inp, uint8_t* wq, float* da, float* db,
+                             uint8_t* aq, int8_t* bq, hipStream_t stream);
+hipError_t launch_q6k_encode(const float* W, int64_t out, int64_t in, uint8_t* wq, int8_t* sc, float* ds,
+                             hipStream_t stream);
 // Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
                                int64_t in, int64_t npad, uint8_t* q, void* s, void* s_rb, hipStream_t stream);

@@ -25,7 +25,8 @@ from ._lib import RQ_BF16, RQ_F16, RQ_F32, RQ_Q4_0, RQ_Q4_K, RQ_Q6_K, RQ_Q8_0, R
 
 __all__ = [
     "Context", "QWeight", "RqError", "context", "decode_attention", "quantize_act_i8", "quantize_act_q8k",
-    "qlinear_q8", "qlinear_q8_dx", "dequant_q8_dense",
+    "qlinear_q8", "qlinear_q8_dx", "dequant_q8_dense", "qlinear_i8", "qlinear_i8_q8", "nextpad", "q8_quantize",
+    "q4k_of", "quantize_weight_q6k",
     "RQ_F32", "RQ_BF16", "RQ_F16", "RQ_Q8_0", "RQ_Q4_0",
 ]
 
@@ -399,6 +400,70 @@ def decode_attention(ctx: Context, q, k, v, kcache, vcache, pos: int, n_q: int, 
     return out
 
 
+def nextpad(in_: int) -> int:
+    """raster.quant.pack/nextpad: `in` rounded up to a multiple of 256 (rq_nextpad)."""
+    v = C.c_int64()
+    call("rq_nextpad", int(in_), C.byref(v))
+    return v.value
+
+
+def q8_quantize(ctx: Context, W, out: int, in_: int, stream=None):
+    """raster.quant.train/q8-quantize on the device (rq_q8_quantize): W f32
+    [out*in] CUDA tensor -> (codes int8 [out, in], scales f32 [out, in/32])."""
+    import torch
+
+    _need(W.is_cuda and W.is_contiguous() and W.dtype == torch.float32 and W.numel() == out * in_,
+          "W must be a contiguous f32 CUDA tensor of out*in elements")
+    codes = torch.empty((out, in_), dtype=torch.int8, device=W.device)
+    scales = torch.empty((out, in_ // 32), dtype=torch.float32, device=W.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(W.device)
+    call("rq_q8_quantize", ctx.handle, C.c_void_p(W.data_ptr()), out, in_, C.c_void_p(codes.data_ptr()),
+         C.c_void_p(scales.data_ptr()), _stream_ptr(stream))
+    return codes, scales
+
+
+def q4k_of(ctx: Context, W, out: int, in_: int, stream=None):
+    """raster.quant.pack/q4k-of on the device (rq_q4k_of): W f32 [out*in] CUDA
+    tensor, rows zero-padded to inp = nextpad(in) -> dict(wq, da, db, aq, bq,
+    in=inp, out=out) of CUDA tensors, the arrays QWeight.q4k takes."""
+    import torch
+
+    _need(W.is_cuda and W.is_contiguous() and W.dtype == torch.float32 and W.numel() == out * in_,
+          "W must be a contiguous f32 CUDA tensor of out*in elements")
+    inp = nextpad(in_)
+    n = out * inp
+    dev = W.device
+    wq = torch.empty(n // 2, dtype=torch.uint8, device=dev)
+    da, db = torch.empty(n // 256, device=dev), torch.empty(n // 256, device=dev)
+    aq, bq = torch.empty(n // 32, dtype=torch.uint8, device=dev), torch.empty(n // 32, dtype=torch.int8, device=dev)
+    got = C.c_int64()
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    ptr = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    call("rq_q4k_of", ctx.handle, ptr(W), out, in_, ptr(wq), ptr(da), ptr(db), ptr(aq), ptr(bq), C.byref(got),
+         _stream_ptr(stream))
+    return {"wq": wq, "da": da, "db": db, "aq": aq, "bq": bq, "in": got.value, "out": out}
+
+
+def quantize_weight_q6k(ctx: Context, W, out: int, in_: int, stream=None):
+    """quantize-weight-q6k on the device (rq_quantize_weight_q6k), in % 256 == 0:
+    W f32 [out*in] CUDA tensor -> (wq u8 [out*in], sc i8 [out*in/16], ds f32 [out*in/256])."""
+    import torch
+
+    _need(W.is_cuda and W.is_contiguous() and W.dtype == torch.float32 and W.numel() == out * in_,
+          "W must be a contiguous f32 CUDA tensor of out*in elements")
+    dev = W.device
+    wq = torch.empty(out * in_, dtype=torch.uint8, device=dev)
+    sc = torch.empty(out * in_ // 16, dtype=torch.int8, device=dev)
+    ds = torch.empty(out * in_ // 256, dtype=torch.float32, device=dev)
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    call("rq_quantize_weight_q6k", ctx.handle, C.c_void_p(W.data_ptr()), out, in_, C.c_void_p(wq.data_ptr()),
+         C.c_void_p(sc.data_ptr()), C.c_void_p(ds.data_ptr()), _stream_ptr(stream))
+    return wq, sc, ds
+
+
 def _need(cond: bool, msg: str) -> None:
     if not cond:
         raise ValueError(msg)
@@ -441,3 +506,24 @@ def dequant_q8_dense(codes, scales, in_: int, out: int, ctx: Context | None = No
         return w.dequant().cpu().numpy().ravel()
     finally:
         w.destroy()
+
+
+def qlinear_i8(x, wqi, wsi, y, in_: int, out: int, ctx: Context | None = None, nibble: bool = True) -> np.ndarray:
+    """raster.quant.op/qlinear-i8! (x wqi wsi y in out): y[out] = the int8
+    linear of x[in] over an x8 repack-stream weight, y overwritten and returned.
+    nibble=False is qlinear-i8-q8! (the zero-point-128 Q8 layout)."""
+    ctx = ctx or context()
+    x = np.ascontiguousarray(x, np.float32)
+    wqi = np.ascontiguousarray(wqi).view(np.uint8)
+    wsi = np.ascontiguousarray(wsi, np.float32)
+    _need(isinstance(y, np.ndarray) and y.dtype == np.float32 and y.flags["C_CONTIGUOUS"] and y.size == out,
+          "y must be a contiguous float32 array of out elements")
+    _need(x.size == in_ and wsi.size == (out // 8) * (in_ // 32) * 8
+          and wqi.size == (out // 8) * (in_ // 32) * (128 if nibble else 256), "array sizes do not match in, out")
+    call("rq_qlinear_i8", ctx.handle, _np_ptr(x), _np_ptr(wqi), _np_ptr(wsi), 1 if nibble else 0, _np_ptr(y), in_, out)
+    return y
+
+
+def qlinear_i8_q8(x, wqi, wsi, y, in_: int, out: int, ctx: Context | None = None) -> np.ndarray:
+    """raster.quant.op/qlinear-i8-q8!: qlinear_i8 over the Q8 x8 layout."""
+    return qlinear_i8(x, wqi, wsi, y, in_, out, ctx, nibble=False)

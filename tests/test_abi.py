@@ -64,3 +64,16 @@ def test_ctx_create_without_gpu_reports_device_error():
     h = C.c_void_p()
     assert _lib.lib().rq_ctx_create(0, C.byref(h)) == _lib.RQ_ERR_DEVICE
     assert not h.value
+
+
+def test_nextpad_through_the_abi():
+    # test/raster/quant/pack_test.clj:14-18, host-side only (no device work)
+    L = _lib.lib()
+    v = C.c_int64()
+    got = []
+    for i in (1, 256, 257, 640):
+        assert L.rq_nextpad(i, C.byref(v)) == _lib.RQ_OK
+        got.append(v.value)
+    assert got == [256, 256, 512, 768]
+    assert L.rq_nextpad(0, C.byref(v)) == _lib.RQ_ERR_SHAPE
+    assert L.rq_nextpad(5, None) == _lib.RQ_ERR_NULL

@@ -349,10 +349,14 @@ def test_decode_special_activations(torch, ctx, orc):
     assert not np.any(np.isfinite(ref[3])) and not np.any(np.isfinite(ref[4]))
 
 
-@pytest.mark.parametrize("m,in_,out", [(2, 20480, 16), (16, 8192, 48), (9, 4096, 4096), (16, 14336, 64)])
+@pytest.mark.parametrize("m,in_,out", [(2, 20480, 16), (12, 8192, 4160), (16, 8192, 48), (9, 4096, 4096),
+                                       (16, 14336, 64)])
 def test_decode_k_split(torch, ctx, orc, m, in_, out):
-    # activations too long for one workgroup's LDS: the decode kernel cuts K
-    # into slices whose partial sums a second kernel adds in slice order
+    # K cut into slices whose partial sums a second kernel adds in slice order.
+    # m = 2 and m = 12 over a weight above 32 Mi elements (34 Mi at 4160 x 8192):
+    # the int8-level decode kernel, its activations too long for one
+    # workgroup's LDS. The m = 9 / 16 rows below 32 Mi elements: the MFMA
+    # decode kernel, whose slices also spread a thin grid over the CUs.
     import raster_amd
 
     codes, scales = wl.q8_weights(out, in_, seed=8)

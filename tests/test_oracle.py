@@ -190,6 +190,59 @@ def test_parametric_encode(orc):
     assert e8 < 0.2 * e4
 
 
+def _decode_unsigned(wq, ws, n, zp, nibble):
+    """Independent numpy decode of the parametric format
+    (raster/compiler/backend/cpu/quant.clj:27-39,60-67): per 32-block b, byte k of
+    a nibble block holds element k in its low nibble and element k + 16 in its
+    high nibble; W = d * (q - zp) with one f32 rounding of the exact product."""
+    nb = n // 32
+    if nibble:
+        by = wq.reshape(nb, 16).astype(np.int64)
+        q = np.concatenate([by & 0xF, by >> 4], axis=1)  # elements 0..15, then 16..31
+    else:
+        q = wq.reshape(nb, 32).astype(np.int64)
+    return q, (ws.astype(np.float64)[:, None] * (q - zp)).astype(np.float32).ravel()
+
+
+@pytest.mark.parametrize("bits,zp,nibble", [(4, 8, True), (8, 128, False)])
+def test_parametric_encode_decode_pinned(orc, bits, zp, nibble):
+    # Pins the encoder and the decoder with checks a swapped nibble order, a
+    # dropped zero point or a wrong scale sign fails:
+    #  * the decoder equals an independent decode bit for bit;
+    #  * every element whose code is not clamped lies within |d|/2 of its
+    #    reconstruction (round to nearest), clamped ones sit at the range end;
+    #  * the block's extreme element (d = v / -zp, quant.clj:55-60) is code 0
+    #    and reconstructs exactly.
+    rng = np.random.default_rng(40 + bits)
+    n = 32 * 96
+    w = (rng.standard_normal(n) * rng.uniform(0.01, 4.0, n)).astype(np.float32)
+    w[32:64] = 0.0  # an all-zero block: d = 0, every code = zp, W = 0
+    wq, ws = orc.quantize_weight(w, bits, zp, nibble)
+    q, dec = _decode_unsigned(wq, ws, n, zp, nibble)
+    assert np.array_equal(orc.dequant_weight(wq, ws, n, zp, nibble).view(np.uint32), dec.view(np.uint32))
+    d = ws.astype(np.float64)
+    wb = w.reshape(-1, 32).astype(np.float64)
+    qmax = (1 << bits) - 1
+    inner = (q > 0) & (q < qmax)
+    err = np.abs(dec.reshape(-1, 32).astype(np.float64) - wb)
+    half = np.abs(d)[:, None] / 2 * (1 + 1e-6) + 1e-30
+    assert np.all(err[inner] <= np.broadcast_to(half, err.shape)[inner])
+    ext = np.argmax(np.abs(wb), axis=1)
+    nz = d != 0
+    assert np.all(q[np.arange(len(d)), ext][nz] == 0)
+    assert np.array_equal(dec.reshape(-1, 32)[np.arange(len(d)), ext][nz], w.reshape(-1, 32)[np.arange(len(d)), ext][nz])
+    assert np.all(q[1] == zp) and np.all(dec[32:64] == 0)
+    # the nibble order itself: a block whose element k is k - 16 (k < 16) and
+    # k - 15 (k >= 16) encodes to bytes whose low nibble is element k
+    if nibble:
+        blk = np.concatenate([np.arange(-16, 0), np.arange(1, 17)]).astype(np.float32)
+        bq, bs = orc.quantize_weight(blk, 4, 8, True)
+        assert bs[0] == np.float32(2.0)  # d = -16 / -8
+        # Java Math/round: ties toward +infinity (-7.5 -> -7)
+        assert np.array_equal(bq & 0xF, np.floor(blk[:16] / 2 + 0.5).astype(np.int64) + 8)
+        assert np.array_equal(bq >> 4, np.minimum(np.floor(blk[16:] / 2 + 0.5).astype(np.int64) + 8, 15))
+
+
 def test_q4_dequant_closed_form(orc):
     rng = np.random.default_rng(9)
     out, in_ = 8, 128
@@ -582,3 +635,46 @@ def test_quantize_act_q8k_properties(orc, sub):
     nz = d > 0
     assert np.all(np.abs(q[nz] * d[nz, None] - sb[nz]) <= d[nz, None] / 2 + 1e-12)
     assert np.all(xq[:256] == 0)
+
+
+# ---------------------------------------------------------------- q4k-of ingestion
+def test_nextpad_known_answers(orc):
+    # test/raster/quant/pack_test.clj:14-18
+    assert [orc.nextpad(i) for i in (1, 256, 257, 640)] == [256, 256, 512, 768]
+    assert orc.nextpad(512) == 512 and orc.nextpad(513) == 768
+
+
+def test_q4k_of_no_pad_matches_the_packer(orc):
+    # test/raster/quant/pack_test.clj:42-60: in = 256 needs no padding, so q4k-of
+    # is the CPU packer's output byte for byte
+    out, in_ = 2, 256
+    W = orc.jfill_uniform_centered(11, out * in_)
+    wq, da, db, aq, bq, inp = orc.q4k_of(W, out, in_)
+    ref = orc.quantize_weight_q4k(W)
+    assert inp == in_
+    for a, b in zip((wq, da, db, aq, bq), ref):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def test_q4k_of_pads_rows_with_zeros(orc):
+    # test/raster/quant/pack_test.clj:61-69: in = 640 pads rows to 768 and the
+    # padded packing equals packing the zero-padded W; and each row's first
+    # super-blocks (all real columns) equal the unpadded row's own packing
+    out, in_, inp = 3, 640, 768
+    W = orc.jfill_uniform_centered(13, out * in_)
+    wq, da, db, aq, bq, got = orc.q4k_of(W, out, in_)
+    assert got == inp
+    Wp = np.zeros((out, inp), np.float32)
+    Wp[:, :in_] = W.reshape(out, in_)
+    ref = orc.quantize_weight_q4k(Wp.ravel())
+    for a, b in zip((wq, da, db, aq, bq), ref):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    for o in range(out):
+        r = orc.quantize_weight_q4k(W.reshape(out, in_)[o, :512].copy())
+        assert np.array_equal(da.reshape(out, 3)[o, :2], r[1])
+        assert np.array_equal(wq.reshape(out, inp // 2)[o, :256], r[0])
+    # the padded columns of a zero-padded activation contribute nothing
+    x = np.zeros(inp, np.float32)
+    x[:in_] = orc.jfill_uniform_centered(14, in_)
+    xq, xs, bs = orc.quantize_act_q8k(x, 1, inp, 32)
+    assert np.all(xq[in_:] == 0) and np.all(bs[in_ // 32:] == 0)
