@@ -177,6 +177,26 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
 int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                void* stream);
 
+/* Bytes of the fixed device scratch behind rq_qmatmul_noalloc. */
+#define RQ_NOALLOC_SCRATCH_MAX (32u << 20)
+
+/* rq_qmatmul that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory mid-stream (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results as rq_qmatmul, bit for bit; no kernel-timing
+ * events are recorded. Where rq_qmatmul would use per-stream scratch (the
+ * packed activations of the bf16 GEMM, K-slice partial sums) this call uses a
+ * fixed device array of RQ_NOALLOC_SCRATCH_MAX bytes that each GPU holds from
+ * the first context created on it until the process ends; a call that needs
+ * more fails with RQ_ERR_SHAPE and a message saying so (for example bf16 x
+ * with m * in above 16 Mi elements). Every call on one GPU shares that GPU's
+ * array, whatever its context or stream: calls that may overlap on one GPU
+ * (different streams, or different host threads) race and must be ordered
+ * by the caller. Nothing in the array needs to start at zero: each call
+ * writes every scratch byte it later reads. */
+int rq_qmatmul_noalloc(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+                       void* stream);
+
 /* Options of rq_qmatmul_fused; a NULL / 0 field is off. They fold the
  * decoder glue around a linear into its decode kernel (Raster chains them as
  * separate ops, test/raster/dl/decoder_layer_gpu_test.clj:25-83):

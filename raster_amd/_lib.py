@@ -45,6 +45,7 @@ SIGNATURES = {
     "rq_weight_device_ptrs": ([_p, C.POINTER(_p), C.POINTER(_p)], _i),
     "rq_qmatmul": ([_p, _p, _p, _i, _p, _i, _i64, _p], _i),
     "rq_qmatmul_fused": ([_p, _p, _p, _i, _p, _i, _i64, _p, _p], _i),
+    "rq_qmatmul_noalloc": ([_p, _p, _p, _i, _p, _i, _i64, _p], _i),
     "rq_quantize_act_i8": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
     "rq_qmatmul_i8": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
     "rq_quantize_act_q8k": ([_p, _p, _i64, _i64, _i, _p, _p, _p, _p], _i),

@@ -16,6 +16,15 @@
 
 namespace rq {
 
+// Device scratch of rq_qmatmul_noalloc: a file-scope array that every GPU the
+// library runs on holds until the process ends. In host code `scratch` names a
+// host-side stand-in, not device memory: its device address (one per device)
+// comes from hipGetSymbolAddress at context creation and is kept in
+// g_scratch_ptr; only that address is passed to kernels.
+static constexpr size_t kNoAllocScratchBytes = (size_t)RQ_NOALLOC_SCRATCH_MAX;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static constexpr int kMaxDevices = 64;
+
 struct Ctx {
   uint32_t magic;
   int device;
@@ -46,6 +55,7 @@ static constexpr uint32_t kCtxMagic = 0x52514358u;     // "RQCX"
 static constexpr uint32_t kWeightMagic = 0x52515754u;  // "RQWT"
 
 static std::mutex g_mu;
+static void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device (under g_mu)
 static std::unordered_set<Ctx*> g_ctxs;
 static std::unordered_set<Weight*> g_weights;
 static thread_local std::string t_err;
@@ -300,6 +310,19 @@ int rq_ctx_create(int device, rq_ctx* out) {
   RQ_HIP(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
   if (std::string(p.gcnArchName).rfind("gfx950", 0) != 0)
     return fail(RQ_ERR_DEVICE, std::string("device is ") + p.gcnArchName + ", librq is built for gfx950");
+  if (device >= kMaxDevices) return fail(RQ_ERR_DEVICE, "device id above the library's device table");
+  {
+    // once per device, with the device current: the address of this device's
+    // copy of `scratch` (rq_qmatmul_noalloc)
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_scratch_ptr[device]) {
+      RQ_HIP(hipSetDevice(device), "hipSetDevice");
+      void* ptr = nullptr;
+      RQ_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+      if (!ptr) return fail(RQ_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+      g_scratch_ptr[device] = ptr;
+    }
+  }
   Ctx* c = new (std::nothrow) Ctx();
   if (!c) return fail(RQ_ERR_OOM, "host allocation failed");
   c->magic = kCtxMagic;
@@ -661,8 +684,37 @@ static int lookup(rq_ctx h, rq_weight wh, Ctx** c, Weight* copy) {
 namespace rq {
 
 // rq_qmatmul / rq_qmatmul_fused; ops == nullptr is the plain product.
+// The fixed device scratch of one rq_qmatmul_noalloc call: regions are taken
+// from `base` in order, 256-byte aligned, up to `cap` bytes.
+struct FixedScratch {
+  uint8_t* base;
+  size_t cap;
+  size_t used;
+};
+
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
-                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream);
+                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream,
+                      FixedScratch* fixed = nullptr);
+
+// A scratch region of `bytes` for one call: from the fixed scratch when the
+// call allocates nothing, else the stream's grow-only buffer (`which` 0: the
+// packed activations, 1: the K-slices' partial sums).
+static int call_scratch(Ctx* c, FixedScratch* fixed, hipStream_t stream, size_t bytes, int which, void** out) {
+  if (fixed) {
+    const size_t at = align256(fixed->used);
+    if (bytes > fixed->cap || at > fixed->cap - bytes)
+      return fail(RQ_ERR_SHAPE, "rq_qmatmul_noalloc: this call needs more than the " +
+                                    std::to_string(fixed->cap >> 20) + " MiB of fixed scratch (use rq_qmatmul)");
+    *out = fixed->base + at;
+    fixed->used = at + bytes;
+    return RQ_OK;
+  }
+  if (which == 0) return stream_pack(c, stream, bytes, out);
+  float* p = nullptr;
+  const int s = stream_split(c, stream, bytes, &p);
+  *out = p;
+  return s;
+}
 
 static bool kquant(const Weight& w) { return w.format == RQ_Q4_K || w.format == RQ_Q6_K; }
 static const char* kKquantMsg = "K-quant weights take q8_K activations: use rq_qmatmul_q8k";
@@ -708,7 +760,7 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
 // bf16 x, the MFMA decode kernel), else the GEMM for the activation dtype;
 // per-stream scratch and kernel timing around it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
-                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream) {
+                      int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream, FixedScratch* fixed) {
   if (int s = set_device(c)) return s;
   MatmulArgs a;
   a.q = w.q;
@@ -733,22 +785,24 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   // the m = 1 GEMV also quantizes to int8 blocks itself (act_i8)
   const bool plain_g1 = !dops.norm_gain && !dops.residual && !dops.swiglu;
   const G1Plan g1 = plain_g1 && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};
+  void* part = nullptr;
   if (g1.ok) {
     // the m = 1 GEMV uses no scratch
   } else if (mf.ok) {
     if (mf.ks > 1) {
-      if (int s = stream_split(c, a.stream, (size_t)mf.ks * (size_t)m * (size_t)w.out * 4, &a.part)) return s;
+      if (int s = call_scratch(c, fixed, a.stream, (size_t)mf.ks * (size_t)m * (size_t)w.out * 4, 1, &part))
+        return s;
     }
   } else if (plan.ok && plan.ksplit > 1) {
-    if (int s = stream_split(c, a.stream, plan.part_bytes, &a.part)) return s;
+    if (int s = call_scratch(c, fixed, a.stream, plan.part_bytes, 1, &part)) return s;
   } else if (!plan.ok && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
-    if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
+    if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
     if (gemm_sm_takes(w.format, m)) {
       a.slices = gemm_sm_slices(m, w.in, w.npad, c->cu_count);
       if (a.slices > 1) {
-        if (int s = stream_split(c, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, &a.part))
+        if (int s = call_scratch(c, fixed, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, 1, &part))
           return s;
       }
     }
@@ -756,9 +810,11 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     // fragment-major int8 activations with their scales and sums: 640 B per
     // 16-row tile and 32-block
     const size_t bytes = (size_t)((m + 15) / 16) * (size_t)(w.in / 32) * 640;
-    if (int s = stream_pack(c, a.stream, bytes, &a.scratch)) return s;
+    if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
   }
-  const auto ev = timing_pair(c, a.stream);
+  a.part = static_cast<float*>(part);
+  // no timing events for calls that allocate nothing (creating one allocates)
+  const auto ev = fixed ? std::pair<hipEvent_t, hipEvent_t>{nullptr, nullptr} : timing_pair(c, a.stream);
   a.ev_main[0] = ev.first;
   a.ev_main[1] = ev.second;
   hipError_t e = g1.ok                ? launch_gemv1(a, g1)
@@ -779,6 +835,32 @@ extern "C" {
 
 int rq_qmatmul(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m, void* stream) {
   return qmatmul_impl(h, wh, x, x_dtype, y, y_dtype, m, nullptr, stream);
+}
+
+int rq_qmatmul_noalloc(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
+                       void* stream) {
+  Ctx* c;
+  Weight w;
+  if (int s = lookup(h, wh, &c, &w)) return s;
+  if (kquant(w)) return fail(RQ_ERR_DTYPE, kKquantMsg);
+  if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
+  if (m == 0) return RQ_OK;
+  if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
+  if (!x || !y) return fail(RQ_ERR_NULL, "x or y is NULL");
+  if (x_dtype != RQ_F32 && x_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "x must be f32 or bf16");
+  if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
+  if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
+  if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  void* ptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    ptr = g_scratch_ptr[c->device];  // set when the context was created
+  }
+  if (!ptr) return fail(RQ_ERR_HIP, "no device address for the fixed scratch of this device");
+  FixedScratch fs = {static_cast<uint8_t*>(ptr), kNoAllocScratchBytes, 0};
+  const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
+  const DecodeOps dops = {nullptr, 0.0f, nullptr, 0, 0, nullptr, nullptr};
+  return run_matmul(c, w, plan, x, x_dtype, y, y_dtype, m, dops, (hipStream_t)stream, &fs);
 }
 
 int rq_qmatmul_fused(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
