@@ -1,42 +1,59 @@
 """Benchmark of librq's block-quantized matmul on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite headline|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite all|headline]
 
 Headline (the JSON `value`): the Q8 prefill GEMM of the second workload
-configuration, M=512 K=4096 N=11008, bf16 activations, bf16 output, f32
-accumulation, weights resident in HBM (`Q8 prefill GEMM, Llama-7B MLP up`).
-A step is one rq_qmatmul call over that batch; `value` is TFLOP/s
-(2*M*K*N flop per step) timed with HIP events on the stream the kernel runs on.
-Before the W warm-up steps the step runs untimed for RAMP_S seconds so that the
-timed steps see the GPU at its working clocks.
+configuration (C2), M=512 K=4096 N=11008, bf16 activations, bf16 output, f32
+accumulation, weights resident in HBM. A step is one rq_qmatmul call over that
+batch (activation packing + GEMM); `value` is TFLOP/s (2*M*K*N flop per step),
+timed with HIP events on the stream the kernels run on. Before the W warm-up
+steps the step runs untimed for RAMP_S seconds so that the timed steps see the
+GPU at its working clocks.
 
-Beside it, on the same JSON line:
-  gemv   - the M=1 Q8 decode GEMV (K=N=4096, f32 in/out) in GB/s of
-           algorithmic bytes (codes + scales + x + y). Timed over 100
-           back-to-back calls in one captured HIP graph, rotating through
-           enough weight copies (> 512 MB) that every call reads its weight
-           from HBM, not the 256 MB Infinity Cache ("cold"); warm = one copy.
-  decoder - the two-layer decode step (fourth workload configuration) in one
-           captured HIP graph: us per token step and tokens/s, for the fused
-           chain and for the unfused one (torch glue between the matmuls).
-  int8   - the int8-activation path: rq_quantize_act_i8 over 512 x 4096 f32
-           (GB/s), rq_qmatmul_i8 at the headline shape (TOP/s, activations
-           quantized once before timing) and at M = 1 (cold / warm GB/s).
-  sweep  - (--suite all) Q4 skinny M in {1,4,16} and the 70B-MLP shapes.
-  roofline      - the GEMM kernel against dense bf16 MFMA peak: 2*M*K*N flop
-                  per launch over the kernel's average duration, from the end
-                  of the activation-packing kernel to the end of the GEMM that
-                  follows it, which librq captures in HIP events on the call's
-                  stream (rq_ctx_set_kernel_timing) during the timed steps. A
-                  step also runs the packing kernel, so `value` is lower.
-  roofline_gemv - the decode kernel against HBM peak: algorithmic bytes per
-                  launch over its cold per-call time (the graph replays above:
-                  one kernel per call, launch gaps included).
-  traffic       - HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and
-                  WRITE_SIZE runs, committed under profiles/ (null if absent).
-  cpu_baseline  - the C restatement of Raster's qlinear-q8 loop
-                  (oracle/cpu_baseline.c) on a row sample of the same GEMM,
-                  all host threads; reported only.
+Beside it, on the same JSON line (default suite "all"; "headline" keeps C2,
+the C1 GEMV and the CPU baseline):
+  gemv          C1: the M=1 Q8 decode GEMV (K=N=4096, f32 in/out).
+  configs       every other workload configuration, one line per shape:
+                C3 (Q4, M = 1 / 4 / 16, K=4096 N=14336, f32) and C5 (Q4 and Q8,
+                K=8192 N=28672, bf16, M = 1 / 32 / 256).
+  decoder       C4: the two-layer decode step in one captured HIP graph.
+  read_ceiling  a plain streaming read (rq_stream_read) of the C1, C3 and C5
+                weight sizes, timed like the decode lines: the most any
+                kernel reading that many bytes per launch reaches here.
+  int8, kquant  the int8-activation path and the K-quant GEMV (next-step
+                rows of the path), as before.
+  roofline      the C2 GEMM kernel against dense bf16 MFMA peak (below).
+  roofline_gemv the C1 decode kernel against HBM peak (below).
+  cpu_baseline  Raster's CPU routes restated in C (oracle/cpu_baseline.c),
+                timed on this box's host cores: reported only (below).
+
+HBM-bound lines are measured "cold": the call rotates through enough weight
+copies (> 2x the 256 MB Infinity Cache per cycle) that every call reads its
+weight from HBM. Each gives
+  per_call_us   100 calls captured back to back in one HIP graph, median of 5
+                replays: launch gaps included (what a caller sees);
+  kernel_us     the kernels' own duration, from HIP events librq records at
+                the dispatch's start and end (rq_ctx_set_kernel_timing) over
+                the same rotation, 100 calls queued behind a GPU spin so they
+                run back to back: no launch gaps;
+  frac_hbm      algorithmic bytes / kernel_us / 8 TB/s (the roofline figure),
+  frac_hbm_per_call  the same over per_call_us,
+  frac_read_ceiling  read_ceiling time for the same bytes / kernel_us.
+MFMA-bound lines (M = 256, and the headline) give kernel_us and TFLOP/s.
+
+roofline: `achieved` = 46,170,898,432 flop per launch over the GEMM kernel's
+average duration, which librq captures in HIP events on the call's stream
+during the timed steps (from the end of the activation-packing kernel to the
+end of the GEMM that follows it). `traffic` is HBM bytes per launch from the
+rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summaries under profiles/.
+
+cpu_baseline: `value` is the qlinear-q8 loop (B1: f32 products, f64
+accumulation, the arithmetic of the GPU path's reference) on all usable host
+cores (at most 16, the box's share) over a row sample of C2, in TFLOP/s.
+`legs` times B1 and B2 (quantize-act-i8 + the x8 dpbusd GEMV, Raster's
+production int8 route; Q8 and Q4_0 tiles) at 1 thread (Raster's default
+RASTER_DECODE_THREADS) and at all cores, on the C1, C3 and C2 shapes, each
+leg about one second; `cpu_model` names the host CPU.
 
 Multi-GPU runs are not part of this build: --gpus above 1 exits with a message.
 """
@@ -60,6 +77,8 @@ INT8_PEAK_TOPS = 5000.0
 RAMP_S = 0.2  # seconds of untimed headline steps that bring an idle GPU to its working clocks
 MALL_BYTES = 256 << 20
 PROFILES = os.path.join(ROOT, "profiles")
+CALLS = 100  # launches per captured graph
+SPIN_CYCLES = 20_000_000  # GPU spin ahead of event-timed calls (~8 ms at 2.4 GHz), longer than their host launches
 
 
 def log(msg: str) -> None:
@@ -79,77 +98,92 @@ def q4_bytes(m, k, n, xb, yb):
     return int(n * k // 2 + n * (k // 32) * 2 + m * k * xb + m * n * yb)
 
 
-class Case:
-    """One resident-weight workload: `copies` weight copies rotated per call."""
+def copies_for_cold(nbytes):
+    return max(1, -(-2 * MALL_BYTES // nbytes))
 
-    def __init__(self, torch, ctx, fmt, m, k, n, xdt, ydt, copies=1, seed=0):
+
+class Weights:
+    """`copies` resident copies of one seeded weight (rotated per call)."""
+
+    def __init__(self, ctx, fmt, k, n, copies, seed=0):
         import numpy as np
 
         import raster_amd
         from raster_amd import workloads as wl
 
-        self.torch, self.m, self.k, self.n, self.fmt = torch, m, k, n, fmt
+        self.fmt, self.k, self.n = fmt, k, n
         if fmt == "q8":
             codes, scales = wl.q8_weights(n, k, seed=seed)
-            self.weights = [raster_amd.QWeight.q8(codes, scales, n, k, ctx) for _ in range(copies)]
-            self.bytes = q8_bytes(m, k, n, act_bytes(xdt), 4 if ydt == "f32" else 2)
+            self.ws = [raster_amd.QWeight.q8(codes, scales, n, k, ctx) for _ in range(copies)]
         else:
             packed, sc16 = wl.q4_weights(n, k, seed=seed)
-            self.weights = [raster_amd.QWeight.q4(packed, sc16.view(np.float16), n, k, ctx)
-                            for _ in range(copies)]
-            self.bytes = q4_bytes(m, k, n, act_bytes(xdt), 4 if ydt == "f32" else 2)
-        self.flops = 2.0 * m * k * n
-        x = torch.from_numpy(wl.activations(m, k, seed=seed + 1, dtype="f32" if xdt == "i8" else xdt)).cuda()
-        self.x = x.reshape(m, k).to(torch.bfloat16) if xdt == "bf16" else x.reshape(m, k)
-        self.xi8 = raster_amd.quantize_act_i8(ctx, x, k) if xdt == "i8" else None
-        ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
-        self.y = torch.empty((m, n), dtype=ydtype, device="cuda")
+            self.ws = [raster_amd.QWeight.q4(packed, sc16.view(np.float16), n, k, ctx) for _ in range(copies)]
+
+    def bytes(self, m, xdt, ydt):
+        f = q8_bytes if self.fmt == "q8" else q4_bytes
+        return f(m, self.k, self.n, act_bytes(xdt), 4 if ydt == "f32" else 2)
+
+    def destroy(self):
+        for w in self.ws:
+            w.destroy()
+        self.ws = []
+
+
+class Case:
+    """One matmul shape over a Weights set: step() calls the next copy."""
+
+    def __init__(self, torch, ctx, weights, m, xdt, ydt, seed=1):
+        import raster_amd
+        from raster_amd import workloads as wl
+
+        self.torch, self.w, self.m = torch, weights, m
+        self.bytes = weights.bytes(m, xdt, ydt)
+        self.flops = 2.0 * m * weights.k * weights.n
+        x = torch.from_numpy(wl.activations(m, weights.k, seed=seed, dtype="f32" if xdt == "i8" else xdt)).cuda()
+        self.x = x.reshape(m, weights.k).to(torch.bfloat16) if xdt == "bf16" else x.reshape(m, weights.k)
+        self.xi8 = raster_amd.quantize_act_i8(ctx, x, weights.k) if xdt == "i8" else None
+        self.y = torch.empty((m, weights.n), dtype=torch.bfloat16 if ydt == "bf16" else torch.float32, device="cuda")
         self.i = 0
 
     def step(self):
-        w = self.weights[self.i % len(self.weights)]
+        w = self.w.ws[self.i % len(self.w.ws)]
         self.i += 1
         if self.xi8 is not None:
             w.matmul_i8(*self.xi8, y=self.y)
         else:
             w.matmul(self.x, self.y)
 
-    def destroy(self):
-        for w in self.weights:
-            w.destroy()
-        self.weights = []
 
-
-def time_eager(torch, case, steps, warmup):
+def time_eager(torch, step, steps, warmup):
     """Event-timed back-to-back calls on the current stream; ms per call."""
     for _ in range(warmup):
-        case.step()
+        step()
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for _ in range(steps):
-        case.step()
+        step()
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
 
 
-def time_graph(torch, case, calls=100, reps=5):
+def time_graph(torch, step, calls=CALLS, reps=5):
     """`calls` launches captured in one HIP graph, replayed `reps` times after a
     warm replay; returns (median ms per call, coefficient of variation). The
-    warm-up runs on the capture stream itself, so per-stream scratch (the
-    prefill GEMM's packed activations) exists before capture begins."""
+    warm-up runs on the capture stream itself, so per-stream scratch exists
+    before capture begins."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for _ in range(3):
-            case.step()
+            step()
     s.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for _ in range(calls):
-            case.step()
+            step()
     g.replay()
     torch.cuda.synchronize()
     times = []
@@ -167,26 +201,132 @@ def time_graph(torch, case, calls=100, reps=5):
     return med, cv
 
 
-def copies_for_cold(nbytes):
-    return max(1, -(-2 * MALL_BYTES // nbytes))
+def time_kernels(torch, ctx, step, calls=CALLS, warmup=10):
+    """Average duration (ms) of the kernels of `calls` calls, from the dispatch
+    timestamps librq records (rq_ctx_set_kernel_timing). The calls are queued
+    behind a GPU spin of a few milliseconds so that they run back to back, as
+    in a graph, instead of each starting on an idle GPU after the host's
+    launch gap."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.kernel_time()
+    ctx.set_kernel_timing(True)
+    torch.cuda._sleep(SPIN_CYCLES)
+    for _ in range(calls):
+        step()
+    torch.cuda.synchronize()
+    total, n = ctx.kernel_time()
+    ctx.set_kernel_timing(False)
+    return total / max(n, 1)
 
 
-def hbm_line(torch, ctx, name, fmt, m, k, n, xdt, ydt):
-    """Cold (rotating copies) and warm GB/s for an HBM-bound shape."""
-    out = {"workload": name, "fmt": fmt, "m": m, "k": k, "n": n, "x": xdt, "y": ydt}
-    one = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=1)
-    wbytes = one.bytes
-    warm_ms, warm_cv = time_graph(torch, one)
-    one.destroy()
-    c = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=copies_for_cold(wbytes))
-    cold_ms, cold_cv = time_graph(torch, c)
-    out.update(copies=len(c.weights), bytes=wbytes, flop=c.flops)
-    c.destroy()
-    out.update(cold_us=round(cold_ms * 1e3, 3), cold_GBs=round(wbytes / cold_ms / 1e6, 1),
-               cold_cv=round(cold_cv, 4), cold_frac_hbm=round(wbytes / cold_ms / 1e6 / HBM_PEAK_GBS, 4),
-               warm_us=round(warm_ms * 1e3, 3), warm_GBs=round(wbytes / warm_ms / 1e6, 1),
+class ReadCeiling:
+    """rq_stream_read over rotating slices of one buffer larger than 2x the MALL."""
+
+    def __init__(self, torch, ctx):
+        import ctypes as C
+
+        from raster_amd import _lib
+
+        self.torch, self.ctx, self.C, self._lib = torch, ctx, C, _lib
+        self.buf = torch.empty(600 << 20, dtype=torch.uint8, device="cuda")
+        self.sink = torch.empty(ctx.device_info()["cu_count"] * 16 * 256, dtype=torch.int32, device="cuda")
+        self.cache = {}
+
+    def step_fn(self, nbytes, wg):
+        nb = (nbytes + 255) // 256 * 256
+        slots = max(1, self.buf.numel() // nb)
+        st = {"i": 0}
+
+        def step():
+            off = (st["i"] % slots) * nb
+            st["i"] += 1
+            self._lib.call("rq_stream_read", self.ctx.handle, self.C.c_void_p(self.buf.data_ptr() + off), nb, wg,
+                           self.C.c_void_p(self.sink.data_ptr()),
+                           self.C.c_void_p(self.torch.cuda.current_stream().cuda_stream))
+        return step
+
+    def us(self, nbytes):
+        """Best per-launch time (graph, launch gaps included) and kernel time
+        over 2 / 4 / 8 workgroups per CU."""
+        if nbytes not in self.cache:
+            best = None
+            for wg in (2, 4, 8):
+                ms, _ = time_graph(self.torch, self.step_fn(nbytes, wg))
+                kms = time_kernels(self.torch, self.ctx, self.step_fn(nbytes, wg))
+                if best is None or kms < best[1]:
+                    best = (ms, kms, wg)
+            self.cache[nbytes] = {"bytes": nbytes, "per_call_us": round(best[0] * 1e3, 3),
+                                  "kernel_us": round(best[1] * 1e3, 3),
+                                  "GBs": round(nbytes / best[1] / 1e6, 1),
+                                  "frac_hbm": round(nbytes / best[1] / 1e6 / HBM_PEAK_GBS, 4),
+                                  "wg_per_cu": best[2]}
+        return self.cache[nbytes]
+
+
+def hbm_line(torch, ctx, name, weights_cold, weights_warm, m, xdt, ydt, ceiling=None):
+    """Cold (rotating copies) and warm numbers for an HBM-bound shape."""
+    w = weights_cold
+    out = {"workload": name, "fmt": w.fmt, "m": m, "k": w.k, "n": w.n, "x": xdt, "y": ydt}
+    warm = Case(torch, ctx, weights_warm, m, xdt, ydt)
+    warm_ms, warm_cv = time_graph(torch, warm.step)
+    cold = Case(torch, ctx, w, m, xdt, ydt)
+    cold_ms, cold_cv = time_graph(torch, cold.step)
+    kern_ms = time_kernels(torch, ctx, cold.step)
+    b = cold.bytes
+    out.update(copies=len(w.ws), bytes=b, flop=cold.flops,
+               per_call_us=round(cold_ms * 1e3, 3), kernel_us=round(kern_ms * 1e3, 3),
+               GBs=round(b / kern_ms / 1e6, 1), frac_hbm=round(b / kern_ms / 1e6 / HBM_PEAK_GBS, 4),
+               frac_hbm_per_call=round(b / cold_ms / 1e6 / HBM_PEAK_GBS, 4), cold_cv=round(cold_cv, 4),
+               warm_per_call_us=round(warm_ms * 1e3, 3), warm_GBs=round(b / warm_ms / 1e6, 1),
                warm_cv=round(warm_cv, 4))
+    if ceiling is not None:
+        c = ceiling.us(b)
+        out["read_ceiling_kernel_us"] = c["kernel_us"]
+        out["frac_read_ceiling"] = round(c["kernel_us"] / 1e3 / kern_ms, 4)
     return out
+
+
+def mfma_line(torch, ctx, name, weights, m, xdt, ydt, steps=50, warmup=5):
+    c = Case(torch, ctx, weights, m, xdt, ydt)
+    ms = time_eager(torch, c.step, steps, warmup)
+    kms = time_kernels(torch, ctx, c.step, calls=steps)
+    tf = c.flops / kms / 1e9
+    return {"workload": name, "fmt": weights.fmt, "m": m, "k": weights.k, "n": weights.n, "x": xdt, "y": ydt,
+            "per_call_us": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3), "TFLOPs": round(tf, 2),
+            "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
+            "TFLOPs_per_call": round(c.flops / ms / 1e9, 2)}
+
+
+def config_lines(torch, ctx, ceiling):
+    """C3 and C5 at every M the workload definition names."""
+    lines = []
+    # C3: Q4_0, K=4096, N=14336, f32 in / out
+    one = Weights(ctx, "q4", 4096, 14336, 1, seed=3)
+    cold = Weights(ctx, "q4", 4096, 14336, copies_for_cold(one.bytes(1, "f32", "f32")), seed=3)
+    for m in (1, 4, 16):
+        ln = hbm_line(torch, ctx, "C3 Q4 decode skinny", cold, one, m, "f32", "f32", ceiling)
+        log(f"C3 m={m}: kernel {ln['kernel_us']} us ({ln['frac_hbm']:.3f} of HBM, "
+            f"{ln['frac_read_ceiling']:.3f} of the read ceiling), per call {ln['per_call_us']} us")
+        lines.append(ln)
+    cold.destroy()
+    one.destroy()
+    # C5: K=8192, N=28672, bf16 in / out, Q4_0 (fp16 scales) and Q8_0
+    for fmt in ("q4", "q8"):
+        one = Weights(ctx, fmt, 8192, 28672, 1, seed=5)
+        cold = Weights(ctx, fmt, 8192, 28672, copies_for_cold(one.bytes(1, "bf16", "bf16")), seed=5)
+        for m in (1, 32):
+            ln = hbm_line(torch, ctx, f"C5 70B MLP", cold, one, m, "bf16", "bf16", ceiling)
+            log(f"C5 {fmt} m={m}: kernel {ln['kernel_us']} us ({ln['frac_hbm']:.3f} of HBM), "
+                f"per call {ln['per_call_us']} us")
+            lines.append(ln)
+        cold.destroy()
+        ln = mfma_line(torch, ctx, "C5 70B MLP", one, 256, "bf16", "bf16")
+        log(f"C5 {fmt} m=256: kernel {ln['kernel_us']} us, {ln['TFLOPs']} TFLOP/s ({ln['frac_bf16_mfma']:.3f})")
+        lines.append(ln)
+        one.destroy()
+    return lines
 
 
 class QuantCase:
@@ -211,18 +351,24 @@ def int8_lines(torch, ctx):
     int8-MFMA GEMM at the headline shape (its activations quantized once,
     outside the timed region) and the int8 decode kernel at M = 1."""
     qc = QuantCase(torch, ctx, 512, 4096)
-    q_ms, _ = time_graph(torch, qc)
+    q_ms, _ = time_graph(torch, qc.step)
     lines = {"quantize_act_i8": {"m": 512, "k": 4096, "us": round(q_ms * 1e3, 3),
                                  "GBs": round(qc.bytes / q_ms / 1e6, 1)}}
-    c = Case(torch, ctx, "q8", 512, 4096, 11008, "i8", "bf16")
-    ms = time_eager(torch, c, 50, 5)
-    c.destroy()
-    lines["gemm_i8_q8_C2_shape"] = {"m": 512, "k": 4096, "n": 11008, "y": "bf16", "us": round(ms * 1e3, 3),
-                                    "TOPs": round(c.flops / ms / 1e9, 1),
-                                    "frac_int8_mfma": round(c.flops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
+    w = Weights(ctx, "q8", 4096, 11008, 1)
+    c = Case(torch, ctx, w, 512, "i8", "bf16")
+    kms = time_kernels(torch, ctx, c.step, calls=50)
+    w.destroy()
+    lines["gemm_i8_q8_C2_shape"] = {"m": 512, "k": 4096, "n": 11008, "y": "bf16", "kernel_us": round(kms * 1e3, 3),
+                                    "TOPs": round(c.flops / kms / 1e9, 1),
+                                    "frac_int8_mfma": round(c.flops / kms / 1e9 / INT8_PEAK_TOPS, 4)}
     for fmt, k, n in (("q8", 4096, 4096), ("q4", 4096, 14336)):
-        ln = hbm_line(torch, ctx, "int8 decode", fmt, 1, k, n, "i8", "f32")
-        lines[f"decode_i8_{fmt}_m1_{n}x{k}"] = {kk: ln[kk] for kk in ("cold_us", "cold_GBs", "warm_us", "warm_GBs")}
+        one = Weights(ctx, fmt, k, n, 1)
+        cold = Weights(ctx, fmt, k, n, copies_for_cold(one.bytes(1, "i8", "f32")))
+        ln = hbm_line(torch, ctx, "int8 decode", cold, one, 1, "i8", "f32")
+        cold.destroy()
+        one.destroy()
+        lines[f"decode_i8_{fmt}_m1_{n}x{k}"] = {kk: ln[kk] for kk in ("kernel_us", "frac_hbm", "per_call_us",
+                                                                      "warm_per_call_us")}
     return lines
 
 
@@ -259,47 +405,43 @@ class KquantCase:
 
 
 def kquant_lines(torch, ctx, m=1, k=4096, n=14336):
-    """The K-quant GEMV at the Q4 decode shape: cold / warm GB/s of weight bytes."""
+    """The K-quant GEMV at the Q4 decode shape: cold kernel time and GB/s of weight bytes."""
     lines = {}
     for fmt in ("q4k", "q6k"):
         one = KquantCase(torch, ctx, fmt, m, k, n)
         wb = one.bytes
-        warm_ms, _ = time_graph(torch, one)
+        warm_ms, _ = time_graph(torch, one.step)
         one.destroy()
         c = KquantCase(torch, ctx, fmt, m, k, n, copies=copies_for_cold(wb))
-        cold_ms, _ = time_graph(torch, c)
+        cold_ms, _ = time_graph(torch, c.step)
+        kms = time_kernels(torch, ctx, c.step)
         c.destroy()
-        lines[f"{fmt}_m{m}_{n}x{k}"] = {"weight_bytes": wb, "cold_us": round(cold_ms * 1e3, 3),
-                                          "cold_GBs": round(wb / cold_ms / 1e6, 1),
-                                          "warm_us": round(warm_ms * 1e3, 3), "warm_GBs": round(wb / warm_ms / 1e6, 1)}
+        lines[f"{fmt}_m{m}_{n}x{k}"] = {"weight_bytes": wb, "kernel_us": round(kms * 1e3, 3),
+                                          "frac_hbm": round(wb / kms / 1e6 / HBM_PEAK_GBS, 4),
+                                          "per_call_us": round(cold_ms * 1e3, 3),
+                                          "warm_per_call_us": round(warm_ms * 1e3, 3)}
     return lines
 
 
-def mfma_line(torch, ctx, name, fmt, m, k, n, xdt, ydt, steps=50, warmup=5):
-    c = Case(torch, ctx, fmt, m, k, n, xdt, ydt, copies=1)
-    ms = time_eager(torch, c, steps, warmup)
-    c.destroy()
-    tf = c.flops / ms / 1e9
-    return {"workload": name, "fmt": fmt, "m": m, "k": k, "n": n, "x": xdt, "y": ydt,
-            "us": round(ms * 1e3, 3), "TFLOPs": round(tf, 2), "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
-
-
-def decoder_step_us(torch, ctx, fused, replays=200):
+def decoder_step_us(torch, ctx, fused, sets=1, replays=200):
     """us per replay of the two-layer decode step captured in one HIP graph,
-    and the linears' weight bytes."""
+    and the linears' weight bytes per step. With sets > 1 the graph holds one
+    step per weight set (distinct copies of both layers) and the time is per
+    step, so consecutive steps read their weights from HBM, not the MALL."""
     from raster_amd import workloads as wl
     from raster_amd.decoder import DecoderLayer
 
     cfg = wl.DECODER
     layers, x = wl.decoder_weights(cfg, seed=0)
-    dl = [DecoderLayer(ctx, L["weights"], L["gain1"], L["gain2"], cfg["d"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"],
-                       cfg["ffn"], cfg["eps"], cfg["theta"], fused=fused) for L in layers]
+    stacks = [[DecoderLayer(ctx, L["weights"], L["gain1"], L["gain2"], cfg["d"], cfg["n_q"], cfg["n_kv"],
+                            cfg["head_dim"], cfg["ffn"], cfg["eps"], cfg["theta"], fused=fused) for L in layers]
+              for _ in range(sets)]
     kcs = [torch.from_numpy(L["kcache"]).cuda() for L in layers]
     vcs = [torch.from_numpy(L["vcache"]).cuda() for L in layers]
     xin = torch.from_numpy(x).cuda()
     pos = cfg["cached"]
 
-    def step():
+    def step(dl):
         h = xin
         for layer, kc, vc in zip(dl, kcs, vcs):
             h = layer.step(h, kc, vc, pos)
@@ -308,42 +450,50 @@ def decoder_step_us(torch, ctx, fused, replays=200):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        step()
+        step(stacks[0])
     s.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        step()
+        for dl in stacks:
+            step(dl)
     for _ in range(10):
         g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
+    reps = max(1, replays // sets)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(replays):
+    for _ in range(reps):
         g.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / replays * 1e3
-    wbytes = sum(layer.matmul_bytes() for layer in dl)
+    us = e0.elapsed_time(e1) / (reps * sets) * 1e3
+    wbytes = sum(layer.matmul_bytes() for layer in stacks[0])
     del g
-    for layer in dl:
-        layer.destroy()
+    for dl in stacks:
+        for layer in dl:
+            layer.destroy()
     return us, wbytes
 
 
 def decoder_line(torch, ctx):
     """The two-layer decode step (d 2048, 16 x 128 heads, SwiGLU 5632, Q8_0,
     128 cached positions, batch 1), captured in one HIP graph and replayed
-    back to back: us per step (one token), tokens/s and the GB/s of the
-    linears' weight bytes, for the fused chain (norms, SwiGLU and residuals in
-    the matmuls, one attention kernel) and for the unfused one (torch glue)."""
+    back to back: us per step (one token) and tokens/s, for the fused chain
+    (norms, SwiGLU and residuals in the matmuls, one attention kernel) warm
+    (one weight set, which fits the MALL) and cold (5 weight sets rotated,
+    580 MB), and for the unfused chain (torch glue) warm."""
     us, wbytes = decoder_step_us(torch, ctx, fused=True)
+    us_cold, _ = decoder_step_us(torch, ctx, fused=True, sets=5)
     us_unfused, _ = decoder_step_us(torch, ctx, fused=False)
-    return {"workload": "two-layer decode step, d 2048, 16x128 heads, SwiGLU 5632, Q8_0, 128 cached positions",
-            "us_per_step": round(us, 3), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wbytes,
-            "weight_GBs": round(wbytes / us / 1e3, 1), "frac_hbm": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "unfused_us_per_step": round(us_unfused, 3),
-            "note": "weights fit the 256 MB MALL, so replays read them warm; fused: 5 librq launches per layer"}
+    return {"workload": "C4 two-layer decode step, d 2048, 16x128 heads, SwiGLU 5632, Q8_0, 128 cached positions",
+            "us_per_step": round(us_cold, 3), "tokens_per_s": round(1e6 / us_cold, 1), "weight_bytes": wbytes,
+            "weight_GBs": round(wbytes / us_cold / 1e3, 1),
+            "frac_hbm": round(wbytes / us_cold / 1e3 / HBM_PEAK_GBS, 4),
+            "warm_us_per_step": round(us, 3), "warm_tokens_per_s": round(1e6 / us, 1),
+            "unfused_warm_us_per_step": round(us_unfused, 3),
+            "note": "us_per_step: 5 weight sets rotated in the graph (cold); warm: one set, MALL-resident; "
+                    "fused: 5 librq launches per layer"}
 
 
 COPY_ELEMS = 64 << 20  # f32 elements of the calibration copy: 256 MiB read + 256 MiB written
@@ -361,17 +511,19 @@ def traffic_run(torch, ctx, launches=5):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
-    head = Case(torch, ctx, "q8", 512, 4096, 11008, "bf16", "bf16")
+    w = Weights(ctx, "q8", 4096, 11008, 1)
+    head = Case(torch, ctx, w, 512, "bf16", "bf16")
     for _ in range(launches):
         head.step()
     torch.cuda.synchronize()
-    head.destroy()
+    w.destroy()
     one = q8_bytes(1, 4096, 4096, 4, 4)
-    dec = Case(torch, ctx, "q8", 1, 4096, 4096, "f32", "f32", copies=copies_for_cold(one))
-    for _ in range(len(dec.weights)):
+    dw = Weights(ctx, "q8", 4096, 4096, copies_for_cold(one))
+    dec = Case(torch, ctx, dw, 1, "f32", "f32")
+    for _ in range(len(dw.ws)):
         dec.step()
     torch.cuda.synchronize()
-    dec.destroy()
+    dw.destroy()
     log(f"traffic run: {launches} x neg({COPY_ELEMS} f32), {launches} x C2 GEMM step, "
         f"{copies_for_cold(one)} x C1 decode (cold rotation)")
 
@@ -390,9 +542,37 @@ def read_traffic(kernel_tag):
     return None
 
 
-def cpu_baseline(m, k, n, budget_s=10.0):
-    """Raster's qlinear-q8 loop restated in C (oracle/cpu_baseline.c), all host
-    threads, on a row sample of the GEMM; TFLOP/s scaled to the full shape."""
+def host_cores():
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(n, 16))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, budget_s):
+    """Calls fn() until about budget_s seconds have passed; (calls, seconds)."""
+    n, dt = 0, 0.0
+    while n == 0 or dt < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        dt += time.perf_counter() - t0
+        n += 1
+    return n, dt
+
+
+def cpu_baseline(leg_s=1.0, head_s=10.0):
+    """Raster's CPU routes (oracle/cpu_baseline.c) on this host; see the module
+    docstring. B1 runs a row sample of each shape sized to the budget, B2 one
+    activation row at a time as qlinear-i8! does (its M rows are M calls)."""
     import ctypes as C
 
     import numpy as np
@@ -401,29 +581,102 @@ def cpu_baseline(m, k, n, budget_s=10.0):
     from raster_amd import workloads as wl
 
     L = oracle.baseline_lib()
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
-    codes, scales = wl.q8_weights(n, k, seed=0)
-    x = wl.activations(m, k, seed=1, dtype="bf16")
+    cores = host_cores()
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
 
-    def run(rows):
-        y = np.empty(rows * n, np.float32)
+    def b1(m, k, n, threads, budget):
+        codes, scales = wl.q8_weights(n, k, seed=0)
+        x = wl.activations(m, k, seed=1)
+        y = np.empty(m * n, np.float32)
         t0 = time.perf_counter()
-        L.rqb_qlinear_q8(x.ctypes.data_as(C.c_void_p), codes.ctypes.data_as(C.c_void_p),
-                         scales.ctypes.data_as(C.c_void_p), rows, k, n, y.ctypes.data_as(C.c_void_p), threads)
-        return time.perf_counter() - t0
+        L.rqb_qlinear_q8(ptr(x), ptr(codes), ptr(scales), 1, k, n, ptr(y), threads)
+        t1 = time.perf_counter() - t0
+        rows = int(max(1, min(m, budget / max(t1, 1e-6) / 2)))
+        calls, dt = _timed(lambda: L.rqb_qlinear_q8(ptr(x), ptr(codes), ptr(scales), rows, k, n, ptr(y), threads),
+                           budget)
+        return calls * rows, dt
 
-    t1 = run(1)
-    rows = int(max(1, min(m, budget_s / max(t1, 1e-6))))
-    # whole passes over `rows` rows until about budget_s of wall time is spent
-    reps, dt = 0, 0.0
-    while reps == 0 or dt < budget_s:
-        dt += run(rows)
-        reps += 1
-    flop = 2.0 * rows * k * n * reps
-    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"qlinear-q8 loop (f32 products, f64 accumulation), {reps} pass(es) over {rows} of {m} "
-                      f"activation rows x K={k} x N={n}, {dt:.2f} s, {threads} threads"}
+    def b2(fmt, m, k, n, threads, budget):
+        rng = np.random.default_rng(0)
+        nb = k // 32
+        if fmt == "q8":
+            wqi = rng.integers(0, 256, size=(n // 8) * nb * 256, dtype=np.uint8)
+            fn = L.rqb_qmatmul_q8_x8
+        else:
+            wqi = rng.integers(0, 256, size=(n // 8) * nb * 128, dtype=np.uint8)
+            fn = L.rqb_qmatmul_q4_x8
+        wsi = rng.uniform(0.002, 0.02, (n // 8) * nb * 8).astype(np.float32)
+        x = wl.activations(1, k, seed=1)
+        xq, xs, xsum = np.empty(k, np.int8), np.empty(nb, np.float32), np.empty(nb, np.int32)
+        y = np.empty(n, np.float32)
+
+        def one():
+            L.rqb_quantize_act_i8(ptr(x), 1, k, ptr(xq), ptr(xs), ptr(xsum), threads)
+            fn(ptr(xq), ptr(xs), ptr(xsum), ptr(wqi), ptr(wsi), ptr(y), k, n, threads)
+        one()
+        return _timed(one, budget)
+
+    legs = []
+    shapes = [("C1", "q8", 1, 4096, 4096), ("C3", "q4", 1, 4096, 14336), ("C3", "q4", 4, 4096, 14336),
+              ("C3", "q4", 16, 4096, 14336), ("C2", "q8", 512, 4096, 11008)]
+    for cfg, fmt, m, k, n in shapes:
+        for threads in (1, cores):
+            if fmt == "q8":
+                rows, dt = b1(m, k, n, threads, leg_s)
+                legs.append({"config": cfg, "route": "B1 qlinear-q8 loop", "fmt": "q8_0", "m": m, "k": k, "n": n,
+                             "threads": threads, "rows_timed": rows, "seconds": round(dt, 3),
+                             "us_per_row": round(dt / rows * 1e6, 2),
+                             "GFLOPs": round(2.0 * rows * k * n / dt / 1e9, 2)})
+            calls, dt = b2(fmt, m, k, n, threads, leg_s)
+            wb = n * k + n * (k // 32) * 4 if fmt == "q8" else n * k // 2 + n * (k // 32) * 4
+            legs.append({"config": cfg, "route": f"B2 quantize-act-i8 + x8 dpbusd GEMV ({fmt})", "m": m, "k": k,
+                         "n": n, "threads": threads, "rows_timed": calls, "seconds": round(dt, 3),
+                         "us_per_row": round(dt / calls * 1e6, 2), "us_per_call_of_m_rows": round(dt / calls * m * 1e6, 2),
+                         "GFLOPs": round(2.0 * calls * k * n / dt / 1e9, 2),
+                         "weight_GBs": round(wb * calls / dt / 1e9, 2)})
+    # the headline value: B1 on all cores over a row sample of C2, ~head_s seconds
+    M, K, N = 512, 4096, 11008
+    rows, dt = b1(M, K, N, cores, head_s)
+    L.rqb_pool_shutdown()
+    flop = 2.0 * rows * K * N
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"B1 qlinear-q8 loop (f32 products, f64 accumulation) over {rows} activation rows of the C2 "
+                      f"GEMM (K={K}, N={N}) in {dt:.2f} s on {cores} threads; TFLOP/s of that sample",
+            "cpu_model": cpu_model(), "vnni": bool(L.rqb_have_vnni()), "legs": legs}
+
+
+def headline(torch, ctx, args):
+    """The C2 GEMM: ramp, W warm-up steps, K timed steps."""
+    M, K, N = 512, 4096, 11008
+    log(f"headline gemm q8 m={M} k={K} n={N} steps={args.steps} warmup={args.warmup}")
+    w = Weights(ctx, "q8", K, N, 1)
+    head = Case(torch, ctx, w, M, "bf16", "bf16")
+    # An idle GPU ramps its clocks over the first milliseconds of work: before
+    # the W counted warm-up steps the step runs untimed for RAMP_S seconds;
+    # the timed region is unchanged.
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < RAMP_S:
+        for _ in range(20):
+            head.step()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        head.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ctx.kernel_time()
+    ctx.set_kernel_timing(True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        head.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kern_total, kern_n = ctx.kernel_time()
+    ctx.set_kernel_timing(False)
+    ms = e0.elapsed_time(e1) / args.steps
+    kern_ms = kern_total / max(kern_n, 1)
+    w.destroy()
+    return head.flops, ms, kern_ms, kern_n
 
 
 def main():
@@ -431,11 +684,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--suite", choices=["headline", "all"], default="headline")
+    ap.add_argument("--suite", choices=["headline", "all"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
     ap.add_argument("--only-decode", action="store_true",
-                    help="time the decode shapes only (C1 GEMV, Q4 skinny, 70B M=1, decoder step) for profiling")
+                    help="the decode shapes only (C1, C3, C5 at M = 1 and 32, the decoder step) for profiling")
     ap.add_argument("--traffic-run", action="store_true",
                     help="a short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: a copy kernel of "
                          "known size (calibration), then the headline GEMM and the cold C1 decode kernel")
@@ -460,66 +713,28 @@ def main():
     peak_props = info["cu_count"] * 4 * 1024 * clock_ghz / 1e3
     log(f"device: {torch.cuda.get_device_name(0)} cu={info['cu_count']} clock={clock_ghz:.3f} GHz")
 
-    if args.only_decode:
-        lines = [hbm_line(torch, ctx, "Q8 decode GEMV", "q8", 1, 4096, 4096, "f32", "f32")]
-        for m in (1, 4, 16):
-            lines.append(hbm_line(torch, ctx, "Q4 decode skinny", "q4", m, 4096, 14336, "f32", "f32"))
-        for fmt in ("q8", "q4"):
-            lines.append(hbm_line(torch, ctx, "70B MLP", fmt, 1, 8192, 28672, "bf16", "bf16"))
-        for ln in lines:
-            log(f"{ln['workload']} {ln['fmt']} m={ln['m']}: cold {ln['cold_us']} us {ln['cold_GBs']} GB/s, "
-                f"warm {ln['warm_us']} us {ln['warm_GBs']} GB/s")
-        dec = decoder_line(torch, ctx)
-        log(f"decoder: {dec['us_per_step']} us/step fused, {dec['unfused_us_per_step']} us/step unfused")
-        ctx.close()
-        print(json.dumps({"decode": lines, "decoder": dec}), flush=True)
-        return
-
     if args.traffic_run:
         traffic_run(torch, ctx)
         ctx.close()
         return
 
-    # ---- headline: Q8 GEMM M=512 K=4096 N=11008, bf16 in / bf16 out
-    M, K, N = 512, 4096, 11008
-    log(f"headline gemm q8 m={M} k={K} n={N} steps={args.steps} warmup={args.warmup}")
-    head = Case(torch, ctx, "q8", M, K, N, "bf16", "bf16")
-    # An idle GPU ramps its clocks over the first milliseconds of work: with
-    # 10 warm-up steps the GEMM measured 64-68 us, with 300-1000 56-58 us. So
-    # before the W counted warm-up steps the step runs untimed for at least
-    # RAMP_S seconds; the timed region is unchanged.
-    t_ramp = time.perf_counter()
-    while time.perf_counter() - t_ramp < RAMP_S:
-        for _ in range(20):
-            head.step()
-        torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        head.step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ctx.kernel_time()
-    # librq captures the GEMM dispatch's own start/end timestamps in HIP
-    # events on the call's stream (torch's current stream here), which
-    # separates the kernel from the activation-packing pass for the roofline
-    ctx.set_kernel_timing(True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        head.step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_total, kern_n = ctx.kernel_time()
-    ctx.set_kernel_timing(False)
-    ms = e0.elapsed_time(e1) / args.steps
-    kern_ms = kern_total / max(kern_n, 1)
-    head.destroy()
-    tflops = head.flops / ms / 1e9
-    kern_tflops = head.flops / kern_ms / 1e9
-    log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s (wall {wall:.3f} s); "
-        f"GEMM kernel {kern_ms * 1e3:.2f} us avg over {kern_n} launches, {kern_tflops:.1f} TFLOP/s")
+    if args.only_decode:
+        ceiling = ReadCeiling(torch, ctx)
+        one = Weights(ctx, "q8", 4096, 4096, 1)
+        cold = Weights(ctx, "q8", 4096, 4096, copies_for_cold(one.bytes(1, "f32", "f32")))
+        lines = [hbm_line(torch, ctx, "C1 Q8 decode GEMV", cold, one, 1, "f32", "f32", ceiling)]
+        cold.destroy()
+        one.destroy()
+        lines += [ln for ln in config_lines(torch, ctx, ceiling) if ln["m"] <= 32]
+        dec = decoder_line(torch, ctx)
+        ctx.close()
+        print(json.dumps({"decode": lines, "decoder": dec}), flush=True)
+        return
 
+    flops, ms, kern_ms, kern_n = headline(torch, ctx, args)
+    tflops, kern_tflops = flops / ms / 1e9, flops / kern_ms / 1e9
+    log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s; "
+        f"GEMM kernel {kern_ms * 1e3:.2f} us avg over {kern_n} launches, {kern_tflops:.1f} TFLOP/s")
     result = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -535,63 +750,53 @@ def main():
         "data": "synthetic (seeded: int8 codes U{-127..127}, f32 scales U(0.002,0.02), x N(0,1) rounded to bf16)",
         "config": {"workload": "Q8 prefill GEMM, Llama-7B MLP up-projection: M=512 K=4096 N=11008, "
                                "bf16 activations, f32 accumulation, bf16 output",
-                   "m": M, "k": K, "n": N, "weights": "q8_0 resident in HBM"},
+                   "m": 512, "k": 4096, "n": 11008, "weights": "q8_0 resident in HBM"},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": read_traffic("gemm_bf16_q8_C2"),
                      "peak_from_device_props": round(peak_props, 1),
-                     "kernel": "rq::gemm_wl_kernel<0, float, 2, 6, 4, 2, 8>", "flop_per_launch": head.flops,
+                     "kernel": "rq::gemm_wl_kernel", "flop_per_launch": flops,
                      "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
 
     if not args.only_gemm:
-        # ---- decode GEMV: Q8 M=1 K=N=4096, f32 in / f32 out
-        log("gemv q8 m=1 k=4096 n=4096 (cold rotation + warm)")
-        gv = hbm_line(torch, ctx, "Q8 decode GEMV", "q8", 1, 4096, 4096, "f32", "f32")
+        ceiling = ReadCeiling(torch, ctx)
+        log("C1 gemv q8 m=1 k=4096 n=4096 (cold rotation + warm)")
+        one = Weights(ctx, "q8", 4096, 4096, 1)
+        cold = Weights(ctx, "q8", 4096, 4096, copies_for_cold(one.bytes(1, "f32", "f32")))
+        gv = hbm_line(torch, ctx, "C1 Q8 decode GEMV", cold, one, 1, "f32", "f32", ceiling)
+        cold.destroy()
+        one.destroy()
         result["gemv"] = gv
-        # a decode step is this one kernel: its average duration is the cold
-        # graph's time per call (100 launches back to back, HIP events around
-        # each replay on the replaying stream; the ~0.7 us gaps between
-        # launches are included, so the rate is a lower bound)
-        result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["cold_GBs"], "peak": HBM_PEAK_GBS,
-                                   "unit": "GB/s", "frac": gv["cold_frac_hbm"],
-                                   "traffic": read_traffic("skinny_q8_f32_C1"),
-                                   "kernel": "rq::skinny_kernel<0, float, 0, 4, 8, 4, 2>",
-                                   "bytes_per_launch": gv["bytes"], "kernel_avg_us": gv["cold_us"]}
-        log(f"gemv: cold {gv['cold_us']} us {gv['cold_GBs']} GB/s; warm {gv['warm_us']} us {gv['warm_GBs']} GB/s")
-
-    if not args.only_gemm:
-        log("two-layer decode step")
-        result["decoder"] = decoder_line(torch, ctx)
-        log(f"decoder: {result['decoder']['us_per_step']} us/step fused, {result['decoder']['tokens_per_s']} tokens/s;"
-            f" {result['decoder']['unfused_us_per_step']} us/step unfused")
-        log("int8-activation path")
-        result["int8"] = i8 = int8_lines(torch, ctx)
-        log("K-quant GEMV")
-        result["kquant"] = kq = kquant_lines(torch, ctx)
-        log("kquant: " + "; ".join(f"{k} cold {v['cold_us']} us {v['cold_GBs']} GB/s" for k, v in kq.items()))
-        log(f"int8: quantize {i8['quantize_act_i8']['us']} us {i8['quantize_act_i8']['GBs']} GB/s; "
-            f"gemm {i8['gemm_i8_q8_C2_shape']['us']} us {i8['gemm_i8_q8_C2_shape']['TOPs']} TOP/s; "
-            f"decode q8 cold {i8['decode_i8_q8_m1_4096x4096']['cold_us']} us, "
-            f"q4 cold {i8['decode_i8_q4_m1_14336x4096']['cold_us']} us")
+        result["roofline_gemv"] = {"bound": "hbm", "achieved": gv["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": gv["frac_hbm"], "traffic": read_traffic("skinny_q8_f32_C1"),
+                                   "kernel": "rq::skinny_kernel", "bytes_per_launch": gv["bytes"],
+                                   "kernel_avg_us": gv["kernel_us"], "per_call_us": gv["per_call_us"],
+                                   "frac_per_call": gv["frac_hbm_per_call"],
+                                   "read_ceiling_kernel_us": gv["read_ceiling_kernel_us"],
+                                   "frac_read_ceiling": gv["frac_read_ceiling"]}
+        log(f"C1: kernel {gv['kernel_us']} us = {gv['GBs']} GB/s ({gv['frac_hbm']:.3f} of HBM, "
+            f"{gv['frac_read_ceiling']:.3f} of the read ceiling); per call {gv['per_call_us']} us")
 
     if args.suite == "all" and not args.only_gemm:
-        sweep = []
-        for m in (1, 4, 16):
-            log(f"q4 skinny m={m}")
-            sweep.append(hbm_line(torch, ctx, "Q4 decode skinny", "q4", m, 4096, 14336, "f32", "f32"))
-        for fmt in ("q8", "q4"):
-            for m in (1, 32):
-                log(f"70B MLP {fmt} m={m}")
-                sweep.append(hbm_line(torch, ctx, "70B MLP", fmt, m, 8192, 28672, "bf16", "bf16"))
-            log(f"70B MLP {fmt} m=256")
-            sweep.append(mfma_line(torch, ctx, "70B MLP", fmt, 256, 8192, 28672, "bf16", "bf16"))
-        result["sweep"] = sweep
+        result["configs"] = config_lines(torch, ctx, ceiling)
+        log("C4 two-layer decode step")
+        result["decoder"] = dec = decoder_line(torch, ctx)
+        log(f"C4: {dec['us_per_step']} us/step cold, {dec['warm_us_per_step']} warm, "
+            f"{dec['unfused_warm_us_per_step']} unfused warm")
+        result["read_ceiling"] = sorted(ceiling.cache.values(), key=lambda d: d["bytes"])
+        log("int8-activation path")
+        result["int8"] = int8_lines(torch, ctx)
+        log("K-quant GEMV")
+        result["kquant"] = kquant_lines(torch, ctx)
+    elif not args.only_gemm:
+        result["read_ceiling"] = sorted(ceiling.cache.values(), key=lambda d: d["bytes"])
 
     if not args.no_cpu and not args.only_gemm:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(M, K, N)
-        log(f"cpu baseline: {result['cpu_baseline']['value']} TFLOP/s")
+        result["cpu_baseline"] = cpu_baseline()
+        log(f"cpu baseline: {result['cpu_baseline']['value']} TFLOP/s on {result['cpu_baseline']['cores']} cores "
+            f"({result['cpu_baseline']['cpu_model']})")
     else:
         result["cpu_baseline"] = None
     ctx.close()

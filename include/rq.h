@@ -90,6 +90,14 @@ int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz
 int rq_ctx_set_kernel_timing(rq_ctx ctx, int enable);
 int rq_ctx_kernel_time(rq_ctx ctx, double* total_ms, int64_t* launches);
 
+/* A plain streaming read of `bytes` (a multiple of 16) from device memory at
+ * src (16-byte aligned), by cu_count * wg_per_cu workgroups (1..16 per CU) of
+ * 256 threads with 16-byte loads; sink (device, cu_count * wg_per_cu * 256
+ * words) is written only by chance. No counterpart in the reference: it
+ * measures the HBM read ceiling the HBM-bound kernels are compared with.
+ * Timed like a matmul while kernel timing is enabled. */
+int rq_stream_read(rq_ctx ctx, const void* src, size_t bytes, int wg_per_cu, uint32_t* sink, void* stream);
+
 /* ---- device memory and streams (raster/gpu/ze_runtime.clj:765-787 DeviceBuffer) */
 int rq_buf_alloc(rq_ctx ctx, size_t bytes, void** dptr);
 int rq_buf_free(rq_ctx ctx, void* dptr);

@@ -53,7 +53,9 @@ def baseline_lib():
         _blib.rqb_qlinear_q8.argtypes = [p, p, p, i64, i64, i64, p, i32]
         _blib.rqb_quantize_act_i8.argtypes = [p, i64, i64, p, p, p, i32]
         _blib.rqb_qmatmul_q8_x8.argtypes = [p, p, p, p, p, p, i64, i64, i32]
+        _blib.rqb_qmatmul_q4_x8.argtypes = [p, p, p, p, p, p, i64, i64, i32]
         _blib.rqb_have_vnni.restype = C.c_int
+        _blib.rqb_pool_shutdown.argtypes = []
     return _blib
 
 

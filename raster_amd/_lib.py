@@ -60,6 +60,7 @@ SIGNATURES = {
     "rq_qlinear_i8": ([_p, _p, _p, _p, _i, _p, _i64, _i64], _i),
     "rq_q4k_of": ([_p, _p, _i64, _i64, _p, _p, _p, _p, _p, C.POINTER(_i64), _p], _i),
     "rq_quantize_weight_q6k": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
+    "rq_stream_read": ([_p, _p, _sz, _i, _p, _p], _i),
 }
 
 

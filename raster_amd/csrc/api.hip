@@ -1115,6 +1115,23 @@ int rq_qlinear_i8(rq_ctx h, const float* x, const uint8_t* wqi, const float* wsi
   return s;
 }
 
+int rq_stream_read(rq_ctx h, const void* src, size_t bytes, int wg_per_cu, uint32_t* sink, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (!src || !sink) return fail(RQ_ERR_NULL, "src or sink is NULL");
+  if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)src & 15) != 0)
+    return fail(RQ_ERR_SHAPE, "bytes must be a positive multiple of 16 and src 16-byte aligned");
+  if (wg_per_cu < 1 || wg_per_cu > 16) return fail(RQ_ERR_SHAPE, "wg_per_cu must be 1 .. 16");
+  if (int s = set_device(c)) return s;
+  const auto ev = timing_pair(c, (hipStream_t)stream);
+  if (ev.first) (void)hipEventRecord(ev.first, (hipStream_t)stream);
+  hipError_t e = launch_stream_read(src, bytes, c->cu_count * wg_per_cu, sink, (hipStream_t)stream);
+  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, (hipStream_t)stream);
+  timing_done(c, ev, e == hipSuccess);
+  if (e != hipSuccess) return hip_fail(e, "stream read launch");
+  return RQ_OK;
+}
+
 int rq_qlinear_q8_dx(rq_ctx h, const float* dy, const int8_t* codes, const float* scales, int64_t m, int64_t in,
                      int64_t out, float* dx) {
   Ctx* c = reinterpret_cast<Ctx*>(h);

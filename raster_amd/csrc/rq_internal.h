@@ -186,6 +186,10 @@ hipError_t launch_q4k_encode(const float* W, int64_t out, int64_t in, int64_t in
                              uint8_t* aq, int8_t* bq, hipStream_t stream);
 hipError_t launch_q6k_encode(const float* W, int64_t out, int64_t in, uint8_t* wq, int8_t* sc, float* ds,
                              hipStream_t stream);
+// Streaming read of `bytes` (a multiple of 16) for the read-ceiling
+// measurement (stream.hip): `grid` workgroups of 256 threads; sink holds
+// grid * 256 words.
+hipError_t launch_stream_read(const void* src, size_t bytes, int grid, uint32_t* sink, hipStream_t stream);
 // Row-major (Raster's layout) -> chunked, for codes and scales (layout.hip).
 hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm, const void* s_rm, int64_t out,
                                int64_t in, int64_t npad, uint8_t* q, void* s, void* s_rb, hipStream_t stream);

@@ -678,3 +678,46 @@ def test_q4k_of_pads_rows_with_zeros(orc):
     x[:in_] = orc.jfill_uniform_centered(14, in_)
     xq, xs, bs = orc.quantize_act_q8k(x, 1, inp, 32)
     assert np.all(xq[in_:] == 0) and np.all(bs[in_ // 32:] == 0)
+
+
+# ---------------------------------------------------------------- the timed CPU baseline
+@pytest.mark.parametrize("nibble", [True, False])
+def test_cpu_baseline_x8_matches_the_oracle(orc, nibble):
+    # the B2 route bench.py times (oracle/cpu_baseline.c) computes the oracle's
+    # quantize-act-i8 + qmatmul-q4-x8! / qmatmul-q8-x8! (f32 lanes summed in
+    # another association, so to 1e-5), on 1 and 4 threads
+    import ctypes as C
+
+    L = orc.baseline_lib()
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    rng = np.random.default_rng(90 + nibble)
+    out, in_ = 64, 512
+    W = rng.standard_normal(out * in_).astype(np.float32)
+    x = rng.standard_normal(in_).astype(np.float32)
+    wq, ws = orc.quantize_weight_q4(W) if nibble else orc.quantize_weight_q8u(W)
+    wqi, wsi = orc.repack_x8(wq, ws, out, in_, nibble)
+    rxq, rxs, rxsum = orc.quantize_act_i8(x, 1, in_)
+    ref = orc.qmatmul_x8(rxq, rxs, rxsum, wqi, wsi, in_, out, nibble)
+    for threads in (1, 4):
+        xq, xs, xsum = np.empty(in_, np.int8), np.empty(in_ // 32, np.float32), np.empty(in_ // 32, np.int32)
+        L.rqb_quantize_act_i8(ptr(x), 1, in_, ptr(xq), ptr(xs), ptr(xsum), threads)
+        assert np.array_equal(xq, rxq) and np.array_equal(xs, rxs) and np.array_equal(xsum, rxsum)
+        y = np.empty(out, np.float32)
+        fn = L.rqb_qmatmul_q4_x8 if nibble else L.rqb_qmatmul_q8_x8
+        fn(ptr(xq), ptr(xs), ptr(xsum), ptr(wqi), ptr(wsi), ptr(y), in_, out, threads)
+        assert orc.normwise_relerr(y, ref) < 1e-5
+
+
+def test_cpu_baseline_qlinear_matches_the_oracle(orc):
+    import ctypes as C
+
+    L = orc.baseline_lib()
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+    rng = np.random.default_rng(92)
+    m, out, in_ = 3, 40, 256
+    codes = rng.integers(-127, 128, out * in_, dtype=np.int8)
+    scales = rng.uniform(0.002, 0.02, out * in_ // 32).astype(np.float32)
+    x = rng.standard_normal(m * in_).astype(np.float32)
+    y = np.empty(m * out, np.float32)
+    L.rqb_qlinear_q8(ptr(x), ptr(codes), ptr(scales), m, in_, out, ptr(y), 4)
+    assert orc.normwise_relerr(y, orc.qlinear_q8(x, codes, scales, m, in_, out)) < 1e-6
