@@ -46,6 +46,9 @@ average duration, which librq captures in HIP events on the call's stream
 during the timed steps (from the end of the activation-packing kernel to the
 end of the GEMM that follows it). `traffic` is HBM bytes per launch from the
 rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summaries under profiles/.
+`dense_bf16_library` times the vendor library's dense bf16 GEMM (torch.matmul,
+hipBLASLt) at the same shape with an unquantized bf16 weight: what the
+library reaches on this shape without any dequantization, for comparison.
 
 cpu_baseline: `value` is the qlinear-q8 loop (B1: f32 products, f64
 accumulation, the arithmetic of the GPU path's reference) on all usable host
@@ -344,6 +347,30 @@ class QuantCase:
 
     def step(self):
         self.raster_amd.quantize_act_i8(self.ctx, self.x, self.k, out=self.out)
+
+
+def dense_library_line(torch, M=512, K=4096, N=11008, warmup=200, calls=500):
+    """A reference point for the headline GEMM's MFMA fraction: the vendor
+    library's dense bf16 GEMM (torch.matmul -> hipBLASLt) at the same shape,
+    y = x @ W^T with W a dense bf16 [N, K] tensor (no quantization, no
+    dequantization), timed back to back with events on torch's stream."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=g)
+    w = torch.randn(N, K, device="cuda", dtype=torch.bfloat16, generator=g)
+    for _ in range(warmup):
+        torch.matmul(x, w.t())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(calls):
+        torch.matmul(x, w.t())
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / calls * 1e3
+    tflops = 2.0 * M * K * N / us / 1e6
+    return {"what": f"torch.matmul bf16 x[{M},{K}] @ W[{N},{K}]^T (hipBLASLt), dense bf16 weight",
+            "us_per_call": round(us, 3), "tflops": round(tflops, 3),
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
 
 def int8_lines(torch, ctx):
@@ -760,6 +787,8 @@ def main():
     }
 
     if not args.only_gemm:
+        result["roofline"]["dense_bf16_library"] = lib = dense_library_line(torch)
+        log(f"dense bf16 library GEMM at the C2 shape: {lib['us_per_call']} us, {lib['tflops']} TFLOP/s")
         ceiling = ReadCeiling(torch, ctx)
         log("C1 gemv q8 m=1 k=4096 n=4096 (cold rotation + warm)")
         one = Weights(ctx, "q8", 4096, 4096, 1)

@@ -301,7 +301,14 @@ int rq_qmatmul_i8(rq_ctx ctx, rq_weight w, const int8_t* xq, const float* xs, co
  * query over rows 0..pos with the given scale: out f32[n_q*head_dim]. Query
  * head h reads KV head h / (n_q/n_kv). head_dim a multiple of 4 up to 512:
  * any cache length; other even head_dim: pos + 1 <= about 40K positions
- * (the scores sit in one workgroup's LDS). */
+ * (the scores sit in one workgroup's LDS). With head_dim a multiple of 4 and
+ * pos >= 32 the cached rows are split over several workgroups per head, whose
+ * partial softmax states are merged in a fixed order (results do not depend
+ * on scheduling); that uses per-stream scratch of the context, allocated by
+ * the first such call on the stream and grown by larger ones (as for the bf16
+ * GEMM: a call being captured into a graph that would need to grow it fails
+ * with RQ_ERR_SHAPE, so run it once on the stream before capturing). Calls
+ * on one stream run in order; calls on different streams do not share it. */
 int rq_decode_attention(rq_ctx ctx, const float* q, const float* k, const float* v, float* kcache, float* vcache,
                         int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale,
                         float* out, void* stream);

@@ -41,6 +41,8 @@ struct Ctx {
     size_t pack_bytes = 0;
     void* red = nullptr;  // K-split partial sums
     size_t red_bytes = 0;
+    void* attn = nullptr;  // split attention: the ranges' softmax records
+    size_t attn_bytes = 0;
   };
   std::unordered_map<hipStream_t, StreamScratch> scratch;
   // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
@@ -224,6 +226,18 @@ static int stream_split(Ctx* c, hipStream_t stream, size_t part_bytes, float** p
   return RQ_OK;
 }
 
+// The split attention's range records for `stream`: `bytes` (grow-only).
+static int stream_attn(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto& e = c->scratch[stream];
+  if (e.attn_bytes < bytes) {
+    if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
+    if (int s = regrow(stream, bytes, &e.attn, &e.attn_bytes)) return s;
+  }
+  *out = e.attn;
+  return RQ_OK;
+}
+
 // An event pair for timing the main kernel of one call on `stream`, or
 // {nullptr, nullptr} when timing is off or the stream is being captured.
 static std::pair<hipEvent_t, hipEvent_t> timing_pair(Ctx* c, hipStream_t stream) {
@@ -348,6 +362,7 @@ int rq_ctx_destroy(rq_ctx h) {
   for (auto& kv : c->scratch) {
     (void)hipFree(kv.second.pack);
     (void)hipFree(kv.second.red);
+    (void)hipFree(kv.second.attn);
   }
   timing_release(c);
   c->magic = 0;
@@ -967,8 +982,12 @@ int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v
                               "or above 512: about 40K positions)");
   if (!(theta > 0.0)) return fail(RQ_ERR_SHAPE, "theta must be positive");
   if (int s = set_device(c)) return s;
-  hipError_t e = launch_decode_attention(q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out,
-                                         (hipStream_t)stream);
+  const AttnSplit sp = plan_decode_attention(pos, n_q, head_dim, c->cu_count);
+  void* scratch_buf = nullptr;
+  if (sp.nsplit > 1)
+    if (int s = stream_attn(c, (hipStream_t)stream, sp.scratch_bytes, &scratch_buf)) return s;
+  hipError_t e = launch_decode_attention(q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp,
+                                         scratch_buf, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "attention launch");
   return RQ_OK;
 }

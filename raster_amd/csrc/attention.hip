@@ -22,9 +22,15 @@
 //     its own running maximum, sum and weighted values (the usual online
 //     softmax); the four waves' states are combined at the end. Memory
 //     latency is paid about once per two chunks instead of once per row.
+//     A short cache on few heads would leave most CUs idle, so the cached
+//     rows are split into nsplit contiguous ranges, one workgroup per (head,
+//     range): each writes its range's softmax state (running maximum, sum of
+//     exponentials, weighted values) to a scratch record, and a second
+//     kernel merges each head's records in range order.
 //   generic kernel (any even head_dim): a wave per position for the scores,
 //     a thread per dimension for the values; the scores sit in LDS, so the
 //     cache length is bounded by it.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 
@@ -137,12 +143,17 @@ constexpr int kMaxDims = 512;
 
 // TPR lanes per row, NV 4-dimension vectors per lane (dimension
 // 4 (lane % TPR) + 4 TPR v), NP rows per lane per chunk
-template <int TPR, int NV, int NP>
-__global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
+// Split records: per (head, range) kAttnRec header floats (maximum, sum) then
+// head_dim weighted values.
+constexpr int kAttnRec = 4;
+constexpr int kMaxSplits = 64;
+
+template <int TPR, int NV, int NP, int THREADS>
+__global__ __launch_bounds__(THREADS) void decode_attention_chunk_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ kcache,
     float* __restrict__ vcache, int pos, int n_q, int n_kv, int head_dim, double theta, float scale,
-    float* __restrict__ out) {
-  constexpr int WAVES = kAttnThreads / 64;
+    float* __restrict__ out, int nsplit, int rps, float* __restrict__ part) {
+  constexpr int WAVES = THREADS / 64;
   constexpr int RW = 64 / TPR;         // rows per wave per load
   constexpr int CH = WAVES * RW * NP;  // rows per chunk
   __shared__ __attribute__((aligned(16))) float qr[kMaxDims];
@@ -150,13 +161,14 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
   __shared__ __attribute__((aligned(16))) float vn[kMaxDims];
   __shared__ __attribute__((aligned(16))) float wacc[WAVES][kMaxDims];
   __shared__ float wm[WAVES], wl[WAVES];
-  const int hq = blockIdx.x, group = n_q / n_kv, hkv = hq / group;
+  const int hq = (int)blockIdx.x % n_q, split = (int)blockIdx.x / n_q, group = n_q / n_kv, hkv = hq / group;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int sub = lane % TPR, rg = lane / TPR;
   const int half = head_dim / 2, kvd = n_kv * head_dim;
-  const int nrows = pos;  // cached rows read from memory
-  const int nch = (nrows + CH - 1) / CH;
+  // cached rows [r0, r1) of this range (rows 0..pos-1 are read from memory)
+  const int r0 = min(split * rps, pos), r1 = min(r0 + rps, pos);
+  const int nch = (r1 - r0 + CH - 1) / CH;
   const float* kb = kcache + hkv * head_dim;
   const float* vb = vcache + hkv * head_dim;
 
@@ -166,7 +178,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
   auto load = [&](int slot, int c) {
 #pragma unroll
     for (int p = 0; p < NP; p++) {
-      const int row = min(c * CH + p * WAVES * RW + wave * RW + rg, nrows - 1);
+      const int row = min(r0 + c * CH + p * WAVES * RW + wave * RW + rg, r1 - 1);
 #pragma unroll
       for (int nv = 0; nv < NV; nv++) {
         const int d = min(4 * sub + 4 * TPR * nv, head_dim - 4);
@@ -179,7 +191,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
 
   // RoPE of this head's query and of the KV head's new key; the value as is
   const double ln_theta = log(theta);
-  for (int i = tid; i < half; i += kAttnThreads) {
+  for (int i = tid; i < half; i += THREADS) {
     const double ang = (double)pos * exp((-2.0 * (double)i / (double)head_dim) * ln_theta);
     const double c = cos(ang), s = sin(ang);
     const double q0 = q[hq * head_dim + i], q1 = q[hq * head_dim + i + half];
@@ -189,10 +201,10 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
     kr[i] = (float)(k0 * c - k1 * s);
     kr[i + half] = (float)(k1 * c + k0 * s);
   }
-  for (int d = tid; d < head_dim; d += kAttnThreads) vn[d] = v[hkv * head_dim + d];
+  for (int d = tid; d < head_dim; d += THREADS) vn[d] = v[hkv * head_dim + d];
   __syncthreads();
-  if (hq % group == 0) {
-    for (int d = tid; d < head_dim; d += kAttnThreads) {
+  if (hq % group == 0 && split == 0) {
+    for (int d = tid; d < head_dim; d += THREADS) {
       kcache[(int64_t)pos * kvd + hkv * head_dim + d] = kr[d];
       vcache[(int64_t)pos * kvd + hkv * head_dim + d] = vn[d];
     }
@@ -246,8 +258,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
       }
 #pragma unroll
       for (int off = TPR / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
-      const int row = c * CH + p * WAVES * RW + wave * RW + rg;
-      s[p] = row < nrows ? dot * scale : -INFINITY;
+      const int row = r0 + c * CH + p * WAVES * RW + wave * RW + rg;
+      s[p] = row < r1 ? dot * scale : -INFINITY;
     }
     fold(s, vx[slot]);
   };
@@ -260,7 +272,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
   }
 
   // the new row (pos) from LDS, folded into wave 0's state by its row group 0
-  if (wave == 0) {
+  // (of the last range)
+  if (wave == 0 && split == nsplit - 1) {
     float dot = 0.0f;
     f32x4 vv[NP][NV];
     float s[NP];
@@ -311,11 +324,63 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_chunk_kernel(
     f[w] = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - mx);
     sum += f[w] * wl[w];
   }
-  const float inv = 1.0f / sum;
-  for (int d = tid; d < head_dim; d += kAttnThreads) {
+  if (nsplit == 1) {
+    const float inv = 1.0f / sum;
+    for (int d = tid; d < head_dim; d += THREADS) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; w++) a += f[w] * wacc[w][d];
+      out[hq * head_dim + d] = a * inv;
+    }
+    return;
+  }
+
+  // this range's record; an empty range records maximum -inf and sum 0
+  const int rstride = kAttnRec + head_dim;
+  float* rec = part + ((int64_t)hq * nsplit + split) * rstride;
+  for (int d = tid; d < head_dim; d += THREADS) {
     float a = 0.0f;
 #pragma unroll
     for (int w = 0; w < WAVES; w++) a += f[w] * wacc[w][d];
+    rec[kAttnRec + d] = a;
+  }
+  if (tid == 0) {
+    rec[0] = mx;
+    rec[1] = sum;
+  }
+}
+
+// Merge of the nsplit range records of each head (one workgroup per head), in
+// range order: out = sum_r e_r a_r / sum_r e_r l_r with e_r = exp(m_r - max m).
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_merge_kernel(const float* __restrict__ part,
+                                                                              int nsplit, int head_dim,
+                                                                              float* __restrict__ out) {
+  __shared__ float fac[kMaxSplits], lw[kMaxSplits];
+  __shared__ float inv;
+  const int hq = (int)blockIdx.x, tid = (int)threadIdx.x;
+  const int rstride = kAttnRec + head_dim;
+  const float* hrec = part + (int64_t)hq * nsplit * rstride;
+  if (tid < 64) {
+    const float rm = tid < nsplit ? hrec[(int64_t)tid * rstride] : -INFINITY;
+    float gm = rm;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off, 64));
+    if (tid < nsplit) {
+      const float fr = rm == -INFINITY ? 0.0f : expf(rm - gm);
+      fac[tid] = fr;
+      lw[tid] = fr * hrec[(int64_t)tid * rstride + 1];
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float gs = 0.0f;  // in range order
+    for (int r = 0; r < nsplit; r++) gs += lw[r];
+    inv = 1.0f / gs;
+  }
+  __syncthreads();
+  for (int d = tid; d < head_dim; d += kAttnThreads) {
+    float a = 0.0f;
+    for (int r = 0; r < nsplit; r++) a += fac[r] * hrec[(int64_t)r * rstride + kAttnRec + d];
     out[hq * head_dim + d] = a * inv;
   }
 }
@@ -325,28 +390,81 @@ size_t decode_attention_lds(int64_t pos, int64_t head_dim) {
   return (size_t)(3 * head_dim + pos + 1 + 8) * sizeof(float);
 }
 
+// Row ranges per head of the chunk kernel. Measured on MI355X (hd 128, 16 or
+// 32 heads): a launch costs about 3 us before it reads anything and the merge
+// launch as much again, so a cache under ~256 rows stays in one workgroup per
+// head (8 waves, 2 rows per lane per chunk: 6.4 us at 128 rows against 7.1
+// with 4 waves); longer caches split into ranges of at least kMinSplitRows
+// rows, about one workgroup per CU over all heads (16 heads: 512 rows 16 ->
+// 8 us, 2048 rows 49 -> 11 us, 8192 rows 180 -> 28 us).
+namespace {
+constexpr int kMinSplitRows = 64;
+}  // namespace
+
+AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t head_dim, int cu_count) {
+  AttnSplit p{1, (int)pos, 512, 2, 0};
+  if (!chunk_tpr(head_dim)) return p;
+  const int64_t want = (std::max(cu_count, 1) + n_q - 1) / n_q;
+  const int64_t ns = std::min<int64_t>({want, pos / kMinSplitRows, (int64_t)kMaxSplits});
+  if (ns < 4) return p;
+  p.nsplit = (int)ns;
+  p.rps = (int)((pos + ns - 1) / ns);
+  p.threads = 256;
+  // small ranges take 2 rows per lane per chunk (a chunk is 4 waves x 64 / TPR x NP rows)
+  p.np = p.rps <= 4 * (64 / chunk_tpr(head_dim)) * 2 ? 2 : 8;
+  p.scratch_bytes = (size_t)n_q * (size_t)ns * (size_t)(kAttnRec + head_dim) * sizeof(float);
+  return p;
+}
+
+namespace {
+
+template <int TPR, int NV, int NP, int THREADS>
+hipError_t launch_chunk(const float* q, const float* k, const float* v, float* kcache, float* vcache, int64_t pos,
+                        int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale, float* out,
+                        const AttnSplit& sp, float* part, hipStream_t stream) {
+  const int ns = sp.nsplit;
+  hipLaunchKernelGGL((decode_attention_chunk_kernel<TPR, NV, NP, THREADS>), dim3((unsigned)(n_q * ns)),
+                     dim3(THREADS), 0, stream, q, k, v, kcache, vcache, (int)pos, (int)n_q, (int)n_kv, (int)head_dim,
+                     theta, (float)scale, out, ns, sp.rps, part);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (ns > 1)
+    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3((unsigned)n_q), dim3(kAttnThreads), 0, stream, part, ns,
+                       (int)head_dim, out);
+  return hipGetLastError();
+}
+
+// (threads, rows per lane) of the plan -> one instantiation
+template <int TPR, int NV, int NPS, int NPL>
+hipError_t launch_chunk_cfg(const float* q, const float* k, const float* v, float* kcache, float* vcache, int64_t pos,
+                            int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale, float* out,
+                            const AttnSplit& sp, float* part, hipStream_t stream) {
+#define RQ_ATTN_ARGS q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp, part, stream
+  if (sp.threads == 1024) return launch_chunk<TPR, NV, NPS, 1024>(RQ_ATTN_ARGS);
+  if (sp.threads == 512) return launch_chunk<TPR, NV, NPS, 512>(RQ_ATTN_ARGS);
+  if (sp.np == NPS) return launch_chunk<TPR, NV, NPS, 256>(RQ_ATTN_ARGS);
+  return launch_chunk<TPR, NV, NPL, 256>(RQ_ATTN_ARGS);
+#undef RQ_ATTN_ARGS
+}
+
+}  // namespace
+
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
-                                   double scale, float* out, hipStream_t stream) {
+                                   double scale, float* out, const AttnSplit& sp, void* scratch, hipStream_t stream) {
+  float* part = static_cast<float*>(scratch);
+#define RQ_ATTN_ARGS q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp, part, stream
   switch (chunk_tpr(head_dim)) {
-#define RQ_ATTN(TPR, NV, NP)                                                                                        \
-  hipLaunchKernelGGL((decode_attention_chunk_kernel<TPR, NV, NP>), dim3((unsigned)n_q), dim3(kAttnThreads), 0,   \
-                     stream, q, k, v, kcache, vcache, (int)pos, (int)n_q, (int)n_kv, (int)head_dim, theta,        \
-                     (float)scale, out);                                                                           \
-  return hipGetLastError();
     case 16:
-      RQ_ATTN(16, 1, 8)
+      return launch_chunk_cfg<16, 1, 2, 8>(RQ_ATTN_ARGS);
     case 32:
-      RQ_ATTN(32, 1, 8)
+      return launch_chunk_cfg<32, 1, 2, 8>(RQ_ATTN_ARGS);
     case 64:
-      if (head_dim <= 256) {
-        RQ_ATTN(64, 1, 8)
-      }
-      RQ_ATTN(64, 2, 4)
-#undef RQ_ATTN
+      if (head_dim <= 256) return launch_chunk_cfg<64, 1, 2, 8>(RQ_ATTN_ARGS);
+      return launch_chunk_cfg<64, 2, 2, 4>(RQ_ATTN_ARGS);
     default:
       break;
   }
+#undef RQ_ATTN_ARGS
   const size_t lds = decode_attention_lds(pos, head_dim);
   if (lds > 65536) {
     static std::atomic<uint64_t> attr_set{0};

@@ -177,9 +177,18 @@ hipError_t launch_dx(const Weight& w, const float* dy, float* dx, int64_t m, flo
                      hipStream_t stream);
 // RoPE + KV append + single-query attention for one decode step (attention.hip).
 size_t decode_attention_lds(int64_t pos, int64_t head_dim);
+// Cached rows split into nsplit ranges of rps rows per head; nsplit > 1 needs
+// scratch_bytes of device scratch for the ranges' records.
+struct AttnSplit {
+  int nsplit, rps;
+  int threads;  // workgroup size of the chunk kernel: 256, 512 or 1024
+  int np;       // rows per lane per chunk at 256 threads (2, or the larger default)
+  size_t scratch_bytes;
+};
+AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t head_dim, int cu_count);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
-                                   double scale, float* out, hipStream_t stream);
+                                   double scale, float* out, const AttnSplit& sp, void* scratch, hipStream_t stream);
 // Weight encoders (encode.hip): q4k-of (rows zero-padded from in to inp) and
 // quantize-weight-q6k (in % 256 == 0), device arrays in, device arrays out.
 hipError_t launch_q4k_encode(const float* W, int64_t out, int64_t in, int64_t inp, uint8_t* wq, float* da, float* db,

@@ -198,12 +198,15 @@ def test_fused_rejects_bad_options(torch, ctx):
 @pytest.mark.parametrize("n_q,n_kv,hd,pos", [
     (16, 16, 128, 128), (8, 2, 64, 9), (32, 8, 128, 1000), (4, 4, 64, 0), (4, 1, 256, 5), (2, 2, 320, 3),
     (8, 8, 128, 20000), (4, 2, 128, 63), (4, 2, 128, 64), (4, 2, 128, 65), (6, 3, 96, 200), (2, 1, 512, 70),
-    (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000)])
+    (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000), (2, 1, 512, 2000), (4, 2, 96, 4100)])
 def test_decode_attention(torch, ctx, orc, n_q, n_kv, hd, pos):
     # head_dim a multiple of 4 up to 512 runs the chunk kernel (chunks of 64
     # rows at hd 128: pos 63 / 64 / 65 end inside, at and past a chunk;
-    # hd 96 / 320 leave lanes idle); 66 and 18 run the generic kernel
-    # ((3, 3, 66, 30000): scores beyond 64 KB of LDS). (.., 0): only the new key
+    # hd 96 / 320 leave lanes idle); from 256 cached rows the rows split into
+    # ranges per head, merged by a second kernel ((.., 1000), (.., 20000),
+    # (4, 4, 16, 300), (2, 1, 512, 2000), (4, 2, 96, 4100): ragged last
+    # range); 66 and 18 run the generic kernel ((3, 3, 66, 30000): scores
+    # beyond 64 KB of LDS). (.., 0): only the new key
     import raster_amd
 
     kvd = n_kv * hd
@@ -253,3 +256,50 @@ def test_decode_attention_rejects_bad_shapes(torch, ctx):
         raster_amd.decode_attention(ctx, z(66), z(66), z(66), z((n + 1) * 66), z((n + 1) * 66), n, 1, 1, 66, 1e4,
                                     0.125)
     assert e.value.status == RQ_ERR_SHAPE
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,pos", [(16, 16, 128, 512), (32, 8, 128, 1000), (4, 4, 16, 300)])
+def test_decode_attention_split_repeats_and_graph(torch, ctx, orc, n_q, n_kv, hd, pos):
+    # shapes that split the cached rows over several workgroups per head: the
+    # per-head counters must be zero again after every call, so repeated calls,
+    # and replays of a captured call with eager work in between, give the first
+    # call's output bit for bit
+    import raster_amd
+
+    kvd = n_kv * hd
+    rng = np.random.default_rng(7 + pos)
+    q = rng.standard_normal(n_q * hd, dtype=np.float32)
+    k = rng.standard_normal(kvd, dtype=np.float32)
+    v = rng.standard_normal(kvd, dtype=np.float32)
+    kc = np.zeros((pos + 1, kvd), np.float32)
+    vc = np.zeros((pos + 1, kvd), np.float32)
+    kc[:pos] = rng.standard_normal((pos, kvd), dtype=np.float32)
+    vc[:pos] = rng.standard_normal((pos, kvd), dtype=np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    note(f"decode attention split repeats n_q={n_q} n_kv={n_kv} hd={hd} pos={pos}")
+    dq, dk, dv, dkc, dvc = dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, kc), dev(torch, vc)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    with torch.cuda.stream(s):
+        out = torch.empty(n_q * hd, device="cuda")
+        for _ in range(3):
+            raster_amd.decode_attention(ctx, dq, dk, dv, dkc, dvc, pos, n_q, n_kv, hd, 1e4, scale, out=out)
+            s.synchronize()
+            outs.append(out.cpu().numpy().copy())
+    qr = orc.rope_pos(q, 1, n_q, hd, 1e4, pos)
+    rkc, rvc = kc.copy(), vc.copy()
+    rkc[pos] = orc.rope_pos(k, 1, n_kv, hd, 1e4, pos)
+    rvc[pos] = v
+    ref = orc.gqa_decode_attention(qr, rkc, rvc, pos + 1, n_q, n_kv, hd, scale)
+    assert orc.normwise_relerr(outs[0], ref) < TOL_F32
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        raster_amd.decode_attention(ctx, dq, dk, dv, dkc, dvc, pos, n_q, n_kv, hd, 1e4, scale, out=out)
+    for _ in range(3):
+        out.fill_(0.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), outs[0])
+        _ = torch.ones(16, device="cuda").sum().item()  # eager work between replays
