@@ -22,6 +22,8 @@ the C1 GEMV and the CPU baseline):
                 kernel reading that many bytes per launch reaches here.
   int8, kquant  the int8-activation path and the K-quant GEMV (next-step
                 rows of the path), as before.
+  dx            backward-data (qlinear-q8-dx) of the C2 layer's weight at
+                m = 16 and 512 dy rows (the MFMA GEMM path).
   roofline      the C2 GEMM kernel against dense bf16 MFMA peak (below).
   roofline_gemv the C1 decode kernel against HBM peak (below).
   cpu_baseline  Raster's CPU routes restated in C (oracle/cpu_baseline.c),
@@ -371,6 +373,43 @@ def dense_library_line(torch, M=512, K=4096, N=11008, warmup=200, calls=500):
     return {"what": f"torch.matmul bf16 x[{M},{K}] @ W[{N},{K}]^T (hipBLASLt), dense bf16 weight",
             "us_per_call": round(us, 3), "tflops": round(tflops, 3),
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+
+def dx_lines(torch, ctx, calls=20):
+    """Backward-data (qlinear-q8-dx) of the C2 layer's weight (Q8_0, in 4096,
+    out 11008) at m = 16 and m = 512 dy rows: the MFMA GEMM path. `kernel_us`
+    spans the dy packing pass, the GEMM and the slice reduction (librq's kernel
+    timing); `tflops` counts 2 m in out; the GEMM issues three bf16 MFMAs per
+    product (hi/lo operand splits), so `frac_mfma` = 3 x tflops / dense peak."""
+    import raster_amd
+
+    out_, in_ = 11008, 4096
+    from raster_amd import workloads as wl
+
+    codes, scales = wl.q8_weights(out_, in_, seed=41)
+    w = raster_amd.QWeight.q8(codes, scales, out_, in_, ctx)
+    lines = {}
+    for m in (16, 512):
+        g = torch.Generator(device="cuda").manual_seed(m)
+        dy = torch.randn(m, out_, device="cuda", dtype=torch.float32, generator=g)
+        dx = torch.empty(m, in_, device="cuda", dtype=torch.float32)
+        for _ in range(3):
+            w.matmul_dx(dy, dx)
+        torch.cuda.synchronize()
+        ctx.kernel_time()
+        ctx.set_kernel_timing(True)
+        for _ in range(calls):
+            w.matmul_dx(dy, dx)
+        torch.cuda.synchronize()
+        total, n = ctx.kernel_time()
+        ctx.set_kernel_timing(False)
+        us = total / max(n, 1) * 1e3
+        tflops = 2.0 * m * in_ * out_ / us / 1e6
+        lines[f"dx_q8_m{m}_4096x11008"] = {"m": m, "in": in_, "out": out_, "kernel_us": round(us, 3),
+                                           "tflops": round(tflops, 3),
+                                           "frac_mfma": round(3 * tflops / BF16_PEAK_TFLOPS, 4)}
+    w.destroy()
+    return lines
 
 
 def int8_lines(torch, ctx):
@@ -816,6 +855,8 @@ def main():
         result["read_ceiling"] = sorted(ceiling.cache.values(), key=lambda d: d["bytes"])
         log("int8-activation path")
         result["int8"] = int8_lines(torch, ctx)
+        log("backward-data (dx) GEMM")
+        result["dx"] = dx_lines(torch, ctx)
         log("K-quant GEMV")
         result["kquant"] = kquant_lines(torch, ctx)
     elif not args.only_gemm:

@@ -375,12 +375,39 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
           mf_xpose4(d);
           uint32_t s4[4];
           mf_bcast4(sb, s4);
+          // the quad's four steps side by side: their LDS reads, then the
+          // four MFMA chains, then the four block epilogues, so that neither
+          // the LDS latency nor the MFMA latency is paid once per step. A
+          // step past the share reads the zero slot and has factor 0.
+          bf16x8 ah[4], al[4];
+          f32x4 xo[4];
+          float sv[4];
 #pragma unroll
           for (int jj = 0; jj < 4; jj++) {
             const int u = u0 + 4 * t + jj;
             const int su = kw * spw + u;
-            if (u < spw && su < nst) step(su, mf_q4_dword(d[jj]), scale_from_bits<ST>(s4[jj]));
+            const bool live = u < spw && su < nst;
+            const int ab = su * P * M * 64;
+            ah[jj] = *reinterpret_cast<const bf16x8*>(smem + (live && aoff >= 0 ? ab + aoff : zero_off));
+            if (P == 2)
+              al[jj] = *reinterpret_cast<const bf16x8*>(smem + (live && aoff >= 0 ? ab + M * 64 + aoff : zero_off));
+            xo[jj] = *reinterpret_cast<const f32x4*>(smem + (live ? xs_off + (su * 16 + 4 * qd) * 4 : zero_off));
+            sv[jj] = live ? scale_from_bits<ST>(s4[jj]) : 0.0f;
           }
+          f32x4 blk[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++)
+            blk[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[jj], mf_q4_dword(d[jj]),
+                                                              f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          if (P == 2) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+              blk[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[jj], mf_q4_dword(d[jj]), blk[jj], 0, 0, 0);
+          }
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(sv[jj], blk[jj][e] - xo[jj][e], acc[e]);
         }
       }
       finish(j);

@@ -13,6 +13,7 @@ namespace rq {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -175,6 +176,14 @@ hipError_t launch_kquant_dequant(const Weight& w, float* out, hipStream_t stream
 int dx_slices(int64_t in, int64_t npad, int cu_count);
 hipError_t launch_dx(const Weight& w, const float* dy, float* dx, int64_t m, float* part, int slices,
                      hipStream_t stream);
+// backward-data on bf16 MFMA for m >= kDxMfMinRows (dx_mf.hip): dy packed
+// into `pack` (dx_mf_pack_bytes), reduction slices (part: slices * m * in f32
+// when slices > 1)
+constexpr int64_t kDxMfMinRows = 16;
+size_t dx_mf_pack_bytes(int64_t m, int64_t npad);
+int dx_mf_slices(int64_t m, int64_t in, int64_t npad, int cu_count);
+hipError_t launch_dx_mf(const Weight& w, const float* dy, float* dx, int64_t m, void* pack, float* part, int slices,
+                        hipStream_t stream);
 // RoPE + KV append + single-query attention for one decode step (attention.hip).
 size_t decode_attention_lds(int64_t pos, int64_t head_dim);
 // Cached rows split into nsplit ranges of rps rows per head; nsplit > 1 needs

@@ -1,12 +1,15 @@
 """GPU parity of the backward-data matmul (rq_qmatmul_dx, rq_qlinear_q8_dx)
 against the C oracle's qlinear-q8-dx (raster/quant/train.clj:110-137).
 
-dx[m, i] = sum_o scale[o, i/32] * code[o, i] * dy[m, o]: per-term products
-rounded to f32 on both sides, the GPU sums in f32 where Raster sums in double:
-normwise max|dx - ref| / max|ref| < 2e-5. Q4_0 (Raster has no Q4 dx) is
-checked against a float64 product with the bit-exact Q4_0 dequant. The
-adjoint identity <dy, W x> = <dx, x> pins the transpose independently of the
-oracle's dx.
+dx[m, i] = sum_o scale[o, i/32] * code[o, i] * dy[m, o]. Below 16 dy rows the
+per-term products are rounded to f32 as Raster does and summed in f32 (Raster:
+double); from 16 rows the MFMA GEMM carries w = scale * code (Raster's f32
+product) and dy each as bf16 hi + lo (relative 2^-16) and adds hi*hi + hi*lo +
+lo*hi in f32, so each product is within about 3 * 2^-16 of the f32 one (about
+4e-6 normwise measured). Both: normwise max|dx - ref| / max|ref| < 2e-5. Q4_0
+(Raster has no Q4 dx) is checked against a float64 product with the bit-exact
+Q4_0 dequant. The adjoint identity <dy, W x> = <dx, x> pins the transpose
+independently of the oracle's dx.
 """
 import numpy as np
 import pytest
@@ -107,4 +110,71 @@ def test_qlinear_q8_dx_host_surface(torch, ctx, orc):
     dx = raster_amd.qlinear_q8_dx(dy, codes, scales, m, in_, out, ctx)
     ref = orc.qlinear_q8_dx(dy, codes, scales, m, in_, out)
     assert dx.shape == (m * in_,)
+    assert orc.normwise_relerr(dx, ref) < TOL
+
+
+# ------------------------------------------------ MFMA GEMM path (m >= 16)
+@pytest.mark.parametrize("m,in_,out", [(16, 256, 200), (100, 256, 200), (130, 1056, 48), (512, 1024, 2048),
+                                       (33, 4096, 11008)])
+def test_dx_mfma_q8(torch, ctx, orc, m, in_, out):
+    # 16: the smallest m on the MFMA path; 100 / 130: a partial last row tile;
+    # in 1056: 33 blocks, a partial last column tile; out 200 / 48: a partial
+    # last 16-row group and an odd group count; (512, 1024, 2048), (33, ..,
+    # 11008): the reduction cut into slices
+    import raster_amd
+
+    codes, scales = wl.q8_weights(out, in_, seed=out + 1)
+    dy = wl.activations(m, out, seed=in_ + 2)
+    note(f"dx mfma q8 m={m} in={in_} out={out}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    dx = w.matmul_dx(dev(torch, dy).reshape(m, out))
+    dx2 = w.matmul_dx(dev(torch, dy).reshape(m, out))
+    torch.cuda.synchronize()
+    w.destroy()
+    assert torch.equal(dx, dx2), "fixed order: slices and MFMA chains"
+    ref = orc.qlinear_q8_dx(dy, codes, scales, m, in_, out).reshape(m, in_)
+    assert orc.normwise_relerr(dx.cpu().numpy(), ref) < TOL
+
+
+def test_dx_mfma_c2_layer_rows(torch, ctx, orc):
+    # the backward of the C2 layer (m = 512 dy rows, in 4096, out 11008) on
+    # the GPU; rows 0, 1, 255 and 511 against the oracle, every row by the
+    # adjoint identity <dy_r, W x> = <dx_r, x> with one x (the oracle's m = 1
+    # forward)
+    import raster_amd
+
+    m, in_, out = 512, 4096, 11008
+    codes, scales = wl.q8_weights(out, in_, seed=21)
+    dy = wl.activations(m, out, seed=22).reshape(m, out)
+    note(f"dx mfma q8 C2 layer m={m} in={in_} out={out}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    dx = w.matmul_dx(dev(torch, dy)).cpu().numpy().astype(np.float64)
+    w.destroy()
+    rows = [0, 1, 255, 511]
+    ref = orc.qlinear_q8_dx(dy[rows], codes, scales, len(rows), in_, out).reshape(len(rows), in_)
+    assert orc.normwise_relerr(dx[rows], ref) < TOL
+    x = wl.activations(1, in_, seed=23)
+    y = orc.qlinear_q8(x, codes, scales, 1, in_, out).astype(np.float64)
+    lhs = dy.astype(np.float64) @ y
+    rhs = dx @ x.astype(np.float64)
+    bound = 1e-5 * (np.abs(dy).sum(axis=1) * np.abs(y).max() + 1e-9)
+    assert np.all(np.abs(lhs - rhs) <= bound)
+
+
+@pytest.mark.parametrize("scale_kind", ["f16", "f32"])
+def test_dx_mfma_q4(torch, ctx, orc, scale_kind):
+    import raster_amd
+
+    m, in_, out = 64, 512, 160
+    packed, sc16 = wl.q4_weights(out, in_, seed=31)
+    dy = wl.activations(m, out, seed=32)
+    if scale_kind == "f16":
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+    else:
+        w = raster_amd.QWeight.q4(packed, orc.f16_bits_to_f32(sc16), out, in_, ctx)
+    note(f"dx mfma q4 {scale_kind} m={m} in={in_} out={out}")
+    dx = w.matmul_dx(dev(torch, dy).reshape(m, out)).cpu().numpy()
+    w.destroy()
+    W = orc.dequant_q4(packed, sc16, in_, out).reshape(out, in_).astype(np.float64)
+    ref = dy.reshape(m, out).astype(np.float64) @ W
     assert orc.normwise_relerr(dx, ref) < TOL
