@@ -152,17 +152,30 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * GEMV; m <= 16 runs the HBM-bound GEMV kernels, larger m the MFMA GEMM.
  * m == 0 is a no-op.
  *
+ * Kernel by call (plain calls; every rq_qmatmul_fused call takes the int8-level
+ * decode kernel):
+ *  - m = 1, Q4_0: the v_dot4_i32_i8 GEMV;
+ *  - m <= 16, MFMA decode (bf16 MFMA on exact codes): Q4_0 at 5 <= m <= 16,
+ *    Q8_0 at 9 <= m <= 16 when out * in <= 32 Mi (2^25) elements;
+ *  - every other m <= 16: the int8-level decode kernel (int8 MFMA on the raw
+ *    codes, v_mfma_i32_16x16x64_i8);
+ *  - m > 16: bf16 x: the bf16 MFMA GEMM (Q4_0 at 16 < m <= 64: the
+ *    weight-stream GEMM); f32 x: the exact-code f32 GEMM.
+ *
  * Numerics (all accumulation in f32):
- *  - m <= 8 (Q4_0: m <= 4; every fused call): int8 MFMA (m = 1 with Q4_0:
- *    v_dot4_i32_i8) on the raw weight codes. Each 32-block of each
- *    activation row is held as a 16-bit block fixed-point value: X = rint(x * 2^(15-e)) with e the block's max
- *    exponent, |X| < 2^15, so the per-element error is <= 2^(e-16) (below
- *    1.6e-5 relative to the block maximum). An inf or NaN activation makes its
- *    row's outputs NaN.
- *  - 8 < m <= 16 (Q4_0: 4 < m <= 16): bf16 MFMA on the exact codes (offset so that every code is
- *    a small integer in bf16), the block scale applied in f32 to each block's
- *    dot; f32 x split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|). A
- *    non-finite activation makes its row's outputs non-finite.
+ *  - v_dot4 GEMV and int8-level decode kernel: each 32-block of each
+ *    activation row is held as a 16-bit block fixed-point value:
+ *    X = rint(x * 2^(15-e)) with e the block's max exponent, |X| < 2^15, so
+ *    the per-element error is <= 2^(e-16) (below 1.6e-5 relative to the block
+ *    maximum); the integer dots are exact, the block scale applied in f32. An
+ *    inf or NaN activation makes its row's outputs NaN.
+ *  - MFMA decode: codes enter the bf16 MFMA exactly, offset to small
+ *    non-negative integers (c + 136 for Q4_0, c + 128 for Q8_0), the offset
+ *    times the block's activation sum subtracted and the block scale applied
+ *    in f32; f32 x split into two bf16 terms (|x - hi - lo| <= 2^-17 |x|).
+ *    Finite input range: a block whose largest |x| exceeds about 7e34 (Q4_0)
+ *    or 4e34 (Q8_0) overflows the offset sums and makes its row's outputs
+ *    NaN; a non-finite activation makes its row's outputs non-finite.
  *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
  *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
@@ -173,11 +186,13 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * do not share it):
  *  - bf16 x with m > 16: the packed activation tile, ceil(m/16)*16*in*2 bytes;
  *  - K-slices' partial sums, m * out * 4 bytes per slice, added in slice
- *    order by a second kernel: m <= 8 with activations too long for one
- *    workgroup's LDS (in above 17472 at m <= 4, 8704 at m <= 8); 8 < m <= 16
- *    when a slice of x no longer fits two workgroups' LDS (in above 1216 at
- *    m = 16 with f32 x, up to 4096 at m = 9 with bf16 x), up to in / 32 slices;
- *    Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to 8 slices).
+ *    order by a second kernel: the int8-level decode kernel when a row of x
+ *    does not fit one workgroup's LDS (in above 17472 at m <= 4, 8704 at
+ *    m <= 8); the MFMA decode kernel when a slice of x would not fit two
+ *    workgroups' LDS, and further until the grid covers about 85% of the CUs,
+ *    rounded up to a power of two while each slice keeps 8 blocks (at most
+ *    in / 32 slices); Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to
+ *    8 slices).
  * Under HIP graph capture nothing can be allocated: run the same (or a
  * larger) shape once on the capturing stream before capturing, otherwise the
  * call fails with RQ_ERR_SHAPE and a message saying so.

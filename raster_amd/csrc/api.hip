@@ -770,10 +770,11 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
 
 // Launches the matmul of a validated call: for m <= 16 the int8 decode kernel
 // (for m = 1 with Q4_0 weights the sdot4 GEMV instead, unless a norm,
-// residual or SwiGLU is fused; for 4 < m <= 16 (Q4_0) or 8 < m <= 16 (Q8_0)
-// without fused options, f32 /
-// bf16 x, the MFMA decode kernel), else the GEMM for the activation dtype;
-// per-stream scratch and kernel timing around it.
+// residual or SwiGLU is fused; without fused options and with f32 / bf16 x,
+// the MFMA decode kernel where plan_gemv_mf takes the shape: Q4_0 at
+// 5 <= m <= 16, Q8_0 at 9 <= m <= 16 up to 32 Mi weight elements), else the
+// GEMM for the activation dtype; per-stream scratch and kernel timing around
+// it.
 static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const void* x, int x_dtype, void* y,
                       int y_dtype, int64_t m, const DecodeOps& dops, hipStream_t stream, FixedScratch* fixed) {
   if (int s = set_device(c)) return s;
