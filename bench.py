@@ -755,6 +755,9 @@ def main():
     ap.add_argument("--only-gemm", action="store_true", help="time the headline GEMM only (for profiling)")
     ap.add_argument("--only-decode", action="store_true",
                     help="the decode shapes only (C1, C3, C5 at M = 1 and 32, the decoder step) for profiling")
+    ap.add_argument("--counter-run", action="store_true",
+                    help="a short run for rocprofv3 --pmc instruction / busy counters: the headline GEMM, then "
+                         "the int8 GEMM at the same shape, 10 calls each")
     ap.add_argument("--traffic-run", action="store_true",
                     help="a short run for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: a copy kernel of "
                          "known size (calibration), then the headline GEMM and the cold C1 decode kernel")
@@ -781,6 +784,18 @@ def main():
 
     if args.traffic_run:
         traffic_run(torch, ctx)
+        ctx.close()
+        return
+
+    if args.counter_run:
+        w = Weights(ctx, "q8", 4096, 11008, 1)
+        for xdt in ("bf16", "i8"):
+            c = Case(torch, ctx, w, 512, xdt, "bf16")
+            for _ in range(10):
+                c.step()
+            torch.cuda.synchronize()
+            log(f"counter run: 10 x C2-shape GEMM, {xdt} activations")
+        w.destroy()
         ctx.close()
         return
 
