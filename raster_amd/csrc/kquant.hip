@@ -271,9 +271,12 @@ static hipError_t launch_kq_t(const Weight& w, const int8_t* xq, const float* xs
       attr_set.fetch_or(bit, std::memory_order_acq_rel);
     }
   }
-  // enough waves for every row group, at most 8 per CU
+  // a wave per row group, all of them launched at once: at 14336 x 4096,
+  // m = 1, cold, Q4_K 10.9 us and Q6_K 17.4 us against 11.1-11.3 / 18.5 with
+  // at most 8 waves per CU (each then taking ~2 groups one after another)
   const int64_t groups = (w.out + kKqRows - 1) / kKqRows;
-  const int64_t wg = std::min<int64_t>((groups + 3) / 4, (int64_t)cu_count * 2);
+  const int64_t wg = (groups + 3) / 4;
+  (void)cu_count;
   hipLaunchKernelGGL(kernel, dim3((unsigned)std::max<int64_t>(wg, 1)), dim3(kKqThreads), (unsigned)lds, stream, w.q,
                      w.scales, w.sub_scales, xq, xs, bsums, y, (int)m, (int)w.in, (int)w.out, y_dtype);
   return hipGetLastError();
