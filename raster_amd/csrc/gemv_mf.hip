@@ -11,15 +11,17 @@
 // * Codes enter the MFMA exactly, with an offset: a Q4_0 nibble n as the bf16
 //   128 + n (a byte permute with 0x43, the high byte of 128.0), a Q8_0 code c
 //   as c + 128 (v_cvt_f32_ubyte of c ^ 0x80; every integer below 256 is a
-//   bf16). Per block the MFMA gives sum x (c + OFF) in f32, OFF = 136 for Q4
-//   (c = n - 8) and 128 for Q8; subtracting OFF * sum (hi + lo), formed when
-//   the activations are staged, leaves the block's dot product, which the
-//   block scale multiplies in f32. No rounding of scale * code is involved.
+//   bf16). Per block the MFMA adds sum x (c + OFF) in f32, OFF = 136 for Q4
+//   (c = n - 8) and 128 for Q8, to an accumulator that starts at
+//   -OFF * sum (hi + lo) (formed when the activations are staged, fed as the
+//   MFMA's C operand), which leaves the block's dot product for the block
+//   scale to multiply in f32. No rounding of scale * code is involved.
 // * A workgroup has GW x KW waves and one K-slice (grid.x = columns x ks). It
 //   stages its slice of x (all m rows, hi and lo) in LDS once; then each wave
 //   streams the weight chunks of its 16-row groups through a WD-step register
 //   ring: A = the activation fragment from LDS (lane (r, q): row r, k = 8q ..
-//   8q+7; rows past m read a zero slot), B = the 16 x 32 chunk in the same
+//   8q+7; rows past m read row m - 1, whose products land only in outputs
+//   that are never stored), B = the 16 x 32 chunk in the same
 //   lane order, so lane (r, q) ends up holding y[4q + v][16 g + r], v < 4.
 //   Q4_0 chunks come in fours: lane (r, q) loads the 16-byte row r of the
 //   q-th chunk of a quad (a wave's load moves 1 KB, against 256 B of 8-byte
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
           *reinterpret_cast<u32x4*>(f + qq * 16) = u32x4{hi[0], hi[1], hi[2], hi[3]};
           if (P == 2) *reinterpret_cast<u32x4*>(f + M * 64 + qq * 16) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         }
-        if (qq == 0) *reinterpret_cast<float*>(smem + xs_off + (u * 16 + m) * 4) = OFF * sum;
+        if (qq == 0) *reinterpret_cast<float*>(smem + xs_off + (u * 16 + m) * 4) = -OFF * sum;
       }
     }
   };
@@ -342,19 +344,21 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
     acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   };
 
-  const int aoff = r < M ? r * 64 + qd * 16 : -1;
+  // rows past m read row m - 1: their outputs are never stored, and the rows
+  // stored do not depend on them
+  const int aoff = min(r, M - 1) * 64 + qd * 16;
   // one step's MFMAs and block epilogue
   auto step = [&](int su, const bf16x8& bw, float sv) {
     const int ab = su * P * M * 64;
-    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + aoff : zero_off));
-    f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(smem + ab + aoff);
+    const f32x4 xo = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
+    f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, xo, 0, 0, 0);
     if (P == 2) {
-      const bf16x8 al = *reinterpret_cast<const bf16x8*>(smem + (aoff >= 0 ? ab + M * 64 + aoff : zero_off));
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(smem + ab + M * 64 + aoff);
       blk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, blk, 0, 0, 0);
     }
-    const f32x4 xo = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] = fmaf(sv, blk[e] - xo[e], acc[e]);
+    for (int e = 0; e < 4; e++) acc[e] = fmaf(sv, blk[e], acc[e]);
   };
   if constexpr (FMT == RQ_Q4_0) {
     for (int j = 0; j < nunits; j++) {
@@ -378,27 +382,26 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
           // the quad's four steps side by side: their LDS reads, then the
           // four MFMA chains, then the four block epilogues, so that neither
           // the LDS latency nor the MFMA latency is paid once per step. A
-          // step past the share reads the zero slot and has factor 0.
+          // step past the share reads the slice's last step again and has
+          // factor 0 (a finite block dot, or a row already non-finite).
           bf16x8 ah[4], al[4];
           f32x4 xo[4];
           float sv[4];
 #pragma unroll
           for (int jj = 0; jj < 4; jj++) {
             const int u = u0 + 4 * t + jj;
-            const int su = kw * spw + u;
-            const bool live = u < spw && su < nst;
+            const bool live = u < spw && kw * spw + u < nst;  // workgroup-uniform
+            const int su = min(kw * spw + u, nst - 1);
             const int ab = su * P * M * 64;
-            ah[jj] = *reinterpret_cast<const bf16x8*>(smem + (live && aoff >= 0 ? ab + aoff : zero_off));
-            if (P == 2)
-              al[jj] = *reinterpret_cast<const bf16x8*>(smem + (live && aoff >= 0 ? ab + M * 64 + aoff : zero_off));
-            xo[jj] = *reinterpret_cast<const f32x4*>(smem + (live ? xs_off + (su * 16 + 4 * qd) * 4 : zero_off));
+            ah[jj] = *reinterpret_cast<const bf16x8*>(smem + ab + aoff);
+            if (P == 2) al[jj] = *reinterpret_cast<const bf16x8*>(smem + ab + M * 64 + aoff);
+            xo[jj] = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
             sv[jj] = live ? scale_from_bits<ST>(s4[jj]) : 0.0f;
           }
           f32x4 blk[4];
 #pragma unroll
           for (int jj = 0; jj < 4; jj++)
-            blk[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[jj], mf_q4_dword(d[jj]),
-                                                              f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            blk[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[jj], mf_q4_dword(d[jj]), xo[jj], 0, 0, 0);
           if (P == 2) {
 #pragma unroll
             for (int jj = 0; jj < 4; jj++)
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
 #pragma unroll
           for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = fmaf(sv[jj], blk[jj][e] - xo[jj][e], acc[e]);
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(sv[jj], blk[jj][e], acc[e]);
         }
       }
       finish(j);
