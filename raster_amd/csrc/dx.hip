@@ -102,13 +102,24 @@ __global__ __launch_bounds__(kDxThreads) void dx_kernel(const uint8_t* __restric
   }
 }
 
-// dx = sum over slices of the partial sums, in slice order
+// dx = sum over slices of the partial sums, in slice order (the slices'
+// loads go out four at a time; the adds stay in order)
 __global__ __launch_bounds__(256) void dx_reduce_kernel(const float* __restrict__ part, float* __restrict__ dx,
                                                        int64_t n4, int slices) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= n4) return;
-  f32x4 t = reinterpret_cast<const f32x4*>(part)[e];
-  for (int s = 1; s < slices; s++) t += reinterpret_cast<const f32x4*>(part)[(int64_t)s * n4 + e];
+  const f32x4* p = reinterpret_cast<const f32x4*>(part);
+  f32x4 t = p[e];
+  int s = 1;
+  for (; s + 3 < slices; s += 4) {
+    const f32x4 a = p[(int64_t)s * n4 + e], b = p[(int64_t)(s + 1) * n4 + e];
+    const f32x4 c = p[(int64_t)(s + 2) * n4 + e], d = p[(int64_t)(s + 3) * n4 + e];
+    t += a;
+    t += b;
+    t += c;
+    t += d;
+  }
+  for (; s < slices; s++) t += p[(int64_t)s * n4 + e];
   reinterpret_cast<f32x4*>(dx)[e] = t;
 }
 

@@ -293,23 +293,45 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   }
 }
 
-// y = sum over K-slices of the partial sums part[s * n + e], in slice order
+// y = sum over K-slices of the partial sums part[s * n + e], in slice order.
+// V elements per thread (4: 16-byte loads); the slices' loads go out four at
+// a time (a loop over a run-time slice count would otherwise wait for each
+// load before issuing the next), the adds stay in slice order.
+template <int V>
 __global__ __launch_bounds__(256) void gemm_sm_reduce_kernel(const float* __restrict__ part, void* __restrict__ y,
                                                             int64_t n, int ks, int y_dtype) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef float fv __attribute__((ext_vector_type(V)));
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
   if (e >= n) return;
-  float t = part[e];
-  for (int s = 1; s < ks; s++) t += part[(int64_t)s * n + e];
-  if (y_dtype == RQ_F32)
-    static_cast<float*>(y)[e] = t;
-  else
-    static_cast<uint16_t*>(y)[e] = (uint16_t)f32_to_bf16_bits(t);
+  auto ld = [&](int s) { return *reinterpret_cast<const fv*>(part + (int64_t)s * n + e); };
+  fv t = ld(0);
+  int s = 1;
+  for (; s + 3 < ks; s += 4) {
+    const fv a = ld(s), b = ld(s + 1), c = ld(s + 2), d = ld(s + 3);
+    t += a;
+    t += b;
+    t += c;
+    t += d;
+  }
+  for (; s < ks; s++) t += ld(s);
+  if (y_dtype == RQ_F32) {
+    *reinterpret_cast<fv*>(static_cast<float*>(y) + e) = t;
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; i++) static_cast<uint16_t*>(y)[e + i] = (uint16_t)f32_to_bf16_bits(t[i]);
+  }
 }
 
 hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
                                hipEvent_t stop) {
-  hipExtLaunchKernelGGL(gemm_sm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, nullptr, stop,
-                        0, part, y, n, ks, y_dtype);
+  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(y) & (y_dtype == RQ_F32 ? 15 : 1)) == 0;
+  if (vec)
+    hipExtLaunchKernelGGL(gemm_sm_reduce_kernel<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, stream,
+                          nullptr, stop, 0, part, y, n, ks, y_dtype);
+  else
+    hipExtLaunchKernelGGL(gemm_sm_reduce_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, nullptr,
+                          stop, 0, part, y, n, ks, y_dtype);
   return hipGetLastError();
 }
 

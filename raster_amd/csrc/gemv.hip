@@ -556,8 +556,18 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   float v[MG], rinv[MG];
 #pragma unroll
   for (int mg = 0; mg < MG; mg++) {
+    // the slices' loads four at a time, the adds in slice order
+    auto ld = [&](int sl) { return part[((int64_t)sl * ngroups + g) * (MG * 64) + mg * 64 + lane]; };
     float t = 0.0f;
-    for (int sl = 0; sl < ksplit; sl++) t += part[((int64_t)sl * ngroups + g) * (MG * 64) + mg * 64 + lane];
+    int sl = 0;
+    for (; sl + 3 < ksplit; sl += 4) {
+      const float a = ld(sl), b = ld(sl + 1), c = ld(sl + 2), d = ld(sl + 3);
+      t += a;
+      t += b;
+      t += c;
+      t += d;
+    }
+    for (; sl < ksplit; sl++) t += ld(sl);
     v[mg] = t;
     const int m = 4 * mg + (lane >> 4);
     rinv[mg] = ops.norm_gain && m < M ? 1.0f / sqrtf(ss[m] / (float)K + ops.norm_eps) : 1.0f;

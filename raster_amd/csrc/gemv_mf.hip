@@ -371,14 +371,16 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
             sb = wq[t].s;
           else
             sb = __builtin_bit_cast(uint32_t, wq[t].s);
-          // unconditional refill (past the end it rereads the last quad): a
-          // conditional load leaves the compiler unsure how many loads are in
-          // flight, and its waits then drain the ring once per turn
-          load_q(t, lj, lu);
-          advance4(lj, lu);
           mf_xpose4(d);
           uint32_t s4[4];
           mf_bcast4(sb, s4);
+          // unconditional refill (past the end it rereads the last quad): a
+          // conditional load leaves the compiler unsure how many loads are in
+          // flight, and its waits then drain the ring once per turn. Issued
+          // after the lane swaps have consumed the slot, so the slot's
+          // registers need no copy.
+          load_q(t, lj, lu);
+          advance4(lj, lu);
           // the quad's four steps side by side: their LDS reads, then the
           // four MFMA chains, then the four block epilogues, so that neither
           // the LDS latency nor the MFMA latency is paid once per step. A
