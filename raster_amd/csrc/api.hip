@@ -983,7 +983,7 @@ int rq_decode_attention(rq_ctx h, const float* q, const float* k, const float* v
                               "or above 512: about 40K positions)");
   if (!(theta > 0.0)) return fail(RQ_ERR_SHAPE, "theta must be positive");
   if (int s = set_device(c)) return s;
-  const AttnSplit sp = plan_decode_attention(pos, n_q, head_dim, c->cu_count);
+  const AttnSplit sp = plan_decode_attention(pos, n_q, n_kv, head_dim, c->cu_count);
   void* scratch_buf = nullptr;
   if (sp.nsplit > 1)
     if (int s = stream_attn(c, (hipStream_t)stream, sp.scratch_bytes, &scratch_buf)) return s;

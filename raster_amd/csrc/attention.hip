@@ -350,6 +350,231 @@ __global__ __launch_bounds__(THREADS) void decode_attention_chunk_kernel(
   }
 }
 
+// Grouped-query form of the chunk kernel: one workgroup per (KV head, row
+// range) serves all G query heads that read that KV head, so each cached row
+// is loaded once instead of G times. Per row a lane forms the G partial dot
+// products of its dimensions; each head keeps its own online softmax state.
+// G query heads hkv G .. hkv G + G - 1; 4 waves; 2 rows per lane per chunk.
+// LDS (dynamic): qr[G][hd], kr[hd], vn[hd], wacc[WAVES][G][hd], wm / wl[WAVES][G].
+template <int TPR, int NV, int G>
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_gqa_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ kcache,
+    float* __restrict__ vcache, int pos, int n_q, int n_kv, int head_dim, double theta, float scale,
+    float* __restrict__ out, int nsplit, int rps, float* __restrict__ part) {
+  constexpr int WAVES = kAttnThreads / 64;
+  constexpr int NP = 2;
+  constexpr int RW = 64 / TPR;         // rows per wave per load
+  constexpr int CH = WAVES * RW * NP;  // rows per chunk
+  extern __shared__ __attribute__((aligned(16))) float gsm[];
+  float* qr = gsm;                         // [G][head_dim]
+  float* kr = qr + G * head_dim;           // [head_dim]
+  float* vn = kr + head_dim;               // [head_dim]
+  float* wacc = vn + head_dim;             // [WAVES][G][head_dim]
+  float* wm = wacc + WAVES * G * head_dim;  // [WAVES][G]
+  float* wl = wm + WAVES * G;               // [WAVES][G]
+  const int hkv = (int)blockIdx.x % n_kv, split = (int)blockIdx.x / n_kv, hq0 = hkv * G;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane % TPR, rg = lane / TPR;
+  const int half = head_dim / 2, kvd = n_kv * head_dim;
+  const int r0 = min(split * rps, pos), r1 = min(r0 + rps, pos);
+  const int nch = (r1 - r0 + CH - 1) / CH;
+  const float* kb = kcache + hkv * head_dim;
+  const float* vb = vcache + hkv * head_dim;
+
+  f32x4 kx[2][NP][NV], vx[2][NP][NV];
+  auto load = [&](int slot, int c) {
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const int row = min(r0 + c * CH + p * WAVES * RW + wave * RW + rg, r1 - 1);
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) {
+        const int d = min(4 * sub + 4 * TPR * nv, head_dim - 4);
+        kx[slot][p][nv] = *reinterpret_cast<const f32x4*>(kb + (int64_t)row * kvd + d);
+        vx[slot][p][nv] = *reinterpret_cast<const f32x4*>(vb + (int64_t)row * kvd + d);
+      }
+    }
+  };
+  if (nch > 0) load(0, 0);
+
+  // RoPE of the G queries and of the KV head's new key (the angle depends on
+  // the dimension only); the value as is
+  const double ln_theta = log(theta);
+  for (int i = tid; i < half; i += kAttnThreads) {
+    const double ang = (double)pos * exp((-2.0 * (double)i / (double)head_dim) * ln_theta);
+    const double c = cos(ang), s = sin(ang);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const double q0 = q[(hq0 + g) * head_dim + i], q1 = q[(hq0 + g) * head_dim + i + half];
+      qr[g * head_dim + i] = (float)(q0 * c - q1 * s);
+      qr[g * head_dim + i + half] = (float)(q1 * c + q0 * s);
+    }
+    const double k0 = k[hkv * head_dim + i], k1 = k[hkv * head_dim + i + half];
+    kr[i] = (float)(k0 * c - k1 * s);
+    kr[i + half] = (float)(k1 * c + k0 * s);
+  }
+  for (int d = tid; d < head_dim; d += kAttnThreads) vn[d] = v[hkv * head_dim + d];
+  __syncthreads();
+  if (split == 0) {
+    for (int d = tid; d < head_dim; d += kAttnThreads) {
+      kcache[(int64_t)pos * kvd + hkv * head_dim + d] = kr[d];
+      vcache[(int64_t)pos * kvd + hkv * head_dim + d] = vn[d];
+    }
+  }
+  f32x4 q4[G][NV];
+  bool dlive[NV];
+#pragma unroll
+  for (int nv = 0; nv < NV; nv++) {
+    const int d = 4 * sub + 4 * TPR * nv;
+    dlive[nv] = d < head_dim;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(qr + g * head_dim + min(d, head_dim - 4));
+      q4[g][nv] = dlive[nv] ? t : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+
+  float m[G], l[G];
+  f32x4 acc[G][NV];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++) acc[g][nv] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // fold the scores s[g][p] of NP rows (values vv) into head g's state
+  auto fold = [&](int g, const float (&s)[NP], const f32x4 (&vv)[NP][NV]) {
+    float mc = s[0];
+#pragma unroll
+    for (int p = 1; p < NP; p++) mc = fmaxf(mc, s[p]);
+#pragma unroll
+    for (int off = TPR; off < 64; off <<= 1) mc = fmaxf(mc, __shfl_xor(mc, off, 64));
+    const float mn = fmaxf(m[g], mc);
+    const float alpha = m[g] == -INFINITY ? 0.0f : expf(m[g] - mn);
+    l[g] *= alpha;
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++) acc[g][nv] *= alpha;
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const float e = s[p] == -INFINITY ? 0.0f : expf(s[p] - mn);
+      l[g] += e;
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++) acc[g][nv] += e * vv[p][nv];
+    }
+    m[g] = mn;
+  };
+  auto compute = [&](int slot, int c) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float s[NP];
+#pragma unroll
+      for (int p = 0; p < NP; p++) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int nv = 0; nv < NV; nv++) {
+          const f32x4 kk = kx[slot][p][nv];
+          dot += q4[g][nv][0] * kk[0] + q4[g][nv][1] * kk[1] + q4[g][nv][2] * kk[2] + q4[g][nv][3] * kk[3];
+        }
+#pragma unroll
+        for (int off = TPR / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+        const int row = r0 + c * CH + p * WAVES * RW + wave * RW + rg;
+        s[p] = row < r1 ? dot * scale : -INFINITY;
+      }
+      fold(g, s, vx[slot]);
+    }
+  };
+  for (int c = 0; c < nch; c += 2) {
+    if (c + 1 < nch) load(1, c + 1);
+    compute(0, c);
+    if (c + 1 >= nch) break;
+    if (c + 2 < nch) load(0, c + 2);
+    compute(1, c + 1);
+  }
+
+  // the new row (pos) from LDS, folded into wave 0's states by its row group
+  // 0 (of the last range)
+  if (wave == 0 && split == nsplit - 1) {
+    f32x4 vv[NP][NV], kk[NV];
+#pragma unroll
+    for (int nv = 0; nv < NV; nv++) {
+      const int d = min(4 * sub + 4 * TPR * nv, head_dim - 4);
+      kk[nv] = *reinterpret_cast<const f32x4*>(kr + d);
+      vv[0][nv] = *reinterpret_cast<const f32x4*>(vn + d);
+#pragma unroll
+      for (int p = 1; p < NP; p++) vv[p][nv] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++)
+        dot += q4[g][nv][0] * kk[nv][0] + q4[g][nv][1] * kk[nv][1] + q4[g][nv][2] * kk[nv][2] +
+               q4[g][nv][3] * kk[nv][3];
+#pragma unroll
+      for (int off = TPR / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, 64);
+      float s[NP];
+      s[0] = rg == 0 ? dot * scale : -INFINITY;
+#pragma unroll
+      for (int p = 1; p < NP; p++) s[p] = -INFINITY;
+      fold(g, s, vv);
+    }
+  }
+
+  // each head: the wave's row groups, then the waves
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+#pragma unroll
+    for (int off = TPR; off < 64; off <<= 1) {
+      l[g] += __shfl_xor(l[g], off, 64);
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[g][nv][e] += __shfl_xor(acc[g][nv][e], off, 64);
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int nv = 0; nv < NV; nv++)
+        if (dlive[nv])
+          *reinterpret_cast<f32x4*>(&wacc[(wave * G + g) * head_dim + 4 * sub + 4 * TPR * nv]) = acc[g][nv];
+    }
+    if (lane == 0) {
+      wm[wave * G + g] = m[g];
+      wl[wave * G + g] = l[g];
+    }
+  }
+  __syncthreads();
+  const int rstride = kAttnRec + head_dim;
+  for (int idx = tid; idx < G * head_dim; idx += kAttnThreads) {
+    const int g = idx / head_dim, d = idx - g * head_dim;
+    float mx = wm[g];
+#pragma unroll
+    for (int w = 1; w < WAVES; w++) mx = fmaxf(mx, wm[w * G + g]);
+    float a = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) {
+      const float f = wm[w * G + g] == -INFINITY ? 0.0f : expf(wm[w * G + g] - mx);
+      sum += f * wl[w * G + g];
+      a += f * wacc[(w * G + g) * head_dim + d];
+    }
+    const int hq = hq0 + g;
+    if (nsplit == 1) {
+      out[hq * head_dim + d] = a * (1.0f / sum);
+    } else {
+      float* rec = part + ((int64_t)hq * nsplit + split) * rstride;
+      rec[kAttnRec + d] = a;
+      if (d == 0) {
+        rec[0] = mx;
+        rec[1] = sum;
+      }
+    }
+  }
+}
+
+size_t decode_attention_gqa_lds(int64_t head_dim, int g) {
+  return (size_t)((g + 2) * head_dim + (kAttnThreads / 64) * (g * head_dim + 2 * g)) * sizeof(float);
+}
+
 // Merge of the nsplit range records of each head (one workgroup per head), in
 // range order: out = sum_r e_r a_r / sum_r e_r l_r with e_r = exp(m_r - max m).
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_merge_kernel(const float* __restrict__ part,
@@ -401,10 +626,21 @@ namespace {
 constexpr int kMinSplitRows = 64;
 }  // namespace
 
-AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t head_dim, int cu_count) {
-  AttnSplit p{1, (int)pos, 512, 2, 0};
+AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, int cu_count) {
+  AttnSplit p{1, (int)pos, 512, 2, 1, 0};
   if (!chunk_tpr(head_dim)) return p;
-  const int64_t want = (std::max(cu_count, 1) + n_q - 1) / n_q;
+  // grouped-query heads (4 or 8 per KV head) on long caches: one workgroup
+  // per KV head serves its G query heads, about two workgroups per CU.
+  // Measured (hd 128, 256 CUs): 32 heads over 8, 2048 / 4096 rows 18.0 / 27.2
+  // -> 15.6 / 19.5 us; 64 over 8, 4096 / 16384 rows 46.0 / 158 -> 27.8 / 64.2;
+  // 32 over 4, 8192 rows 45.9 -> 35.9. Shorter caches and pairs of heads stay
+  // with a workgroup per query head (1024 rows: 10.6 against 14.4; 16 over 8,
+  // 2048 rows: 11.0 against 12.7).
+  const int64_t g = n_q / n_kv;
+  const bool gqa = (g == 4 || g == 8) && g * head_dim <= 1024 && pos >= 2048;
+  if (gqa) p.group = (int)g;
+  const int64_t want = gqa ? (2 * (int64_t)std::max(cu_count, 1) + n_kv - 1) / n_kv
+                           : ((int64_t)std::max(cu_count, 1) + n_q - 1) / n_q;
   const int64_t ns = std::min<int64_t>({want, pos / kMinSplitRows, (int64_t)kMaxSplits});
   if (ns < 4) return p;
   p.nsplit = (int)ns;
@@ -448,11 +684,54 @@ hipError_t launch_chunk_cfg(const float* q, const float* k, const float* v, floa
 
 }  // namespace
 
+namespace {
+
+template <int TPR, int NV, int G>
+hipError_t launch_gqa(const float* q, const float* k, const float* v, float* kcache, float* vcache, int64_t pos,
+                      int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale, float* out,
+                      const AttnSplit& sp, float* part, hipStream_t stream) {
+  const int ns = sp.nsplit;
+  hipLaunchKernelGGL((decode_attention_gqa_kernel<TPR, NV, G>), dim3((unsigned)(n_kv * ns)), dim3(kAttnThreads),
+                     (unsigned)decode_attention_gqa_lds(head_dim, G), stream, q, k, v, kcache, vcache, (int)pos,
+                     (int)n_q, (int)n_kv, (int)head_dim, theta, (float)scale, out, ns, sp.rps, part);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (ns > 1)
+    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3((unsigned)n_q), dim3(kAttnThreads), 0, stream, part, ns,
+                       (int)head_dim, out);
+  return hipGetLastError();
+}
+
+template <int TPR, int NV>
+hipError_t launch_gqa_g(const float* q, const float* k, const float* v, float* kcache, float* vcache, int64_t pos,
+                        int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale, float* out,
+                        const AttnSplit& sp, float* part, hipStream_t stream) {
+#define RQ_GQA_ARGS q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp, part, stream
+  if (sp.group == 2) return launch_gqa<TPR, NV, 2>(RQ_GQA_ARGS);
+  if (sp.group == 4) return launch_gqa<TPR, NV, 4>(RQ_GQA_ARGS);
+  return launch_gqa<TPR, NV, 8>(RQ_GQA_ARGS);
+#undef RQ_GQA_ARGS
+}
+
+}  // namespace
+
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
                                    double scale, float* out, const AttnSplit& sp, void* scratch, hipStream_t stream) {
   float* part = static_cast<float*>(scratch);
 #define RQ_ATTN_ARGS q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp, part, stream
+  if (sp.group > 1) {
+    switch (chunk_tpr(head_dim)) {
+      case 16:
+        return launch_gqa_g<16, 1>(RQ_ATTN_ARGS);
+      case 32:
+        return launch_gqa_g<32, 1>(RQ_ATTN_ARGS);
+      case 64:
+        if (head_dim <= 256) return launch_gqa_g<64, 1>(RQ_ATTN_ARGS);
+        return launch_gqa_g<64, 2>(RQ_ATTN_ARGS);
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
   switch (chunk_tpr(head_dim)) {
     case 16:
       return launch_chunk_cfg<16, 1, 2, 8>(RQ_ATTN_ARGS);

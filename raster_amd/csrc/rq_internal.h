@@ -192,9 +192,10 @@ struct AttnSplit {
   int nsplit, rps;
   int threads;  // workgroup size of the chunk kernel: 256, 512 or 1024
   int np;       // rows per lane per chunk at 256 threads (2, or the larger default)
+  int group;    // > 1: the grouped-query kernel, a workgroup per KV head serving this many query heads
   size_t scratch_bytes;
 };
-AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t head_dim, int cu_count);
+AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, int cu_count);
 hipError_t launch_decode_attention(const float* q, const float* k, const float* v, float* kcache, float* vcache,
                                    int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta,
                                    double scale, float* out, const AttnSplit& sp, void* scratch, hipStream_t stream);

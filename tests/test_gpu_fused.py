@@ -198,7 +198,8 @@ def test_fused_rejects_bad_options(torch, ctx):
 @pytest.mark.parametrize("n_q,n_kv,hd,pos", [
     (16, 16, 128, 128), (8, 2, 64, 9), (32, 8, 128, 1000), (4, 4, 64, 0), (4, 1, 256, 5), (2, 2, 320, 3),
     (8, 8, 128, 20000), (4, 2, 128, 63), (4, 2, 128, 64), (4, 2, 128, 65), (6, 3, 96, 200), (2, 1, 512, 70),
-    (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000), (2, 1, 512, 2000), (4, 2, 96, 4100)])
+    (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000), (2, 1, 512, 2000), (4, 2, 96, 4100),
+    (32, 8, 128, 2048), (16, 2, 128, 3000), (8, 2, 64, 5000), (16, 4, 256, 2100), (8, 1, 16, 2500)])
 def test_decode_attention(torch, ctx, orc, n_q, n_kv, hd, pos):
     # head_dim a multiple of 4 up to 512 runs the chunk kernel (chunks of 64
     # rows at hd 128: pos 63 / 64 / 65 end inside, at and past a chunk;
@@ -206,7 +207,10 @@ def test_decode_attention(torch, ctx, orc, n_q, n_kv, hd, pos):
     # ranges per head, merged by a second kernel ((.., 1000), (.., 20000),
     # (4, 4, 16, 300), (2, 1, 512, 2000), (4, 2, 96, 4100): ragged last
     # range); 66 and 18 run the generic kernel ((3, 3, 66, 30000): scores
-    # beyond 64 KB of LDS). (.., 0): only the new key
+    # beyond 64 KB of LDS). (.., 0): only the new key. From 2048 rows, 4 or 8
+    # query heads per KV head take the grouped-query kernel (a workgroup per KV
+    # head and range): (32, 8, 128, 2048), (16, 2, 128, 3000), (8, 2, 64, 5000),
+    # (16, 4, 256, 2100), (8, 1, 16, 2500)
     import raster_amd
 
     kvd = n_kv * hd
@@ -258,7 +262,8 @@ def test_decode_attention_rejects_bad_shapes(torch, ctx):
     assert e.value.status == RQ_ERR_SHAPE
 
 
-@pytest.mark.parametrize("n_q,n_kv,hd,pos", [(16, 16, 128, 512), (32, 8, 128, 1000), (4, 4, 16, 300)])
+@pytest.mark.parametrize("n_q,n_kv,hd,pos", [(16, 16, 128, 512), (32, 8, 128, 1000), (4, 4, 16, 300),
+                                             (64, 8, 128, 4096)])
 def test_decode_attention_split_repeats_and_graph(torch, ctx, orc, n_q, n_kv, hd, pos):
     # shapes that split the cached rows over several workgroups per head: the
     # per-head counters must be zero again after every call, so repeated calls,
