@@ -624,10 +624,11 @@ size_t decode_attention_lds(int64_t pos, int64_t head_dim) {
 // 8 us, 2048 rows 49 -> 11 us, 8192 rows 180 -> 28 us).
 namespace {
 constexpr int kMinSplitRows = 64;
+constexpr int kAttnThreads1 = 512;  // threads of the single-range workgroup
 }  // namespace
 
 AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, int cu_count) {
-  AttnSplit p{1, (int)pos, 512, 2, 1, 0};
+  AttnSplit p{1, (int)pos, kAttnThreads1, 2, 1, 0};
   if (!chunk_tpr(head_dim)) return p;
   // grouped-query heads (4 or 8 per KV head) on long caches: one workgroup
   // per KV head serves its G query heads, about two workgroups per CU.
@@ -642,7 +643,14 @@ AttnSplit plan_decode_attention(int64_t pos, int64_t n_q, int64_t n_kv, int64_t 
   const int64_t want = gqa ? (2 * (int64_t)std::max(cu_count, 1) + n_kv - 1) / n_kv
                            : ((int64_t)std::max(cu_count, 1) + n_q - 1) / n_q;
   const int64_t ns = std::min<int64_t>({want, pos / kMinSplitRows, (int64_t)kMaxSplits});
-  if (ns < 4) return p;
+  if (ns < 4) {
+    // one range per head: beyond two chunks of 2 rows per lane, 8 rows per
+    // lane keep more of the cache in flight (16 heads, hd 128, graph
+    // replays: 128 rows 6.9 -> 6.2 us, 255 rows 9.3 -> 8.1; at two chunks
+    // or fewer the larger chunk is slower: 64 rows 5.5 against 6.0)
+    if (pos > 2 * (kAttnThreads1 / 64) * (64 / chunk_tpr(head_dim)) * 2) p.np = 8;
+    return p;
+  }
   p.nsplit = (int)ns;
   p.rps = (int)((pos + ns - 1) / ns);
   p.threads = 256;
@@ -676,7 +684,8 @@ hipError_t launch_chunk_cfg(const float* q, const float* k, const float* v, floa
                             const AttnSplit& sp, float* part, hipStream_t stream) {
 #define RQ_ATTN_ARGS q, k, v, kcache, vcache, pos, n_q, n_kv, head_dim, theta, scale, out, sp, part, stream
   if (sp.threads == 1024) return launch_chunk<TPR, NV, NPS, 1024>(RQ_ATTN_ARGS);
-  if (sp.threads == 512) return launch_chunk<TPR, NV, NPS, 512>(RQ_ATTN_ARGS);
+  if (sp.threads == 512)
+    return sp.np == NPS ? launch_chunk<TPR, NV, NPS, 512>(RQ_ATTN_ARGS) : launch_chunk<TPR, NV, NPL, 512>(RQ_ATTN_ARGS);
   if (sp.np == NPS) return launch_chunk<TPR, NV, NPS, 256>(RQ_ATTN_ARGS);
   return launch_chunk<TPR, NV, NPL, 256>(RQ_ATTN_ARGS);
 #undef RQ_ATTN_ARGS

@@ -215,6 +215,15 @@ hipError_t launch_chunk_weight(int format, int scale_dtype, const uint8_t* q_rm,
 
 // ---- device helpers shared by every kernel that decodes weights -----------
 
+// A pointer read from a by-value argument struct is generic to the compiler,
+// so loads through it become flat loads; a flat load also counts against the
+// LDS wait counter, and any LDS wait after it then waits for memory. This
+// marks such a pointer as one into global memory.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 // Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).

@@ -199,11 +199,15 @@ def test_fused_rejects_bad_options(torch, ctx):
     (16, 16, 128, 128), (8, 2, 64, 9), (32, 8, 128, 1000), (4, 4, 64, 0), (4, 1, 256, 5), (2, 2, 320, 3),
     (8, 8, 128, 20000), (4, 2, 128, 63), (4, 2, 128, 64), (4, 2, 128, 65), (6, 3, 96, 200), (2, 1, 512, 70),
     (4, 4, 16, 300), (4, 2, 66, 7), (2, 1, 18, 300), (3, 3, 66, 30000), (2, 1, 512, 2000), (4, 2, 96, 4100),
-    (32, 8, 128, 2048), (16, 2, 128, 3000), (8, 2, 64, 5000), (16, 4, 256, 2100), (8, 1, 16, 2500)])
+    (32, 8, 128, 2048), (16, 2, 128, 3000), (8, 2, 64, 5000), (16, 4, 256, 2100), (8, 1, 16, 2500),
+    (8, 2, 64, 200), (4, 1, 256, 100), (4, 4, 16, 129)])
 def test_decode_attention(torch, ctx, orc, n_q, n_kv, hd, pos):
     # head_dim a multiple of 4 up to 512 runs the chunk kernel (chunks of 64
     # rows at hd 128: pos 63 / 64 / 65 end inside, at and past a chunk;
-    # hd 96 / 320 leave lanes idle); from 256 cached rows the rows split into
+    # hd 96 / 320 leave lanes idle); a single range longer than two chunks of
+    # 2 rows per lane takes 8 (4 at hd > 256) rows per lane: (16, 16, 128, 128),
+    # (4, 2, 128, 65), (6, 3, 96, 200), (2, 1, 512, 70), (8, 2, 64, 200),
+    # (4, 1, 256, 100), (4, 4, 16, 129); from 256 cached rows the rows split into
     # ranges per head, merged by a second kernel ((.., 1000), (.., 20000),
     # (4, 4, 16, 300), (2, 1, 512, 2000), (4, 2, 96, 4100): ragged last
     # range); 66 and 18 run the generic kernel ((3, 3, 66, 30000): scores
