@@ -270,10 +270,32 @@ class ReadCeiling:
         return self.cache[nbytes]
 
 
+def path_numerics(fmt, m, k, n, xdt):
+    """The kernel a plain rq_qmatmul call of this shape runs and how it
+    carries the activations, as include/rq.h ("Kernel by call", "Numerics")
+    states the dispatch."""
+    fixed = ("16-bit block fixed point (per 32-block exponent e, X = rint(x 2^(15-e)), |x - X 2^(e-15)| <= "
+             "2^(e-16)), exact integer dots, block scales in f32")
+    if xdt == "i8":
+        kern = "v_dot4_i32_i8 GEMV" if (m == 1 and fmt == "q4") else "int8-level decode kernel"
+        return kern + ": int8 activation codes with f32 block scales (quantize-act-i8), exact integer dots"
+    if m == 1 and fmt == "q4":
+        return "v_dot4_i32_i8 GEMV: " + fixed
+    if m <= 16 and ((fmt == "q4" and m >= 5) or (fmt == "q8" and m >= 9 and n * k <= (1 << 25))):
+        split = "f32 x as two bf16 terms (|x - hi - lo| <= 2^-17 |x|)" if xdt == "f32" else "bf16 x as is"
+        return "MFMA decode: exact codes on bf16 MFMA, " + split + ", block scales in f32"
+    if m <= 16:
+        return "int8-level decode kernel (int8 MFMA on the raw codes): " + fixed
+    if xdt == "bf16":
+        return "bf16 MFMA GEMM: weights dequantized to bf16 (exact f32 scale * code, one RNE rounding)"
+    return "f32 GEMM: exact codes on bf16 MFMA, f32 x as two bf16 terms, block scales in f32"
+
+
 def hbm_line(torch, ctx, name, weights_cold, weights_warm, m, xdt, ydt, ceiling=None):
     """Cold (rotating copies) and warm numbers for an HBM-bound shape."""
     w = weights_cold
-    out = {"workload": name, "fmt": w.fmt, "m": m, "k": w.k, "n": w.n, "x": xdt, "y": ydt}
+    out = {"workload": name, "fmt": w.fmt, "m": m, "k": w.k, "n": w.n, "x": xdt, "y": ydt,
+           "numerics": path_numerics(w.fmt, m, w.k, w.n, xdt)}
     warm = Case(torch, ctx, weights_warm, m, xdt, ydt)
     warm_ms, warm_cv = time_graph(torch, warm.step)
     cold = Case(torch, ctx, w, m, xdt, ydt)
@@ -857,7 +879,7 @@ def main():
                                    "kernel_avg_us": gv["kernel_us"], "per_call_us": gv["per_call_us"],
                                    "frac_per_call": gv["frac_hbm_per_call"],
                                    "read_ceiling_kernel_us": gv["read_ceiling_kernel_us"],
-                                   "frac_read_ceiling": gv["frac_read_ceiling"]}
+                                   "frac_read_ceiling": gv["frac_read_ceiling"], "numerics": gv["numerics"]}
         log(f"C1: kernel {gv['kernel_us']} us = {gv['GBs']} GB/s ({gv['frac_hbm']:.3f} of HBM, "
             f"{gv['frac_read_ceiling']:.3f} of the read ceiling); per call {gv['per_call_us']} us")
 
