@@ -24,6 +24,9 @@ the C1 GEMV and the CPU baseline):
                 rows of the path), as before.
   dx            backward-data (qlinear-q8-dx) of the C2 layer's weight at
                 m = 16 and 512 dy rows (the MFMA GEMM path).
+  dense         Raster's dense f32 surface (nn/linear, dgemm!) through
+                rq_linear / rq_sgemm: the C2 layer's shape in f32 and 4096^3,
+                against the f32 MFMA peak (157.3 TFLOP/s).
   roofline      the C2 GEMM kernel against dense bf16 MFMA peak (below).
   roofline_gemv the C1 decode kernel against HBM peak (below).
   cpu_baseline  Raster's CPU routes restated in C (oracle/cpu_baseline.c),
@@ -79,6 +82,7 @@ METRIC = "qmatmul GEMV GB/s (% of HBM peak) at M=1; GEMM TFLOPS (% MFMA) at M=51
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0
+FP32_PEAK_TFLOPS = 157.3  # dense f32 MFMA
 RAMP_S = 0.2  # seconds of untimed headline steps that bring an idle GPU to its working clocks
 MALL_BYTES = 256 << 20
 PROFILES = os.path.join(ROOT, "profiles")
@@ -395,6 +399,42 @@ def dense_library_line(torch, M=512, K=4096, N=11008, warmup=200, calls=500):
     return {"what": f"torch.matmul bf16 x[{M},{K}] @ W[{N},{K}]^T (hipBLASLt), dense bf16 weight",
             "us_per_call": round(us, 3), "tflops": round(tflops, 3),
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+
+def dense_lines(torch, ctx, warmup=20, calls=100):
+    """Raster's dense f32 surface (nn/linear -> blas/dgemm-nt! float arm) on
+    the device through rq_linear: y = x W^T + b at the C2 layer's shape in
+    f32 (x [512, 4096], W [11008, 4096]), and rq_sgemm (dgemm!, C = A B) at
+    4096^3, each timed back to back with events on torch's stream. The
+    product is rocBLAS's f32 GEMM, so `frac` is against the f32 MFMA peak."""
+    from raster_amd import dense
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    out = {}
+    for name, (M, K, N) in (("linear_f32_C2_shape", (512, 4096, 11008)), ("sgemm_f32_4096", (4096, 4096, 4096))):
+        a = torch.randn(M * K, device="cuda", generator=g)
+        b = torch.randn(K * N, device="cuda", generator=g)
+        bias = torch.randn(N, device="cuda", generator=g)
+        y = torch.empty(M * N, device="cuda")
+        if name.startswith("linear"):
+            step = lambda: dense.linear_(a, b, bias, y, M, K, N, ctx)  # noqa: E731
+        else:
+            step = lambda: dense.dgemm(a, b, y, M, K, N, 1.0, 0.0, ctx)  # noqa: E731
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(calls):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / calls * 1e3
+        tf = 2.0 * M * K * N / us / 1e6
+        out[name] = {"m": M, "k": K, "n": N, "us_per_call": round(us, 3), "tflops": round(tf, 2),
+                     "frac_fp32_mfma": round(tf / FP32_PEAK_TFLOPS, 4)}
+        del a, b, bias, y
+    return out
 
 
 def dx_lines(torch, ctx, calls=20):
@@ -896,6 +936,8 @@ def main():
         result["dx"] = dx_lines(torch, ctx)
         log("K-quant GEMV")
         result["kquant"] = kquant_lines(torch, ctx)
+        log("dense f32 GEMM (nn/linear, dgemm!)")
+        result["dense"] = dense_lines(torch, ctx)
     elif not args.only_gemm:
         result["read_ceiling"] = sorted(ceiling.cache.values(), key=lambda d: d["bytes"])
 

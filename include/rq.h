@@ -414,6 +414,30 @@ int rq_quantize_weight_q6k(rq_ctx ctx, const float* W, int64_t out, int64_t in, 
 int rq_qlinear_i8(rq_ctx ctx, const float* x, const uint8_t* wqi, const float* wsi, int nibble, float* y,
                   int64_t in, int64_t out);
 
+/* Dense f32 GEMM, the float arms of raster/linalg/blas.clj (Raster's CPU
+ * path hands them to cblas_sgemm of MKL / OpenBLAS), on device arrays,
+ * row-major, asynchronous on `stream`; a plain library GEMM, so rocBLAS
+ * computes it (f32 products and accumulation, deterministic). As in the
+ * reference, a call with m, n or k not positive does nothing.
+ *   rq_sgemm     C[m*n] = alpha A[m*k] B[k*n] + beta C     dgemm!    blas.clj:287-302
+ *   rq_sgemm_tn  C[m*n] = alpha A^T B + beta C, A [k*m]     dgemm-tn! blas.clj:304-319
+ *   rq_sgemm_nt  C[m*n] = alpha A B^T + beta C, B [n*k]     dgemm-nt! blas.clj:321-337
+ * The first call on a context creates its library handle (device memory):
+ * make it outside HIP graph capture. */
+int rq_sgemm(rq_ctx ctx, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+             float beta, void* stream);
+int rq_sgemm_tn(rq_ctx ctx, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+                float beta, void* stream);
+int rq_sgemm_nt(rq_ctx ctx, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+                float beta, void* stream);
+
+/* linear! (raster/dl/nn.clj:161-183): y[batch*out_f] = x[batch*in_f]
+ * W[out_f*in_f]^T + b[out_f], device arrays, as the reference computes it:
+ * every row of y set to b, then rq_sgemm_nt with alpha = beta = 1. batch or
+ * out_f not positive: nothing; in_f not positive: y = b in every row. */
+int rq_linear(rq_ctx ctx, const float* x, const float* w, const float* b, float* y, int64_t batch, int64_t in_f,
+              int64_t out_f, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,8 @@ def _declare(L):
         "rqo_qmatmul_i8_gemm": ([p, p, p, p, p, i64, i64, i64], None),
         "rqo_i8gemv_dp4a": ([p, p, p, i64, i64], None),
         "rqo_dense_matmul_nt_f64": ([p, p, i64, i64, i64, p], None),
+        "rqo_sgemm": ([C.c_int, C.c_int, i64, i64, i64, C.c_float, p, p, C.c_float, p], None),
+        "rqo_linear": ([p, p, p, p, i64, i64, i64], None),
         "rqo_quantize_weight_q4k": ([p, i64, p, p, p, p, p], None),
         "rqo_nextpad": ([i64], C.c_int64),
         "rqo_q4k_of": ([p, i64, i64, p, p, p, p, p], C.c_int64),
@@ -353,6 +355,22 @@ def dense_matmul_nt_f64(X, W, m: int, in_: int, out: int) -> np.ndarray:
     X, W = _c(X, np.float32), _c(W, np.float32)
     y = np.empty(m * out, np.float64)
     lib().rqo_dense_matmul_nt_f64(_ptr(X), _ptr(W), m, in_, out, _ptr(y))
+    return y
+
+
+def sgemm(trans_a: bool, trans_b: bool, A, B, Cm, m: int, k: int, n: int, alpha: float, beta: float) -> np.ndarray:
+    """dgemm! / dgemm-tn! / dgemm-nt! float arm (rqo_sgemm): a new C."""
+    A, B = _c(A, np.float32), _c(B, np.float32)
+    out = _c(Cm, np.float32).copy()
+    lib().rqo_sgemm(int(trans_a), int(trans_b), m, k, n, alpha, _ptr(A), _ptr(B), beta, _ptr(out))
+    return out
+
+
+def linear(x, W, b, batch: int, in_: int, out: int) -> np.ndarray:
+    """nn/linear (rqo_linear): y[batch*out]."""
+    x, W, b = _c(x, np.float32), _c(W, np.float32), _c(b, np.float32)
+    y = np.zeros(max(batch, 0) * max(out, 0), np.float32)
+    lib().rqo_linear(_ptr(x), _ptr(W), _ptr(b), _ptr(y), batch, in_, out)
     return y
 
 

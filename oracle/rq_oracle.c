@@ -787,6 +787,40 @@ void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t 
 }
 
 /* ------------------------------------------------------------------------- */
+/* dense f32 GEMM surface: the float arms of raster/linalg/blas.clj, nn/linear */
+/* ------------------------------------------------------------------------- */
+/* dgemm! / dgemm-tn! / dgemm-nt! (raster/linalg/blas.clj:287-337): the
+ * cblas_sgemm call C = alpha op(A) op(B) + beta C, row-major; op(A) = A^T
+ * (A stored [k x m]) when trans_a, op(B) = B^T (B stored [n x k]) when
+ * trans_b. The products are summed in double and each element rounded to f32
+ * once (a BLAS sums in f32 in an order of its own; this is the value its
+ * error is measured from). m, n or k not positive: nothing (blas.clj:301,
+ * 318, 334). */
+void rqo_sgemm(int trans_a, int trans_b, int64_t m, int64_t k, int64_t n, float alpha, const float* A,
+               const float* B, float beta, float* C) {
+  if (m <= 0 || n <= 0 || k <= 0) return;
+  for (int64_t i = 0; i < m; i++)
+    for (int64_t j = 0; j < n; j++) {
+      double s = 0.0;
+      for (int64_t p = 0; p < k; p++) {
+        const double a = trans_a ? A[p * m + i] : A[i * k + p];
+        const double b = trans_b ? B[j * k + p] : B[p * n + j];
+        s += a * b;
+      }
+      C[i * n + j] = (float)((double)alpha * s + (double)beta * (double)C[i * n + j]);
+    }
+}
+
+/* linear! (raster/dl/nn.clj:161-183): every row of y set to b, then
+ * dgemm-nt! x W y with alpha = beta = 1. */
+void rqo_linear(const float* x, const float* W, const float* b, float* y, int64_t batch, int64_t in, int64_t out) {
+  if (batch <= 0 || out <= 0) return;
+  for (int64_t r = 0; r < batch; r++)
+    for (int64_t o = 0; o < out; o++) y[r * out + o] = b[o];
+  rqo_sgemm(0, 1, batch, in, out, 1.0f, x, W, 1.0f, y);
+}
+
+/* ------------------------------------------------------------------------- */
 /* decoder-step glue (the host ops around the quantized linears)             */
 /* ------------------------------------------------------------------------- */
 /* rms-norm!: raster/dl/nn.clj:497-516. Row mean of squares in double, one

@@ -185,6 +185,10 @@ void rqo_qmatmul_q6k(const int8_t* xq, const float* xs, const int32_t* bsums, co
                      const float* ds, int64_t m, int64_t in, int64_t out, float* y);
 
 /* ---- dense helpers (brute force, f64) used to pin the restatements ---- */
+/* dense f32 GEMM surface (blas.clj float arms, nn/linear) */
+void rqo_sgemm(int trans_a, int trans_b, int64_t m, int64_t k, int64_t n, float alpha, const float* A,
+               const float* B, float beta, float* C);
+void rqo_linear(const float* x, const float* W, const float* b, float* y, int64_t batch, int64_t in, int64_t out);
 void rqo_dense_matmul_nt_f64(const float* X, const float* W, int64_t m, int64_t in, int64_t out,
                              double* y);
 

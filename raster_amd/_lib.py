@@ -61,6 +61,10 @@ SIGNATURES = {
     "rq_q4k_of": ([_p, _p, _i64, _i64, _p, _p, _p, _p, _p, C.POINTER(_i64), _p], _i),
     "rq_quantize_weight_q6k": ([_p, _p, _i64, _i64, _p, _p, _p, _p], _i),
     "rq_stream_read": ([_p, _p, _sz, _i, _p, _p], _i),
+    "rq_sgemm": ([_p, _p, _p, _p, _i64, _i64, _i64, C.c_float, C.c_float, _p], _i),
+    "rq_sgemm_tn": ([_p, _p, _p, _p, _i64, _i64, _i64, C.c_float, C.c_float, _p], _i),
+    "rq_sgemm_nt": ([_p, _p, _p, _p, _i64, _i64, _i64, C.c_float, C.c_float, _p], _i),
+    "rq_linear": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i),
 }
 
 

@@ -33,6 +33,8 @@ FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
 ]
+# the dense f32 GEMM entries call rocBLAS (dense.hip)
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def hipcc() -> str:
@@ -78,7 +80,7 @@ def build(verbose: bool = False, force: bool = False, jobs: int | None = None) -
         raise RuntimeError("librq build failed:\n" + "\n\n".join(failed))
     if todo or force or not os.path.exists(LIB):
         tmp = LIB + ".tmp"
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for _, o in pairs]]
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for _, o in pairs], *LINK_LIBS]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError("librq link failed:\n" + r.stderr)

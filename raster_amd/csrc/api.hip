@@ -45,6 +45,10 @@ struct Ctx {
     size_t attn_bytes = 0;
   };
   std::unordered_map<hipStream_t, StreamScratch> scratch;
+  // rocBLAS handle of the dense f32 GEMM entries, created on first use; the
+  // mutex covers setting its stream and enqueueing one call
+  void* blas = nullptr;
+  std::mutex blas_mu;
   // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
   // end timestamps of each rq_qmatmul's main kernel, waiting to be read, and a
   // pool of spares.
@@ -365,6 +369,7 @@ int rq_ctx_destroy(rq_ctx h) {
     (void)hipFree(kv.second.attn);
   }
   timing_release(c);
+  dense_destroy(c->blas);
   c->magic = 0;
   g_ctxs.erase(c);
   delete c;
@@ -1180,6 +1185,70 @@ int rq_qlinear_q8_dx(rq_ctx h, const float* dy, const int8_t* codes, const float
   rq_weight_destroy(w);
   if (s) t_err = keep;
   return s;
+}
+
+}  // extern "C"
+
+// ---- dense f32 GEMM (Raster's blas/dgemm! float arms and nn/linear!)
+
+namespace rq {
+
+// C[m x n] = alpha op(A) op(B) + beta C through the context's rocBLAS handle.
+// Like Raster's arms (blas.clj:301, 318, 334), a call with m, n or k not
+// positive does nothing.
+static int dense_call(rq_ctx h, int trans_a, int trans_b, const float* a, const float* b, float* c, int64_t m,
+                      int64_t k, int64_t n, float alpha, float beta, void* stream) {
+  Ctx* ctx = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(ctx)) return s;
+  if (m <= 0 || n <= 0 || k <= 0) return RQ_OK;
+  if (!a || !b || !c) return fail(RQ_ERR_NULL, "NULL argument");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return fail(RQ_ERR_SHAPE, "dimension above 2^31 - 1");
+  if (int s = set_device(ctx)) return s;
+  std::lock_guard<std::mutex> lk(ctx->blas_mu);
+  if (!ctx->blas) {
+    if (capturing((hipStream_t)stream))
+      return fail(RQ_ERR_SHAPE, "the dense GEMM's library handle is created on the first call, which cannot be "
+                                "under HIP graph capture: make one call on any stream before capturing");
+    void* hb = nullptr;
+    if (int st = dense_create(&hb))
+      return fail(RQ_ERR_HIP, std::string("rocblas_create_handle: ") + dense_status_string(st));
+    ctx->blas = hb;
+  }
+  if (int st = dense_sgemm(ctx->blas, (hipStream_t)stream, trans_a, trans_b, m, n, k, alpha, a, b, beta, c))
+    return fail(RQ_ERR_HIP, std::string("rocblas_sgemm: ") + dense_status_string(st));
+  return RQ_OK;
+}
+
+}  // namespace rq
+
+extern "C" {
+
+int rq_sgemm(rq_ctx h, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+             float beta, void* stream) {
+  return dense_call(h, 0, 0, a, b, c, m, k, n, alpha, beta, stream);
+}
+
+int rq_sgemm_tn(rq_ctx h, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+                float beta, void* stream) {
+  return dense_call(h, 1, 0, a, b, c, m, k, n, alpha, beta, stream);
+}
+
+int rq_sgemm_nt(rq_ctx h, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
+                float beta, void* stream) {
+  return dense_call(h, 0, 1, a, b, c, m, k, n, alpha, beta, stream);
+}
+
+int rq_linear(rq_ctx h, const float* x, const float* w, const float* b, float* y, int64_t batch, int64_t in_f,
+              int64_t out_f, void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (batch <= 0 || out_f <= 0) return RQ_OK;
+  if (!b || !y || (in_f > 0 && (!x || !w))) return fail(RQ_ERR_NULL, "NULL argument");
+  if (batch > INT32_MAX || out_f > INT32_MAX || in_f > INT32_MAX) return fail(RQ_ERR_SHAPE, "dimension above 2^31 - 1");
+  if (int s = set_device(c)) return s;
+  // y = b in every row, then y = 1 x W^T + 1 y (nn.clj:166-173)
+  if (hipError_t e = launch_bias_rows(b, y, batch, out_f, (hipStream_t)stream)) return hip_fail(e, "bias launch");
+  return dense_call(h, 0, 1, x, w, y, batch, in_f, out_f, 1.0f, 1.0f, stream);
 }
 
 }  // extern "C"

@@ -129,6 +129,18 @@ DecodePlan plan_decode(int64_t m, int64_t k, int64_t npad, int cu_count);
 // x, 4 < m <= 16 (Q4_0) or 8 < m <= 16 (Q8_0) (the kernel takes m <= 16).
 // kw x gw waves per workgroup,
 // wd-step weight ring, ks K-slices, gcols workgroup columns per slice.
+// Dense f32 GEMM (dense.hip, rocBLAS): a library handle per context, created
+// on first use. Statuses are rocBLAS's (0 = success).
+int dense_create(void** handle);
+void dense_destroy(void* handle);
+const char* dense_status_string(int st);
+// C[m x n] = alpha op(A) op(B) + beta C, row-major; op(A) = A^T when trans_a
+// (A stored [k x m]), op(B) = B^T when trans_b (B stored [n x k])
+int dense_sgemm(void* handle, hipStream_t stream, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+                float alpha, const float* a, const float* b, float beta, float* c);
+// y[r, :] = b for r < rows
+hipError_t launch_bias_rows(const float* b, float* y, int64_t rows, int64_t cols, hipStream_t stream);
+
 struct MfPlan {
   bool ok;
   int kw, gw, wd, ks, gcols;

@@ -84,6 +84,10 @@ int main() {
   EXPECT(rq_decode_attention(bad_ctx, x.data(), x.data(), x.data(), y.data(), y.data(), 0, 1, 1, 64, 1e4, 0.125,
                              y.data(), nullptr) == RQ_ERR_HANDLE);
   EXPECT(rq_stream_read(bad_ctx, junk.data(), 16, 1, nullptr, nullptr) == RQ_ERR_HANDLE);
+  EXPECT(rq_sgemm(bad_ctx, x.data(), x.data(), y.data(), 2, 2, 2, 1.0f, 0.0f, nullptr) == RQ_ERR_HANDLE);
+  EXPECT(rq_sgemm_tn(bad_ctx, x.data(), x.data(), y.data(), 2, 2, 2, 1.0f, 0.0f, nullptr) == RQ_ERR_HANDLE);
+  EXPECT(rq_sgemm_nt(nullptr, x.data(), x.data(), y.data(), 0, 0, 0, 1.0f, 0.0f, nullptr) == RQ_ERR_HANDLE);
+  EXPECT(rq_linear(bad_ctx, x.data(), x.data(), x.data(), y.data(), 2, 2, 2, nullptr) == RQ_ERR_HANDLE);
 
   // the error message is per thread: a failure in one thread leaves another's message alone
   EXPECT(rq_ctx_destroy(nullptr) == RQ_ERR_HANDLE);

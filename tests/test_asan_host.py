@@ -38,7 +38,8 @@ def asan_build(tmp_path_factory):
     lib = str(d / "librq_asan.so")
     r = subprocess.run([rqb.hipcc(), f"--offload-arch={rqb.ARCH}", "-shared", "-fPIC", "-Xarch_host",
                         "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-shared-libasan", "-o", lib,
-                        api_o, *[os.path.join(rqb.OBJ, o) for o in objs]], capture_output=True, text=True)
+                        api_o, *[os.path.join(rqb.OBJ, o) for o in objs], *rqb.LINK_LIBS],
+                       capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-4000:]
     drv = str(d / "driver")
     r = subprocess.run([CLANG, "-std=c++17", "-g", "-O1", "-fsanitize=address,undefined", "-shared-libasan",

@@ -721,3 +721,57 @@ def test_cpu_baseline_qlinear_matches_the_oracle(orc):
     y = np.empty(m * out, np.float32)
     L.rqb_qlinear_q8(ptr(x), ptr(codes), ptr(scales), m, in_, out, ptr(y), 4)
     assert orc.normwise_relerr(y, orc.qlinear_q8(x, codes, scales, m, in_, out)) < 1e-6
+
+
+# ---------------------------------------------------------------- dense f32 GEMM (blas.clj float arms, nn/linear)
+def test_sgemm_reference_known_answers(orc):
+    # test/raster/linalg/blas_test.clj:11-77: dgemm! identity, basic, alpha-beta,
+    # dgemm-tn!, dgemm-nt! (integers, exact in f32)
+    f = lambda v: np.array(v, np.float32)  # noqa: E731
+    assert list(orc.sgemm(False, False, f([1, 0, 0, 1]), f([5, 6, 7, 8]), f([0] * 4), 2, 2, 2, 1.0, 0.0)) == [5, 6, 7, 8]
+    assert list(orc.sgemm(False, False, f([1, 2, 3, 4, 5, 6]), f([7, 8, 9, 10, 11, 12]), f([0] * 4), 2, 3, 2, 1.0,
+                          0.0)) == [58, 64, 139, 154]
+    assert list(orc.sgemm(False, False, f([1, 0, 0, 1]), f([5, 6, 7, 8]), f([10, 20, 30, 40]), 2, 2, 2, 2.0,
+                          3.0)) == [40, 72, 104, 136]
+    assert list(orc.sgemm(True, False, f([1, 4, 2, 5, 3, 6]), f([7, 8, 9, 10, 11, 12]), f([0] * 4), 2, 3, 2, 1.0,
+                          0.0)) == [58, 64, 139, 154]
+    assert list(orc.sgemm(False, True, f([1, 2, 3, 4, 5, 6]), f([7, 9, 11, 8, 10, 12]), f([0] * 4), 2, 3, 2, 1.0,
+                          0.0)) == [58, 64, 139, 154]
+
+
+def test_linear_reference_known_answers(orc):
+    # test/raster/dl/nn_test.clj:93-117: y = x W^T + b
+    y = orc.linear(np.array([1, 2, 3], np.float32), np.array([1, 0, 0, 0, 1, 0], np.float32),
+                   np.array([0.1, 0.2], np.float32), 1, 3, 2)
+    assert list(y) == [np.float32(1) + np.float32(0.1), np.float32(2) + np.float32(0.2)]
+    y = orc.linear(np.arange(1, 7, dtype=np.float32), np.array([1, 0, 0, 0, 1, 0], np.float32),
+                   np.zeros(2, np.float32), 2, 3, 2)
+    assert list(y) == [1, 2, 4, 5]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True)])
+def test_sgemm_against_numpy_f64(orc, ta, tb):
+    # an independent f64 product (numpy), rounded once: a transposed operand,
+    # a wrong leading dimension or a dropped alpha / beta term shows up far
+    # above the f32 rounding of the two
+    rng = np.random.default_rng(7)
+    m, k, n = 7, 13, 5
+    A = rng.standard_normal(m * k).astype(np.float32)
+    B = rng.standard_normal(k * n).astype(np.float32)
+    C0 = rng.standard_normal(m * n).astype(np.float32)
+    Am = A.reshape(k, m).T if ta else A.reshape(m, k)
+    Bm = B.reshape(n, k).T if tb else B.reshape(k, n)
+    want = (0.75 * (Am.astype(np.float64) @ Bm.astype(np.float64)) - 1.5 * C0.reshape(m, n)).astype(np.float32)
+    got = orc.sgemm(ta, tb, A, B, C0, m, k, n, 0.75, -1.5).reshape(m, n)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def test_sgemm_and_linear_degenerate_shapes_do_nothing(orc):
+    # blas.clj:301,318,334 skip the call unless m, n and k are all positive;
+    # nn/linear still writes the bias rows when in_f is 0 (nn.clj:170-171)
+    C0 = np.array([1, 2, 3, 4], np.float32)
+    for m, k, n in ((0, 2, 2), (2, 0, 2), (2, 2, 0)):
+        assert list(orc.sgemm(False, False, np.ones(4, np.float32), np.ones(4, np.float32), C0, m, k, n, 1.0,
+                              0.0)) == [1, 2, 3, 4]
+    y = orc.linear(np.zeros(0, np.float32), np.zeros(0, np.float32), np.array([3, 4], np.float32), 2, 0, 2)
+    assert list(y) == [3, 4, 3, 4]
