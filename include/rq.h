@@ -422,8 +422,9 @@ int rq_qlinear_i8(rq_ctx ctx, const float* x, const uint8_t* wqi, const float* w
  *   rq_sgemm     C[m*n] = alpha A[m*k] B[k*n] + beta C     dgemm!    blas.clj:287-302
  *   rq_sgemm_tn  C[m*n] = alpha A^T B + beta C, A [k*m]     dgemm-tn! blas.clj:304-319
  *   rq_sgemm_nt  C[m*n] = alpha A B^T + beta C, B [n*k]     dgemm-nt! blas.clj:321-337
- * The first call on a context creates its library handle (device memory):
- * make it outside HIP graph capture. */
+ * The first call on a context creates its library handle (device memory)
+ * and fails under HIP graph capture; later calls are not meant for capture
+ * either (the library may allocate or record memory operations there). */
 int rq_sgemm(rq_ctx ctx, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,
              float beta, void* stream);
 int rq_sgemm_tn(rq_ctx ctx, const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n, float alpha,

@@ -369,7 +369,11 @@ int rq_ctx_destroy(rq_ctx h) {
     (void)hipFree(kv.second.attn);
   }
   timing_release(c);
-  dense_destroy(c->blas);
+  {
+    std::lock_guard<std::mutex> bl(c->blas_mu);
+    dense_destroy(c->blas);
+    c->blas = nullptr;
+  }
   c->magic = 0;
   g_ctxs.erase(c);
   delete c;
