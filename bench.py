@@ -60,8 +60,8 @@ accumulation, the arithmetic of the GPU path's reference) on all usable host
 cores (at most 16, the box's share) over a row sample of C2, in TFLOP/s.
 `legs` times B1 and B2 (quantize-act-i8 + the x8 dpbusd GEMV, Raster's
 production int8 route; Q8 and Q4_0 tiles) at 1 thread (Raster's default
-RASTER_DECODE_THREADS) and at all cores, on the C1, C3 and C2 shapes, each
-leg about one second; `cpu_model` names the host CPU.
+RASTER_DECODE_THREADS) and at all cores, on the C1, C3, C2 and C5 (M = 1)
+shapes, each leg about one second; `cpu_model` names the host CPU.
 
 Multi-GPU runs are not part of this build: --gpus above 1 exits with a message.
 """
@@ -745,8 +745,10 @@ def cpu_baseline(leg_s=1.0, head_s=10.0):
         return _timed(one, budget)
 
     legs = []
+    # C5 at M = 1 only: B2 takes one row per call, so its per-row time holds for M = 32 and 256 as well
     shapes = [("C1", "q8", 1, 4096, 4096), ("C3", "q4", 1, 4096, 14336), ("C3", "q4", 4, 4096, 14336),
-              ("C3", "q4", 16, 4096, 14336), ("C2", "q8", 512, 4096, 11008)]
+              ("C3", "q4", 16, 4096, 14336), ("C2", "q8", 512, 4096, 11008), ("C5", "q8", 1, 8192, 28672),
+              ("C5", "q4", 1, 8192, 28672)]
     for cfg, fmt, m, k, n in shapes:
         for threads in (1, cores):
             if fmt == "q8":
