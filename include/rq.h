@@ -160,7 +160,12 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *  - every other m <= 16: the int8-level decode kernel (int8 MFMA on the raw
  *    codes, v_mfma_i32_16x16x64_i8);
  *  - m > 16: bf16 x: the bf16 MFMA GEMM (Q4_0 at 16 < m <= 64: the
- *    weight-stream GEMM); f32 x: the exact-code f32 GEMM.
+ *    weight-stream GEMM); f32 x: the exact-code f32 GEMM;
+ *  - Q4_K / Q6_K weights (f32 x only, any m; bf16 x fails with RQ_ERR_DTYPE):
+ *    x is quantized to q8_K in scratch and the K-quant GEMV runs, the same two
+ *    kernels as rq_quantize_act_q8k + rq_qmatmul_q8k and bit for bit their
+ *    results (QMatrix apply of the built-in :q4_K / :q6_K formats,
+ *    raster/quant/core.clj:55-75).
  *
  * Numerics (all accumulation in f32):
  *  - v_dot4 GEMV and int8-level decode kernel: each 32-block of each
@@ -192,7 +197,9 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    workgroups' LDS, and further until the grid covers about 85% of the CUs,
  *    rounded up to a power of two while each slice keeps 8 blocks (at most
  *    in / 32 slices); Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to
- *    8 slices).
+ *    8 slices);
+ *  - Q4_K / Q6_K: the q8_K activations, m * (in + in/256*4 + in/sub*4)
+ *    bytes (each part rounded up to 256), sub = 32 for Q4_K, 16 for Q6_K.
  * Under HIP graph capture nothing can be allocated: run the same (or a
  * larger) shape once on the capturing stream before capturing, otherwise the
  * call fails with RQ_ERR_SHAPE and a message saying so.
@@ -208,7 +215,8 @@ int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * arguments, kernels and results as rq_qmatmul, bit for bit; no kernel-timing
  * events are recorded. Where rq_qmatmul would use per-stream scratch (the
- * packed activations of the bf16 GEMM, K-slice partial sums) this call uses a
+ * packed activations of the bf16 GEMM, K-slice partial sums, a K-quant
+ * weight's q8_K activations) this call uses a
  * fixed device array of RQ_NOALLOC_SCRATCH_MAX bytes that each GPU holds from
  * the first context created on it until the process ends; a call that needs
  * more fails with RQ_ERR_SHAPE and a message saying so (for example bf16 x
@@ -255,14 +263,17 @@ int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* 
                      const rq_fused_ops* ops, void* stream);
 
 /* K-quant weights from Raster's arrays (Raster's own layout, each row of the
- * [out x in] matrix its own super-blocks, in % 256 == 0; the encoders are
+ * [out x in] matrix its own super-blocks, in % 256 == 0, in <= 32768 for
+ * Q4_K and 32256 for Q6_K (the GEMV stages four activation rows in one
+ * workgroup's LDS), else RQ_ERR_SHAPE; the encoders are
  * quantize-weight-q4k / quantize-weight-q6k, quant.clj:92-137,214-239):
  *  Q4_K: wq u8[out*in/2] nibbles (w[k] low, w[k+16] high per 32-sub-block),
  *        da, db f32[out*in/256], aq u8[out*in/32] (0..63), bq i8[out*in/32];
  *  Q6_K: wq u8[out*in] (0..63), sc i8[out*in/16], ds f32[out*in/256].
  * They take q8_K activations (rq_quantize_act_q8k, rq_qmatmul_q8k); rq_dequant
- * gives dequant-q4k / dequant-q6k bit for bit. rq_qmatmul and its variants
- * reject them with RQ_ERR_DTYPE. */
+ * gives dequant-q4k / dequant-q6k bit for bit. rq_qmatmul and
+ * rq_qmatmul_noalloc take them with f32 x (quantized to q8_K inside the call);
+ * rq_qmatmul_fused and rq_qmatmul_i8 reject them with RQ_ERR_DTYPE. */
 int rq_weight_create_q4k(rq_ctx ctx, const uint8_t* wq, const float* da, const float* db, const uint8_t* aq,
                          const int8_t* bq, int64_t out, int64_t in, rq_weight* w);
 int rq_weight_create_q6k(rq_ctx ctx, const uint8_t* wq, const int8_t* sc, const float* ds, int64_t out, int64_t in,

@@ -635,10 +635,14 @@ static int make_weight_k(Ctx* c, int format, int64_t out, int64_t in, const void
   return RQ_OK;
 }
 
-static int check_shape_k(int64_t out, int64_t in) {
+static int check_shape_k(int format, int64_t out, int64_t in) {
   if (int s = check_shape(out, in)) return s;
   if (in % 256 != 0) return fail(RQ_ERR_SHAPE, "K-quants need in % 256 == 0 (super-blocks of 256)");
-  if (in > (int64_t)1 << 15) return fail(RQ_ERR_SHAPE, "K-quant in above 32768 (activations staged in LDS)");
+  // four activation rows of codes, sub-block sums and scales staged in LDS:
+  // in <= 32768 for Q4_K, 32256 for Q6_K
+  if (in > (int64_t)1 << 15 || kquant_gemv_lds(format, in, 4) > 163840)
+    return fail(RQ_ERR_SHAPE, "K-quant in too large (activations staged in LDS: at most 32768 for Q4_K, "
+                              "32256 for Q6_K)");
   return RQ_OK;
 }
 
@@ -647,7 +651,7 @@ int rq_weight_create_q4k(rq_ctx h, const uint8_t* wq, const float* da, const flo
   Ctx* c = reinterpret_cast<Ctx*>(h);
   if (int s = check_ctx(c)) return s;
   if (!wq || !da || !db || !aq || !bq || !w) return fail(RQ_ERR_NULL, "NULL argument");
-  if (int s = check_shape_k(out, in)) return s;
+  if (int s = check_shape_k(RQ_Q4_K, out, in)) return s;
   const int64_t nsb = out * (in / 256), nsub = out * (in / 32);
   std::vector<float> sup((size_t)(2 * nsb));
   for (int64_t i = 0; i < nsb; i++) {
@@ -665,7 +669,7 @@ int rq_weight_create_q6k(rq_ctx h, const uint8_t* wq, const int8_t* sc, const fl
   Ctx* c = reinterpret_cast<Ctx*>(h);
   if (int s = check_ctx(c)) return s;
   if (!wq || !sc || !ds || !w) return fail(RQ_ERR_NULL, "NULL argument");
-  if (int s = check_shape_k(out, in)) return s;
+  if (int s = check_shape_k(RQ_Q6_K, out, in)) return s;
   return make_weight_k(c, RQ_Q6_K, out, in, wq, (size_t)(out * in), ds, (size_t)(out * (in / 256)) * 4, sc,
                        (size_t)(out * (in / 16)), w);
 }
@@ -740,15 +744,42 @@ static int call_scratch(Ctx* c, FixedScratch* fixed, hipStream_t stream, size_t 
   return s;
 }
 
+// A K-quant weight with f32 x in one call: x quantized to q8_K in scratch,
+// then the K-quant GEMV -- rq_quantize_act_q8k + rq_qmatmul_q8k, with the
+// same kernels and so the same results (QMatrix apply of the built-in :q4_K /
+// :q6_K formats, raster/quant/core.clj:55-75).
+static int run_kquant_matmul(Ctx* c, const Weight& w, const float* x, void* y, int y_dtype, int64_t m,
+                             hipStream_t stream, FixedScratch* fixed) {
+  const int sub = w.format == RQ_Q4_K ? 32 : 16;
+  const size_t xq_b = align256((size_t)m * (size_t)w.in), xs_b = align256((size_t)m * (size_t)(w.in / 256) * 4);
+  const size_t bs_b = (size_t)m * (size_t)(w.in / sub) * 4;
+  void* buf = nullptr;
+  if (int s = call_scratch(c, fixed, stream, xq_b + xs_b + bs_b, 0, &buf)) return s;
+  int8_t* xq = static_cast<int8_t*>(buf);
+  float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(buf) + xq_b);
+  int32_t* bs = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(buf) + xq_b + xs_b);
+  if (int s = set_device(c)) return s;
+  hipError_t e = launch_quantize_act_q8k(x, m, w.in, sub, xq, xs, bs, stream);
+  if (e != hipSuccess) return hip_fail(e, "quantizer launch");
+  const auto ev = fixed ? std::pair<hipEvent_t, hipEvent_t>{nullptr, nullptr} : timing_pair(c, stream);
+  if (ev.first) (void)hipEventRecord(ev.first, stream);
+  e = launch_kquant_gemv(w, xq, xs, bs, y, y_dtype, m, c->cu_count, stream);
+  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, stream);
+  timing_done(c, ev, e == hipSuccess);
+  if (e != hipSuccess) return hip_fail(e, "K-quant GEMV launch");
+  return RQ_OK;
+}
+
 static bool kquant(const Weight& w) { return w.format == RQ_Q4_K || w.format == RQ_Q6_K; }
 static const char* kKquantMsg = "K-quant weights take q8_K activations: use rq_qmatmul_q8k";
+static const char* kKquantX = "K-quant weights take f32 x here (quantized to q8_K in the call), or use rq_qmatmul_q8k";
 
 static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                         const rq_fused_ops* ops, void* stream) {
   Ctx* c;
   Weight w;
   if (int s = lookup(h, wh, &c, &w)) return s;
-  if (kquant(w)) return fail(RQ_ERR_DTYPE, kKquantMsg);
+  if (kquant(w) && ops) return fail(RQ_ERR_DTYPE, "fused options need a Q8_0 or Q4_0 weight");
   if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
   if (m == 0) return RQ_OK;
   if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
@@ -757,6 +788,10 @@ static int qmatmul_impl(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void
   if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
   if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
   if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  if (kquant(w)) {
+    if (x_dtype != RQ_F32) return fail(RQ_ERR_DTYPE, kKquantX);
+    return run_kquant_matmul(c, w, static_cast<const float*>(x), y, y_dtype, m, (hipStream_t)stream, nullptr);
+  }
   const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
   DecodeOps dops = {nullptr, 0.0f, nullptr, 0};
   if (ops) {
@@ -867,7 +902,6 @@ int rq_qmatmul_noalloc(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void*
   Ctx* c;
   Weight w;
   if (int s = lookup(h, wh, &c, &w)) return s;
-  if (kquant(w)) return fail(RQ_ERR_DTYPE, kKquantMsg);
   if (m < 0) return fail(RQ_ERR_SHAPE, "m < 0");
   if (m == 0) return RQ_OK;
   if (m > (int64_t)1 << 24) return fail(RQ_ERR_SHAPE, "m too large");
@@ -876,6 +910,7 @@ int rq_qmatmul_noalloc(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void*
   if (y_dtype != RQ_F32 && y_dtype != RQ_BF16) return fail(RQ_ERR_DTYPE, "y must be f32 or bf16");
   if (((uintptr_t)x & 15) != 0) return fail(RQ_ERR_SHAPE, "x must be 16-byte aligned");
   if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
+  if (kquant(w) && x_dtype != RQ_F32) return fail(RQ_ERR_DTYPE, kKquantX);
   void* ptr;
   {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -883,6 +918,8 @@ int rq_qmatmul_noalloc(rq_ctx h, rq_weight wh, const void* x, int x_dtype, void*
   }
   if (!ptr) return fail(RQ_ERR_HIP, "no device address for the fixed scratch of this device");
   FixedScratch fs = {static_cast<uint8_t*>(ptr), kNoAllocScratchBytes, 0};
+  if (kquant(w))
+    return run_kquant_matmul(c, w, static_cast<const float*>(x), y, y_dtype, m, (hipStream_t)stream, &fs);
   const DecodePlan plan = plan_decode(m, w.in, w.npad, c->cu_count);
   const DecodeOps dops = {nullptr, 0.0f, nullptr, 0, 0, nullptr, nullptr};
   return run_matmul(c, w, plan, x, x_dtype, y, y_dtype, m, dops, (hipStream_t)stream, &fs);

@@ -5,6 +5,8 @@
   rq_qmatmul_q8k       qmatmul-q4k-dp4a! / qmatmul-q6k-dp4a! (raster/quant/kernels_k.clj:186-297):
                        exact integer sub-block dots, scale terms summed in f32 where Raster sums
                        in double: normwise max|y - ref| / max|ref| < 2e-5 (f32 y), 1e-2 (bf16 y)
+  rq_qmatmul (K-quant, f32 x)  the two calls above in one (QMatrix apply, raster/quant/core.clj:55-75):
+                       bit-identical to them, and through them to the oracle's bound
 
 The oracle's restatements are pinned on the CPU (test_oracle.py) by the
 reference's own K-quant tests (test/raster/quant/kernels_k_test.clj), the exact
@@ -126,7 +128,7 @@ def run_gemv(torch, ctx, orc, fmt, m, out, in_, seed, ydt="f32", rows_cap=None):
 
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("m,out,in_", [(1, 4096, 4096), (3, 37, 256), (4, 1000, 5632), (7, 16, 14336),
-                                       (1, 14336, 4096)])
+                                       (1, 14336, 4096), (4, 64, 32256)])
 def test_kquant_gemv(torch, ctx, orc, fmt, m, out, in_):
     note(f"K-quant gemv {fmt} m={m} {out}x{in_}")
     y, ref = run_gemv(torch, ctx, orc, fmt, m, out, in_, seed=out + in_ + m, rows_cap=512)
@@ -160,6 +162,45 @@ def test_kquant_reference_test_on_gpu(torch, ctx, orc, fmt, wseed, xseed):
     assert np.all(np.abs(y - yref) < 1e-2)
 
 
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("m,out,in_,ydt", [(1, 4096, 4096, "f32"), (5, 1000, 5632, "f32"), (33, 256, 2048, "bf16"),
+                                           (2, 14336, 4096, "bf16")])
+def test_kquant_qmatmul_f32_x(torch, ctx, orc, fmt, m, out, in_, ydt):
+    # rq_qmatmul with a K-quant weight and f32 x: the q8_K quantizer and the
+    # K-quant GEMV inside one call, bit for bit the two separate calls; the
+    # allocation-free variant gives the same bits
+    import ctypes as C
+
+    import raster_amd
+    from raster_amd import _lib
+
+    note(f"K-quant rq_qmatmul {fmt} m={m} {out}x{in_} y={ydt}")
+    sub = 32 if fmt == "q4k" else 16
+    arrs = encode(orc, fmt, out, in_, seed=out + m)
+    w = make_weight(raster_amd, ctx, fmt, arrs, out, in_)
+    ytype = torch.bfloat16 if ydt == "bf16" else torch.float32
+    try:
+        x = dev(torch, np.random.default_rng(m).standard_normal(m * in_).astype(np.float32)).reshape(m, in_)
+        y1 = w.matmul(x, out_dtype=ytype)
+        xq, xs, bs = raster_amd.quantize_act_q8k(ctx, x, in_, sub)
+        y2 = w.matmul_q8k(xq, xs, bs, out_dtype=ytype)
+        y3 = torch.full((m, out), float("nan"), dtype=ytype, device="cuda")
+        yc = _lib.RQ_BF16 if ydt == "bf16" else _lib.RQ_F32
+        _lib.call("rq_qmatmul_noalloc", ctx.handle, w.handle, C.c_void_p(x.data_ptr()), _lib.RQ_F32,
+                  C.c_void_p(y3.data_ptr()), yc, m, C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        a, b, c = (t.float().cpu().numpy() for t in (y1, y2, y3))
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+        if ydt == "f32" and out <= 1000:  # and the oracle's bound, end to end
+            ref = oracle_y(orc, fmt, arrs, xq.cpu().numpy().ravel(), xs.cpu().numpy().ravel(),
+                           bs.cpu().numpy().ravel(), m, in_, out)
+            assert orc.normwise_relerr(a, ref) < TOL
+    finally:
+        w.destroy()
+
+
 def test_kquant_rejects(torch, ctx, orc):
     import ctypes as C
 
@@ -170,8 +211,14 @@ def test_kquant_rejects(torch, ctx, orc):
 
     arrs = encode(orc, "q4k", 16, 256, seed=1)
     w = raster_amd.QWeight.q4k(*arrs, 16, 256, ctx)
-    with pytest.raises(RqError) as e:  # f32 activations: the K-quants take q8_K
-        w.matmul(torch.zeros((1, 256), device="cuda"))
+    with pytest.raises(RqError) as e:  # bf16 activations: the K-quants quantize f32 x to q8_K
+        w.matmul(torch.zeros((1, 256), dtype=torch.bfloat16, device="cuda"))
+    assert e.value.status == RQ_ERR_DTYPE
+    with pytest.raises(RqError) as e:  # no fused decoder ops on the K-quant GEMV
+        w.matmul_fused(torch.zeros((1, 256), device="cuda"), residual=torch.zeros((1, 16), device="cuda"))
+    assert e.value.status == RQ_ERR_DTYPE
+    with pytest.raises(RqError) as e:  # nor the int8 blocks of Q8_0 / Q4_0
+        w.matmul_i8(torch.zeros(256, dtype=torch.int8, device="cuda"), torch.zeros(8, device="cuda"))
     assert e.value.status == RQ_ERR_DTYPE
     w.destroy()
     codes, scales = wl.q8_weights(16, 256, seed=1)
@@ -190,4 +237,10 @@ def test_kquant_rejects(torch, ctx, orc):
         call("rq_weight_create_q4k", ctx.handle, z8.ctypes.data_as(C.c_void_p), zf.ctypes.data_as(C.c_void_p),
              zf.ctypes.data_as(C.c_void_p), z8.ctypes.data_as(C.c_void_p), z8.ctypes.data_as(C.c_void_p), 4, 192,
              C.byref(h))
+    assert e.value.status == RQ_ERR_SHAPE
+    # in = 32512: four Q6_K activation rows no longer fit the GEMV's LDS
+    z8, zs, zf = np.zeros(4 * 32512, np.uint8), np.zeros(4 * 32512 // 16, np.int8), np.zeros(4 * 127, np.float32)
+    with pytest.raises(RqError) as e:
+        call("rq_weight_create_q6k", ctx.handle, z8.ctypes.data_as(C.c_void_p), zs.ctypes.data_as(C.c_void_p),
+             zf.ctypes.data_as(C.c_void_p), 4, 32512, C.byref(h))
     assert e.value.status == RQ_ERR_SHAPE

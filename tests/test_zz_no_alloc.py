@@ -1,7 +1,8 @@
 """rq_qmatmul_noalloc, the rq_qmatmul variant that allocates nothing, against
 rq_qmatmul itself through the C ABI: bit-identical outputs on every kernel
 route that uses scratch (K-slice partial sums of the decode kernels, the packed
-activations of the bf16 GEMMs, both for the small-m GEMM) and on routes that
+activations of the bf16 GEMMs, both for the small-m GEMM, a K-quant weight's
+q8_K activations) and on routes that
 use none, two calls in a row with the second one smaller, and a call that needs
 more than the fixed scratch is refused with RQ_ERR_SHAPE.
 """
@@ -39,6 +40,14 @@ def ctx(torch):
 
 
 def weight(raster_amd, ctx, fmt, out, in_, seed):
+    if fmt in ("q4k", "q6k"):
+        rng = np.random.default_rng(seed)
+        W = (rng.standard_normal(out * in_) * 0.05).astype(np.float32)
+        from oracle import oracle as orc
+
+        arrs = orc.quantize_weight_q4k(W) if fmt == "q4k" else orc.quantize_weight_q6k(W)
+        make = raster_amd.QWeight.q4k if fmt == "q4k" else raster_amd.QWeight.q6k
+        return make(*arrs, out, in_, ctx)
     if fmt == "q8":
         codes, scales = wl.q8_weights(out, in_, seed=seed)
         return raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
@@ -73,6 +82,8 @@ CASES = [
     ("q4", 8192, 8192, [64, 32], "bf16", "bf16"),        # small-m GEMM: packed x + K-slices
     ("q8", 11008, 4096, [512, 128], "bf16", "bf16"),     # prefill GEMM: packed x
     ("q8", 1000, 1024, [300, 17], "f32", "f32"),         # exact-f32 GEMM, no scratch
+    ("q4k", 4096, 4096, [8, 1], "f32", "f32"),           # K-quant: q8_K activations in scratch
+    ("q6k", 1024, 2048, [40, 3], "f32", "bf16"),         # K-quant, m above the decode range
 ]
 
 
