@@ -88,37 +88,23 @@ __device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
 // multiple of 16 are zero. Row-major fragment loads hit 16 rows one row
 // stride apart (K*2 bytes, which aliases in L1) and use half of each cache
 // line; from xf every fragment is one contiguous kilobyte.
-// One workgroup moves a 16-row x 512-element region (16 k-blocks, 16 KB):
-// each thread reads four 16-byte pieces (16 threads cover 256 contiguous
-// bytes of a row per round), the tile is transposed through LDS (rows padded
-// to 65 pieces against bank conflicts) and written back as 16 contiguous
-// kilobytes, four pieces per thread.
-constexpr int kPackBlocks = 16;  // k-blocks per pack workgroup
+// A wave copies one fragment: lane l loads its 16 bytes straight from x and
+// stores them at position l, so the wave's store is one contiguous kilobyte;
+// the four waves of a workgroup take four consecutive k-blocks of one 16-row
+// tile (16 rows x 256 contiguous bytes read). At C2 (x 512 x 4096) this
+// measured 2.6 us alone and 1.7 us less per pack + GEMM step than a
+// transposing copy through LDS with four pieces per thread.
+constexpr int kPackBlocks = 4;  // k-blocks per pack workgroup, one per wave
 __global__ __launch_bounds__(256) void pack_x_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xf, int M,
                                                     int K) {
-  __shared__ uint4 t[16 * (4 * kPackBlocks + 1)];
-  constexpr int PR = 4 * kPackBlocks + 1;  // LDS pieces per row
   const int nb = K / 32, nq = (nb + kPackBlocks - 1) / kPackBlocks;
-  const int tile = blockIdx.x / nq, b0 = (blockIdx.x % nq) * kPackBlocks;
-  const int i = threadIdx.x;
-  const int r = i >> 4, pp = i & 15;  // row, piece within a 256-byte round
-  const int m = tile * 16 + r;
-  uint4 v[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int p = pp + 16 * j, b = b0 + (p >> 2);  // piece p of the row's 64
-    v[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (m < M && b < nb) v[j] = *reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * b0 + 8 * p);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) t[r * PR + pp + 16 * j] = v[j];
-  __syncthreads();
-  const int l = i & 63, lr = l & 15, fg = l >> 4;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int bb = (i >> 6) + 4 * j, b = b0 + bb;  // block of this store
-    if (b < nb) *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = t[lr * PR + bb * 4 + fg];
-  }
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tile = blockIdx.x / nq, b = (blockIdx.x % nq) * kPackBlocks + w;
+  if (b >= nb) return;
+  const int m = tile * 16 + (l & 15);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (m < M) v = *reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * b + 8 * (l >> 4));
+  *reinterpret_cast<uint4*>(xf + (((int64_t)tile * nb + b) * 64 + l) * 8) = v;
 }
 
 template <int FMT, typename ST, int MT, int NTW, int WD = 6>
