@@ -105,17 +105,6 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
   float* ls = reinterpret_cast<float*>(smem + MT * K + MT * nsub * 4);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // stage the activations (rows past M as zeros)
-  for (int i = tid; i < MT * K / 16; i += kKqThreads) {
-    const int t = i / (K / 16);
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (t < M) v = reinterpret_cast<const u32x4*>(xq + (int64_t)t * K)[i % (K / 16)];
-    reinterpret_cast<u32x4*>(lx)[i] = v;
-  }
-  for (int i = tid; i < MT * nsub; i += kKqThreads) lb[i] = i / nsub < M ? bsums[(int64_t)i] : 0;
-  for (int i = tid; i < MT * nsb; i += kKqThreads) ls[i] = i / nsb < M ? xs[(int64_t)i] : 0.0f;
-  __syncthreads();
-
   // ---- this wave's work: row groups gi = 0 .. ng-1 (rows o0 = 4 (gw + gi
   // nwaves) ..), each swept in nit steps (lane: sub-block lane + 64 si). The
   // steps stream through a D-step register ring of raw code and scale bits
@@ -128,7 +117,6 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
   const int gw = (int)blockIdx.x * (kKqThreads / 64) + wave, nwaves = (int)gridDim.x * (kKqThreads / 64);
   const int ngrp = (N + kKqRows - 1) / kKqRows;
   const int ng = gw < ngrp ? (ngrp - 1 - gw) / nwaves + 1 : 0;
-  if (ng == 0) return;  // wave-uniform; no barrier follows
   const int nit = (nsub + 63) / 64, nitp = (nit + D - 1) / D * D;
   constexpr int CODE_ROW = FMT == RQ_Q4_K ? 1 : 2;  // K * CODE_ROW / 2 code bytes per row
   struct Slot {
@@ -165,11 +153,28 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
       ++gi;
     }
   };
+  // the first weight loads go out before the activations are staged, so
+  // their latency overlaps the staging (14336 x 4096, m = 1, cold: Q4_K
+  // 11.65 -> 11.19 us; Q6_K unchanged at 16.9)
+  if (ng > 0) {
 #pragma unroll
-  for (int i = 0; i < D; i++) {
-    load(i, lg, ls_);
-    advance(lg, ls_);
+    for (int i = 0; i < D; i++) {
+      load(i, lg, ls_);
+      advance(lg, ls_);
+    }
   }
+
+  // stage the activations (rows past M as zeros)
+  for (int i = tid; i < MT * K / 16; i += kKqThreads) {
+    const int t = i / (K / 16);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (t < M) v = reinterpret_cast<const u32x4*>(xq + (int64_t)t * K)[i % (K / 16)];
+    reinterpret_cast<u32x4*>(lx)[i] = v;
+  }
+  for (int i = tid; i < MT * nsub; i += kKqThreads) lb[i] = i / nsub < M ? bsums[(int64_t)i] : 0;
+  for (int i = tid; i < MT * nsb; i += kKqThreads) ls[i] = i / nsb < M ? xs[(int64_t)i] : 0.0f;
+  __syncthreads();
+  if (ng == 0) return;  // wave-uniform; no barrier follows
 
   float acc[kKqRows][MT];
 #pragma unroll
