@@ -525,20 +525,24 @@ static hipError_t launch_wl(const MatmulArgs& a) {
 // or one after another, so a tiling costs that count times the tile area.
 // Candidates, ties to the first: 8 waves x 256 x 96 (two fragments of rows
 // each, one workgroup per CU), 4 waves x 256 x 64 and 4 waves x 256 x 48 (two
-// per CU). Measured (Q8, clocks settled): M = 512, K = 4096, N = 11008:
-// 52.6 / 56.1 / 54.5 us (8 waves x 512 x 48, the same area: 54.8 us, its
-// activation traffic from L2 twice that of 256 x 96); M = 256, K = 8192,
-// N = 28672: 256 x 64 144 us, 256 x 48 197 us, 8 x 256 x 96 191 us; M = 1024:
-// 256 x 96 103 us, 256 x 64 106 to 108 us. The model ranks them the same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
+// per CU), 8 waves x 256 x 112. (256 x 128 would never be chosen: it costs
+// at least what 256 x 64 does.) Measured (Q8, clocks settled): M = 512,
+// K = 4096, N = 11008: 52.6 / 56.1 / 54.5 / 54.9 us (8 waves x 512 x 48, the
+// same area: 54.8 us, its activation traffic from L2 twice that of 256 x 96);
+// M = 256, K = 8192, N = 28672: 256 x 112 (256 tiles, one per CU) 122 us,
+// 256 x 64 143, 256 x 48 197, 256 x 96 191, 256 x 128 123 (Q4, f16 scales:
+// 256 x 112 113 us against 122 at 256 x 64);
+// M = 1024: 256 x 96 103 us, 256 x 64 106 to 108 us. The model ranks them the
+// same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
 // (twice the workgroups of 64 x 128) measured 126 against 151 us (Q4) and 68
 // against 81 us (Q8) at M = 32, K = 8192, N = 28672.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   if (a.m > 128) {
-    const int64_t bm[3] = {256, 256, 256}, bn[3] = {96, 64, 48};
+    const int64_t bm[4] = {256, 256, 256, 256}, bn[4] = {96, 64, 48, 112};
     int best = 0;
     int64_t best_cost = INT64_MAX;
-    for (int i = 0; i < 3; i++) {
+    for (int i = 0; i < 4; i++) {
       const int64_t tiles = (a.m + bm[i] - 1) / bm[i] * ((a.npad + bn[i] - 1) / bn[i]);
       const int64_t cost = (tiles + cu_count - 1) / std::max(cu_count, 1) * bm[i] * bn[i];
       if (cost < best_cost) {
@@ -548,7 +552,8 @@ static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
     }
     if (best == 0) return launch_wl<FMT, ST, 2, 6, 4, 2, 8>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
-    return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
+    if (best == 2) return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
+    return launch_wl<FMT, ST, 2, 7, 4, 2, 8>(a);
   }
   if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);
   return launch_t<FMT, ST, 8, 2>(a);

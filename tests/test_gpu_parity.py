@@ -233,11 +233,13 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
     assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
 
 
-@pytest.mark.parametrize("m,in_,out", [(500, 96, 12004), (300, 416, 12000), (512, 1024, 11008)])
+@pytest.mark.parametrize("m,in_,out", [(500, 96, 12004), (300, 416, 12000), (512, 1024, 11008), (200, 96, 27999),
+                                       (256, 416, 28000)])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_gemm_bf16_wide_tiles(torch, ctx, orc, m, in_, out, fmt):
-    # wide N near m = 512: the tile cost model picks the 8-wave 512 x 48 tile
-    # (one workgroup per CU); ragged M and N, 3 and 13 K-blocks
+    # wide N: the tile cost model picks an 8-wave tile, one workgroup per CU
+    # (256 x 96 near m = 512, 256 x 112 near N = 28672 at m <= 256); ragged
+    # M and N, 3 and 13 K-blocks
     import raster_amd
 
     x = wl.activations(m, in_, seed=m + in_, dtype="bf16")
