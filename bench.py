@@ -900,7 +900,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(kern_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": read_traffic("gemm_bf16_q8_C2"),
                      "peak_from_device_props": round(peak_props, 1),
-                     "kernel": "rq::gemm_wl_kernel", "flop_per_launch": flops,
+                     "kernel": "rq::gemm_wk_kernel", "flop_per_launch": flops,
                      "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
 

@@ -480,6 +480,198 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
   }
 }
 
+// K-split wave pairs (8 waves, 256 x 16 NT tiles): waves w and w + 4 share a
+// SIMD and own the same 64 rows (four 16-row activation fragments); wave w
+// takes the even k-steps and wave w + 4 the odd ones. Per k-step each
+// dequantized weight fragment in LDS is read by four waves instead of eight
+// (24 KB of LDS reads per k-step at NT 6, against 48 KB when the eight waves
+// stack along M), and one barrier serves two k-steps. The two waves' f32
+// accumulators are added through LDS at the end (a different summation order
+// from the one-wave-per-row-block kernel: two interleaved partial sums).
+// Pipeline per macro step t (k-steps 2t, 2t+1; ring indices compile-time):
+//   VMEM: this wave's activation fragments of macro step t+1 (two-slot ring),
+//         weight codes of macro step t+R (2 NT dequant units per macro step,
+//         (fragment, k parity), dealt over the 8 waves)
+//   LDS:  read this wave's NT weight fragments of macro step t; write macro
+//         step t+2's, dequantized, into LDS buffer (t+2) % 4
+//   MFMA: 4 NT per wave, half before and half after the dequant
+//   one barrier
+// Measured at C2 (M 512, K 4096, N 11008): 50.1-50.8 us against 52.4-52.9 us
+// for gemm_wl_kernel<.., 2, 6, 4, 2, 8>; C5 (M 256, K 8192, N 28672, NT 7):
+// 121 against 123 us. Keeping the next macro step's weight fragments in
+// registers (a second B buffer) measured the same at NT 6 and far slower at
+// NT 7 (226 us); a four-slot activation ring 51.3-51.9 us.
+template <int FMT, typename ST, int NT, int R>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_wk_kernel(
+    const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
+    int M, int K, int N, int npad, int y_dtype, int tiles_m) {
+  constexpr int W = 8, MT = 4, L = 4, RA = 2;
+  constexpr int NU = 2 * NT;            // dequant units (fragment, k parity) per macro step
+  constexpr int CW = (NU + W - 1) / W;  // units per wave (at most)
+  constexpr int RC = (L * 2 * NT) / (4 * MT);  // fragments per round of the final reduction
+  static_assert(R >= 4 && R % L == 0, "ring depth: whole turns of the LDS ring");
+  static_assert(RC >= 1, "the final reduction fits the LDS ring");
+  __shared__ __attribute__((aligned(16))) bf16x8 Bs[L][2][NT][64];
+
+  // tile order as gemm_wl_kernel: row tiles of a column tile on one XCD
+  const int nblk = (int)gridDim.x, bid = (int)blockIdx.x;
+  const int xcd = bid & 7, per = nblk >> 3, rem = nblk & 7;
+  const int tord = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
+  const int tm = tord % tiles_m, tn = tord / tiles_m;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 3, kh = wave >> 2;  // row block, k parity
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nkb = K / 32;
+  const int m0 = tm * (16 * MT * 4) + wm * (16 * MT);
+  const int n0 = tn * (16 * NT);
+
+  const int mt_last = (M + 15) / 16 - 1;
+  const uint16_t* asrc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; i++) asrc[i] = xf + (int64_t)min(m0 / 16 + i, mt_last) * nkb * 512 + lane * 8;
+  // dequant unit u = wave + W j: k parity u / NT, weight fragment u % NT
+  const int g_last = npad / 16 - 1;
+  int64_t wchunk[CW];
+  int upar[CW];
+#pragma unroll
+  for (int j = 0; j < CW; j++) {
+    const int u = min(wave + W * j, NU - 1);
+    upar[j] = u / NT;
+    wchunk[j] = (int64_t)min(n0 / 16 + u % NT, g_last) * nkb;
+  }
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int c = 0; c < NT; c++) acc[i][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  bf16x8 a[RA][MT];
+  WCodes wc[R][CW];
+  bf16x8 b[NT];
+
+#define WK_LOAD_A(t_, u_)                                                                         \
+  do {                                                                                            \
+    const int kk_ = min(2 * (t_) + kh, nkb - 1);                                                  \
+    _Pragma("unroll") for (int i = 0; i < MT; i++) a[(u_) % RA][i] =                              \
+        *reinterpret_cast<const bf16x8*>(asrc[i] + (int64_t)kk_ * 512);                           \
+  } while (0)
+#define WK_LOAD_W(t_, u_)                                                                         \
+  do {                                                                                            \
+    _Pragma("unroll") for (int j = 0; j < CW; j++) {                                              \
+      const int kk_ = min(2 * (t_) + upar[j], nkb - 1);                                           \
+      load_wcodes<FMT, ST>(wc[(u_) % R][j], q, sc, wchunk[j] + kk_, fr, fg);                      \
+    }                                                                                             \
+  } while (0)
+#define WK_DEQUANT(u_)                                                                            \
+  do {                                                                                            \
+    _Pragma("unroll") for (int j = 0; j < CW; j++) {                                              \
+      const bf16x8 d_ = dequant_frag<FMT, ST>(wc[(u_) % R][j], fg);                               \
+      if (wave + W * j < NU) Bs[(u_) % L][upar[j]][(wave + W * j) % NT][lane] = d_;               \
+    }                                                                                             \
+  } while (0)
+#define WK_READ_B(u_)                                                                             \
+  do {                                                                                            \
+    _Pragma("unroll") for (int c = 0; c < NT; c++) b[c] = Bs[(u_) % L][kh][c][lane];              \
+  } while (0)
+#define WK_MFMA(u_, c0, c1)                                                                       \
+  do {                                                                                            \
+    _Pragma("unroll") for (int c = (c0); c < (c1); c++)                                           \
+      _Pragma("unroll") for (int i = 0; i < MT; i++)                                              \
+        acc[i][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[c], a[(u_) % RA][i], acc[i][c], 0, 0, 0); \
+  } while (0)
+#define WK_STEP(t_, u_, live_)                                                                    \
+  do {                                                                                            \
+    WK_LOAD_A((t_) + RA - 1, (u_) + RA - 1);                                                      \
+    WK_LOAD_W((t_) + R, (u_) + R);                                                                \
+    WK_READ_B(u_);                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    if (live_) WK_MFMA(u_, 0, NT / 2);                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    WK_DEQUANT((u_) + 2);                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+    if (live_) WK_MFMA(u_, NT / 2, NT);                                                           \
+    __syncthreads();                                                                              \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  } while (0)
+
+  // prologue: activations of macro step 0, weight codes of 0..R-1, LDS
+  // buffers 0 and 1 dequantized
+  WK_LOAD_A(0, 0);
+#pragma unroll
+  for (int st = 0; st < R; st++) WK_LOAD_W(st, st);
+  WK_DEQUANT(0);
+  WK_DEQUANT(1);
+  __syncthreads();
+
+  // macro steps with both k-steps present, then the rest (the last one may
+  // hold only an even k-step: the odd-k waves skip its MFMAs, not its
+  // barriers)
+  const int nm = (nkb + 1) / 2, nfull = nkb / 2;
+  int t = 0;
+  for (; t + R <= nfull; t += R) {
+#pragma unroll
+    for (int u = 0; u < R; u++) WK_STEP(t + u, u, true);
+  }
+#pragma unroll
+  for (int u = 0; u < R; u++)
+    if (t + u < nm) WK_STEP(t + u, u, 2 * (t + u) + kh < nkb);
+#undef WK_STEP
+#undef WK_MFMA
+#undef WK_READ_B
+#undef WK_DEQUANT
+#undef WK_LOAD_W
+#undef WK_LOAD_A
+
+  // the pair's sum through the LDS ring, RC fragments a round: the odd-k wave
+  // writes its accumulators, the even-k wave adds them to its own and stores.
+  // acc[i][c] holds y[m][n .. n+3], m = m0 + 16 i + fr, n = n0 + 16 c + 4 fg.
+  f32x4* red = reinterpret_cast<f32x4*>(&Bs[0][0][0][0]);
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+  for (int h = 0; h < (NT + RC - 1) / RC; h++) {
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int c = 0; c < RC; c++)
+          if (h * RC + c < NT) red[((wm * MT + i) * RC + c) * 64 + lane] = acc[i][h * RC + c];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        const int m = m0 + i * 16 + fr;
+#pragma unroll
+        for (int c = 0; c < RC; c++) {
+          const int cc = h * RC + c;
+          if (cc >= NT || m >= M) break;
+          const f32x4 v = acc[i][cc] + red[((wm * MT + i) * RC + c) * 64 + lane];
+          const int n = n0 + cc * 16 + 4 * fg;
+          if (vec && n + 3 < N) {
+            if (y_dtype == RQ_F32)
+              *reinterpret_cast<float4*>(static_cast<float*>(y) + (int64_t)m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
+            else
+              *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + (int64_t)m * N + n) =
+                  make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              if (n + r >= N) break;
+              if (y_dtype == RQ_F32)
+                static_cast<float*>(y)[(int64_t)m * N + n + r] = v[r];
+              else
+                static_cast<uint16_t*>(y)[(int64_t)m * N + n + r] = (uint16_t)f32_to_bf16_bits(v[r]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Kernel timing (a.ev_main set): the packing pass's end and the GEMM's end.
 // A start event would put an extra packet, and an idle gap of a few
 // microseconds, in front of the GEMM; the GEMM follows the packing pass
@@ -511,6 +703,18 @@ static hipError_t launch_wl(const MatmulArgs& a) {
   if (hipError_t e = launch_pack_x(a)) return e;
   hipExtLaunchKernelGGL((gemm_wl_kernel<FMT, ST, MT, NT, R, WPE, W>), dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * W), 0,
                         a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype, tiles_m);
+  return hipGetLastError();
+}
+
+template <int FMT, typename ST, int NT>
+static hipError_t launch_wk(const MatmulArgs& a) {
+  const int tiles_m = (int)((a.m + 255) / 256);
+  const int tiles_n = (int)((a.npad / 16 + NT - 1) / NT);
+  if (hipError_t e = launch_pack_x(a)) return e;
+  hipExtLaunchKernelGGL((gemm_wk_kernel<FMT, ST, NT, 4>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, a.stream,
+                        nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m);
   return hipGetLastError();
@@ -550,10 +754,10 @@ static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
         best = i;
       }
     }
-    if (best == 0) return launch_wl<FMT, ST, 2, 6, 4, 2, 8>(a);
+    if (best == 0) return launch_wk<FMT, ST, 6>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
     if (best == 2) return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
-    return launch_wl<FMT, ST, 2, 7, 4, 2, 8>(a);
+    return launch_wk<FMT, ST, 7>(a);
   }
   if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);
   return launch_t<FMT, ST, 8, 2>(a);
