@@ -182,7 +182,10 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    or 4e34 (Q8_0) overflows the offset sums and makes its row's outputs
  *    NaN; a non-finite activation makes its row's outputs non-finite.
  *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
- *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA.
+ *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA;
+ *    on the GEMM's eight-wave tiles (m > 128 where the tile cost model picks
+ *    them) K is summed as two f32 partial sums, of the even and of the odd
+ *    32-blocks, added at the end.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
  *    split into two bf16 terms (about 16 mantissa bits).
  *
