@@ -159,8 +159,9 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    Q8_0 at 9 <= m <= 16 when out * in <= 32 Mi (2^25) elements;
  *  - every other m <= 16: the int8-level decode kernel (int8 MFMA on the raw
  *    codes, v_mfma_i32_16x16x64_i8);
- *  - m > 16: bf16 x: the bf16 MFMA GEMM (Q4_0 at 16 < m <= 64: the
- *    weight-stream GEMM); f32 x: the exact-code f32 GEMM;
+ *  - m > 16: bf16 x: the bf16 MFMA GEMM (the weight-stream GEMM for Q4_0
+ *    at 16 < m <= 64 and for Q8_0 at 16 < m <= 48, or <= 64 when
+ *    in >= 8192); f32 x: the exact-code f32 GEMM;
  *  - Q4_K / Q6_K weights (f32 x only, any m; bf16 x fails with RQ_ERR_DTYPE):
  *    x is quantized to q8_K in scratch and the K-quant GEMV runs, the same two
  *    kernels as rq_quantize_act_q8k + rq_qmatmul_q8k and bit for bit their
@@ -199,8 +200,8 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    m <= 8); the MFMA decode kernel when a slice of x would not fit two
  *    workgroups' LDS, and further until the grid covers about 85% of the CUs,
  *    rounded up to a power of two while each slice keeps 8 blocks (at most
- *    in / 32 slices); Q4_0 with bf16 x and 16 < m <= 64 on a thin grid (up to
- *    8 slices);
+ *    in / 32 slices); the weight-stream GEMM (bf16 x, 16 < m <= 64) on a
+ *    thin grid (up to 8 slices);
  *  - Q4_K / Q6_K: the q8_K activations, m * (in + in/256*4 + in/sub*4)
  *    bytes (each part rounded up to 256), sub = 32 for Q4_K, 16 for Q6_K.
  * Under HIP graph capture nothing can be allocated: run the same (or a

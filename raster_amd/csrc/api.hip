@@ -859,8 +859,8 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     // fragment-major copy of the activations: ceil(m/16)*16 rows
     const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
     if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
-    if (gemm_sm_takes(w.format, m)) {
-      a.slices = gemm_sm_slices(m, w.in, w.npad, c->cu_count);
+    if (gemm_sm_takes(w.format, m, w.in)) {
+      a.slices = gemm_sm_slices(w.format, m, w.in, w.npad, c->cu_count);
       if (a.slices > 1) {
         if (int s = call_scratch(c, fixed, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, 1, &part))
           return s;
@@ -881,7 +881,7 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
                  : mf.ok              ? launch_gemv_mf(a, mf)
                  : plan.ok            ? launch_gemv(a, plan)
                  : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
-                 : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m) ? launch_gemm_sm(a, a.slices)
+                 : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m, w.in) ? launch_gemm_sm(a, a.slices)
                                                                     : launch_gemm_bf16(a, c->cu_count))
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);

@@ -360,17 +360,29 @@ static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
 // slice keeps at least 8 chunks of K. Measured (Q4, bf16 x, two fragments per
 // wave, 4-step chunks): M = 32, K = 8192, N = 28672: 3 / 4 / 6 / 8 slices
 // 52.5 / 53.2 / 52.3 / 51.5 us; M = 64: 1 / 2 slices 82.9 / 69.1 us;
-// M = 17, K = 4096, N = 14336: 2 / 4 slices 21.1 / 19.2 us.
-int gemm_sm_slices(int64_t m, int64_t k, int64_t npad, int cu_count) {
-  const int64_t waves = (npad / (64 * kSmNTW)) * 4, want = (int64_t)cu_count * (m <= 32 ? 24 : 12);
+// M = 17, K = 4096, N = 14336: 2 / 4 slices 21.1 / 19.2 us. Q8_0 (cold,
+// packing included), K = 8192, N = 28672: M = 17 2 / 3 / 4 / 6 slices 69.9 /
+// 63.3 / 63.2 / 66.2 us, M = 32 75.3 / 67.1 / 69.5 / 71.3, M = 64 87.4 / 81.1 /
+// 90.7 / 86.7.
+int gemm_sm_slices(int format, int64_t m, int64_t k, int64_t npad, int cu_count) {
+  // Q8_0 moves twice the bytes per step: 12 waves per CU at every m
+  const int64_t waves = (npad / (64 * kSmNTW)) * 4;
+  const int64_t want = (int64_t)cu_count * (format == RQ_Q8_0 || m > 32 ? 12 : 24);
   int64_t ks = std::max<int64_t>(1, want / std::max<int64_t>(waves, 1));
   ks = std::min<int64_t>(ks, std::max<int64_t>(1, (k / 32) / (8 * kSmKC)));
   return (int)std::min<int64_t>(ks, 8);
 }
 
-// Q4_0 only: for Q8_0 (twice the bytes per step) the per-wave-weights GEMM
-// measured ahead (64 vs 67 us at M = 32, K = 8192, N = 28672).
-bool gemm_sm_takes(int format, int64_t m) { return format == RQ_Q4_0 && m > 16 && m <= 64; }
+// Q4_0 at 16 < m <= 64. Q8_0 at 16 < m <= 48, and up to 64 from K = 8192:
+// measured cold against the per-wave-weights GEMM (Q8_0, bf16 x and y,
+// packing included), K = 8192, N = 28672: m = 17 / 32 / 48 / 64 63 / 67 / 79 /
+// 81 us against 92 / 84 / 88 / 87; K = 4096, N = 11008: m = 17 / 32 / 48 / 64
+// 24.3 / 25.3 / 28.4 / 29.1 against 27.9 / 29.1 / 29.4 / 29.3; K = 4096,
+// N = 14336: m = 17 / 32 / 64 26.5 / 27.7 / 32.5 against 30.3 / 30.1 / 31.0.
+bool gemm_sm_takes(int format, int64_t m, int64_t k) {
+  if (m <= 16 || m > 64) return false;
+  return format == RQ_Q4_0 || m <= 48 || k >= 8192;
+}
 
 hipError_t launch_gemm_sm(const MatmulArgs& a, int ks) {
   if (a.m <= 16 || a.m > 64) return hipErrorInvalidValue;

@@ -166,8 +166,8 @@ hipError_t launch_gemm(const MatmulArgs& a, int cu_count);
 hipError_t launch_gemm_bf16(const MatmulArgs& a, int cu_count);
 // bf16 x, 16 < m <= 64, weight-stream GEMM with LDS-staged activations
 // (gemm_sm.hip); K-slices and whether it takes a call
-int gemm_sm_slices(int64_t m, int64_t k, int64_t npad, int cu_count);
-bool gemm_sm_takes(int format, int64_t m);
+int gemm_sm_slices(int format, int64_t m, int64_t k, int64_t npad, int cu_count);
+bool gemm_sm_takes(int format, int64_t m, int64_t k);
 hipError_t launch_gemm_sm(const MatmulArgs& a, int ks);
 // int8 activations (x_dtype kXtI8, scales / sums in a.ops), m > 16 (gemm_i8.hip)
 hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count);

@@ -9,7 +9,7 @@ checked where it is timed:
                        32 and 64 (small-m GEMM with K-slices), 256 (prefill GEMM)
   Q8_0 (f32 scales)    m = 1 (int8-level decode), 12 and 16 (int8-level decode:
                        the weight is above the MFMA decode's 32 Mi elements),
-                       32 (bf16 GEMM, 64 x 64 tiles), 256 (prefill GEMM)
+                       32 (small-m GEMM with K-slices), 256 (prefill GEMM)
 
 bf16 activations as the workload defines them, plus f32 activations at the
 decode sizes. Each output is checked against the C oracle (qlinear-q8's loop,

@@ -291,6 +291,31 @@ def test_gemm_small_m_q4_kslices(torch, ctx, orc, m, in_, out, scale_kind):
     assert orc.normwise_relerr(y32[:, rows], ref) < TOL_BF16
 
 
+@pytest.mark.parametrize("m,in_,out", [(17, 4096, 520), (32, 8192, 256), (48, 2080, 100), (64, 8192, 96),
+                                       (64, 4096, 96), (33, 256, 14336), (20, 96, 40)])
+def test_gemm_small_m_q8_kslices(torch, ctx, orc, m, in_, out):
+    # Q8_0 with bf16 activations takes the small-m GEMM at 16 < m <= 48, and
+    # to m = 64 from in = 8192 (m = 64 at in 4096 stays on the per-wave GEMM):
+    # K-slices added in slice order, so two calls agree bit for bit
+    import raster_amd
+
+    x = wl.activations(m, in_, seed=5 * m + out, dtype="bf16")
+    codes, scales = wl.q8_weights(out, in_, seed=in_ + out)
+    note(f"gemm-sm q8 m={m} {out}x{in_}")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    y32 = run(torch, w, x, m, "bf16", "f32")
+    y32b = run(torch, w, x, m, "bf16", "f32")
+    y16 = run(torch, w, x, m, "bf16", "bf16")
+    w.destroy()
+    assert np.array_equal(y32, y32b)
+    assert np.array_equal(orc.f32_to_bf16_bits(y32), orc.f32_to_bf16_bits(y16))
+    rows = rows_subset(out, 256)
+    cs = codes.reshape(out, in_)[rows].ravel()
+    ss = scales.reshape(out, in_ // 32)[rows].ravel()
+    ref = orc.qlinear_q8(x, cs, ss, m, in_, len(rows)).reshape(m, len(rows))
+    assert orc.normwise_relerr(y32[:, rows], ref) < TOL_BF16
+
+
 # ---------------------------------------------------------------- decode kernel edges
 @pytest.mark.parametrize("m,in_,out", [(1, 32, 16), (3, 96, 40), (16, 160, 33), (5, 4096, 48), (16, 4096, 64)])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])

@@ -80,6 +80,7 @@ CASES = [
     ("q4", 14336, 4096, [16, 6], "f32", "f32"),          # MFMA decode, Q4_0, K-slices
     ("q8", 4160, 8192, [12, 3], "f32", "f32"),           # int8-level decode with K-split (above 32 Mi)
     ("q4", 8192, 8192, [64, 32], "bf16", "bf16"),        # small-m GEMM: packed x + K-slices
+    ("q8", 28672, 8192, [32, 17], "bf16", "bf16"),       # small-m GEMM, Q8_0: packed x + K-slices
     ("q8", 11008, 4096, [512, 128], "bf16", "bf16"),     # prefill GEMM: packed x
     ("q8", 1000, 1024, [300, 17], "f32", "f32"),         # exact-f32 GEMM, no scratch
     ("q4k", 4096, 4096, [8, 1], "f32", "f32"),           # K-quant: q8_K activations in scratch
