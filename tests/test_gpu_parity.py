@@ -234,12 +234,13 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
 
 
 @pytest.mark.parametrize("m,in_,out", [(500, 96, 12004), (300, 416, 12000), (512, 1024, 11008), (200, 96, 27999),
-                                       (256, 416, 28000)])
+                                       (256, 416, 28000), (300, 32, 12004), (300, 64, 12004), (300, 288, 12004)])
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_gemm_bf16_wide_tiles(torch, ctx, orc, m, in_, out, fmt):
     # wide N: the tile cost model picks an 8-wave tile, one workgroup per CU
-    # (256 x 96 near m = 512, 256 x 112 near N = 28672 at m <= 256); ragged
-    # M and N, 3 and 13 K-blocks
+    # (256 x 96 near m = 512, 256 x 112 near N = 28672 at m <= 256), whose
+    # wave pairs split K into even and odd blocks; ragged M and N, 1, 2, 3, 9
+    # (one full ring turn and half a step) and 13 K-blocks
     import raster_amd
 
     x = wl.activations(m, in_, seed=m + in_, dtype="bf16")
