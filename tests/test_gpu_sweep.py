@@ -1,0 +1,112 @@
+"""A seeded sweep of rq_qmatmul shapes across every dispatch route, against the C oracle.
+
+The launch plans pick kernels by m (decode kernels up to 16 rows, the small-m
+weight-stream GEMM to 64, the per-wave-weights GEMM to 128, the tile cost model
+above), by format, activation dtype and weight size, and cut K into slices
+by LDS fit and grid fill. The dedicated tests pin each route at chosen edges;
+this sweep draws 48 shapes from a fixed seed over every m band (in a multiple
+of 32, out anything), both formats, f32 and bf16 x, f32 and bf16 y, and holds
+each to the oracle (qlinear-q8's loop, raster/quant/train.clj:77-108, over the
+Q8_0 or Q4_0 dequant) on a subset of output rows: normwise max|y - ref| /
+max|ref| < 1e-3 for f32 x and y, < 1e-2 with bf16 x or y. Each call is
+repeated and must agree bit for bit (every split adds its slices in a fixed
+order), and rq_qmatmul_noalloc must give the same bits where its fixed
+scratch suffices.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from raster_amd import _lib
+from raster_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 1e-2
+
+
+def note(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    if not t.cuda.is_available():
+        pytest.skip("no GPU")
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import raster_amd
+
+    c = raster_amd.Context(0)
+    yield c
+    c.close()
+
+
+def shapes():
+    rng = np.random.default_rng(20261202)
+    bands = [(1, 1), (2, 4), (5, 8), (9, 16), (17, 32), (33, 64), (65, 128), (129, 600)]
+    out = []
+    for i in range(48):
+        lo, hi = bands[i % len(bands)]
+        m = int(rng.integers(lo, hi + 1))
+        in_ = 32 * int(rng.choice([1, 3, 7, 32, 64, 129, 160, 256]))
+        n = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 6000))]))
+        fmt = ["q8", "q4"][int(rng.integers(0, 2))]
+        xdt = ["f32", "bf16"][int(rng.integers(0, 2))]
+        ydt = ["f32", "bf16"][int(rng.integers(0, 2))]
+        out.append((i, m, in_, n, fmt, xdt, ydt))
+    return out
+
+
+SHAPES = shapes()
+
+
+@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", SHAPES, ids=[f"s{s[0]}" for s in SHAPES])
+def test_sweep(torch, ctx, orc, i, m, in_, out, fmt, xdt, ydt):
+    import raster_amd
+
+    note(f"sweep {i}: {fmt} m={m} in={in_} out={out} x={xdt} y={ydt}")
+    x = wl.activations(m, in_, seed=1000 + i, dtype=xdt)
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=2000 + i)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=2000 + i)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+    try:
+        xt = torch.from_numpy(x).cuda().reshape(m, in_)
+        if xdt == "bf16":
+            xt = xt.to(torch.bfloat16)
+        ytype = torch.bfloat16 if ydt == "bf16" else torch.float32
+        y1 = w.matmul(xt, out_dtype=ytype)
+        y2 = w.matmul(xt, out_dtype=ytype)
+        y3 = torch.full((m, out), float("nan"), dtype=ytype, device="cuda")
+        st = _lib.lib().rq_qmatmul_noalloc(ctx.handle, w.handle, C.c_void_p(xt.data_ptr()),
+                                           _lib.RQ_BF16 if xdt == "bf16" else _lib.RQ_F32, C.c_void_p(y3.data_ptr()),
+                                           _lib.RQ_BF16 if ydt == "bf16" else _lib.RQ_F32, m,
+                                           C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        a, b = y1.float().cpu().numpy(), y2.float().cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert st in (_lib.RQ_OK, _lib.RQ_ERR_SHAPE)
+        if st == _lib.RQ_OK:
+            assert np.array_equal(a.view(np.uint32), y3.float().cpu().numpy().view(np.uint32))
+        rows = np.unique(np.concatenate([[0, out - 1], np.linspace(0, out - 1, min(out, 200)).astype(np.int64)]))
+        if fmt == "q8":
+            ref = orc.qlinear_q8(x, codes.reshape(out, in_)[rows].ravel(),
+                                 scales.reshape(out, in_ // 32)[rows].ravel(), m, in_, len(rows))
+        else:
+            ref = orc.qlinear_q4(x, packed.reshape(out, in_ // 2)[rows].ravel(),
+                                 sc16.reshape(out, in_ // 32)[rows].ravel(), m, in_, len(rows))
+        tol = TOL_F32 if xdt == "f32" and ydt == "f32" else TOL_BF16
+        assert np.all(np.isfinite(a))
+        assert orc.normwise_relerr(a[:, rows], ref.reshape(m, len(rows))) < tol
+    finally:
+        w.destroy()
