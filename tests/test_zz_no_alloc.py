@@ -4,12 +4,15 @@ route that uses scratch (K-slice partial sums of the decode kernels, the packed
 activations of the bf16 GEMMs, both for the small-m GEMM, a K-quant weight's
 q8_K activations) and on routes that
 use none, two calls in a row with the second one smaller, and a call that needs
-more than the fixed scratch is refused with RQ_ERR_SHAPE.
+more than the fixed scratch is refused with RQ_ERR_SHAPE. The seeded shapes
+of the GPU sweep (every dispatch route) give the same bits through both
+entries, or RQ_ERR_SHAPE where a call needs more than the fixed scratch.
 """
 import ctypes as C
 
 import numpy as np
 import pytest
+from sweep_shapes import SHAPES
 
 from raster_amd import _lib
 from raster_amd import workloads as wl
@@ -119,5 +122,39 @@ def test_noalloc_rejects_calls_beyond_its_scratch(torch, ctx):
         # and the same call through rq_qmatmul still works
         w.matmul(x, y)
         torch.cuda.synchronize()
+    finally:
+        w.destroy()
+
+
+@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", SHAPES, ids=[f"s{s[0]}" for s in SHAPES])
+def test_noalloc_sweep(torch, ctx, i, m, in_, out, fmt, xdt, ydt):
+    import raster_amd
+
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=3000 + i)
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=3000 + i)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), out, in_, ctx)
+    try:
+        note(f"noalloc sweep {i}: {fmt} m={m} in={in_} out={out} x={xdt} y={ydt}")
+        x = torch.from_numpy(wl.activations(m, in_, seed=4000 + i)).cuda().reshape(m, in_)
+        if xdt == "bf16":
+            x = x.to(torch.bfloat16)
+        ytype = torch.bfloat16 if ydt == "bf16" else torch.float32
+        y_ref = torch.full((m, out), float("nan"), dtype=ytype, device="cuda")
+        y_na = torch.full((m, out), float("nan"), dtype=ytype, device="cuda")
+        s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        xc, yc = (_lib.RQ_BF16 if xdt == "bf16" else _lib.RQ_F32), (_lib.RQ_BF16 if ydt == "bf16" else _lib.RQ_F32)
+        _lib.call("rq_qmatmul", ctx.handle, w.handle, C.c_void_p(x.data_ptr()), xc, C.c_void_p(y_ref.data_ptr()), yc,
+                  m, s)
+        st = _lib.lib().rq_qmatmul_noalloc(ctx.handle, w.handle, C.c_void_p(x.data_ptr()), xc,
+                                           C.c_void_p(y_na.data_ptr()), yc, m, s)
+        torch.cuda.synchronize()
+        assert st in (_lib.RQ_OK, _lib.RQ_ERR_SHAPE)
+        if st == _lib.RQ_OK:
+            a, b = y_ref.float().cpu().numpy(), y_na.float().cpu().numpy()
+            assert np.all(np.isfinite(a))
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     finally:
         w.destroy()
