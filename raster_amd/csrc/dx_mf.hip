@@ -22,7 +22,13 @@
 // the sums run in f32 in a fixed order. The weight is read once per 128 dy
 // rows instead of once per few rows; when that leaves CUs idle the reduction
 // is cut into slices whose partial sums a second kernel adds in slice order.
-// Waves: 4 along m (32 rows each) x 2 along the columns (two blocks each).
+// Waves: 4 along m (32 rows each, all four column blocks); waves w and w + 4
+// share a SIMD and the rows, and split the reduction: wave w takes the first
+// 16-row group of each step, wave w + 4 the second, so no two waves load the
+// same dy fragments (with the waves split along the columns instead, two
+// waves loaded each fragment: M = 512, K = 4096, N = 11008, one slice, 238 ->
+// 225 us; M = 1024 273 -> 260; K = 11008, N = 4096 189 -> 181). The two
+// partial sums are added through LDS at the end.
 #include <algorithm>
 
 #include "rq_internal.h"
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(kDxmThreads) void dx_mf_kernel(const uint8_t* __res
   const int sl = (int)blockIdx.y, g0 = min(sl * gps, npad / 16), ng = min(npad / 16 - g0, gps);
   const int tid = (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 3, wi = wave >> 2;
+  const int wm = wave & 3, kh = wave >> 2;  // 32-row tile, group parity within a step
   const int mt = tm * 4 + wm;          // this wave's 32-row tile
   const int mtc = min(mt, mt_n - 1);   // clamped for loads (rows past M are never stored)
   const int b0 = ti * kDxmNB;          // the workgroup's first column block
@@ -156,16 +162,17 @@ __global__ __launch_bounds__(kDxmThreads) void dx_mf_kernel(const uint8_t* __res
 
   // ---- dy fragments of this wave: ring of kDxmAR groups
   const uint16_t* abase = dyf + (int64_t)mtc * ngroups * 2 * kDxmFrag + lane * 8;
-  bf16x8 ah[kDxmAR], al[kDxmAR];
+  constexpr int AR = kDxmAR / kDxmG;  // this wave's groups in flight (every other group)
+  bf16x8 ah[AR], al[AR];
   auto load_a = [&](int ri, int g) {
     const int gc = g0 + min(g, ng - 1);
     ah[ri] = *reinterpret_cast<const bf16x8*>(abase + (int64_t)gc * 2 * kDxmFrag);
     al[ri] = *reinterpret_cast<const bf16x8*>(abase + ((int64_t)gc * 2 + 1) * kDxmFrag);
   };
 
-  f32x16 acc[2];
+  f32x16 acc[kDxmNB];
 #pragma unroll
-  for (int c = 0; c < 2; c++)
+  for (int c = 0; c < kDxmNB; c++)
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[c][e] = 0.0f;
 
@@ -183,59 +190,71 @@ __global__ __launch_bounds__(kDxmThreads) void dx_mf_kernel(const uint8_t* __res
 #pragma unroll
   for (int k = 0; k < kDxmDB; k++) load_b(k, k);
 #pragma unroll
-  for (int g = 0; g < kDxmAR; g++) load_a(g, g);
+  for (int r = 0; r < AR; r++) load_a(r, kDxmG * r + kh);
   store_b(0, 0);
   load_b(0, kDxmDB);
 
   auto step = [&](int s, int P) {  // P = s % kDxmDB
     __syncthreads();  // buffer s & 1 complete; buffer (s + 1) & 1 no longer read
     const int buf = P & 1;
-    bf16x8 bh[kDxmG][2], bl[kDxmG][2];
+    bf16x8 bh[kDxmNB], bl[kDxmNB];
 #pragma unroll
-    for (int gg = 0; gg < kDxmG; gg++)
-#pragma unroll
-      for (int c = 0; c < 2; c++) {
-        bh[gg][c] = *reinterpret_cast<const bf16x8*>(&bs[buf][gg][2 * wi + c][0][dxm_slot(lane) * 8]);
-        bl[gg][c] = *reinterpret_cast<const bf16x8*>(&bs[buf][gg][2 * wi + c][1][dxm_slot(lane) * 8]);
-      }
+    for (int c = 0; c < kDxmNB; c++) {
+      bh[c] = *reinterpret_cast<const bf16x8*>(&bs[buf][kh][c][0][dxm_slot(lane) * 8]);
+      bl[c] = *reinterpret_cast<const bf16x8*>(&bs[buf][kh][c][1][dxm_slot(lane) * 8]);
+    }
     // the next step's weights into the other buffer, then that ring slot's
     // refill (step s + 1 + kDxmDB)
     store_b((P + 1) % kDxmDB, buf ^ 1);
     load_b((P + 1) % kDxmDB, s + 1 + kDxmDB);
-#pragma unroll
-    for (int gg = 0; gg < kDxmG; gg++) {
-      const int g = s * kDxmG + gg, ri = (kDxmG * P + gg) % kDxmAR;
+    {
+      const int g = s * kDxmG + kh, ri = P % AR;
       const bf16x8 a_h = ah[ri], a_l = al[ri];
-      if (g < ng) {  // workgroup-uniform
+      if (g < ng) {  // wave-uniform
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, bh[gg][c], acc[c], 0, 0, 0);
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, bl[gg][c], acc[c], 0, 0, 0);
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, bh[gg][c], acc[c], 0, 0, 0);
+        for (int c = 0; c < kDxmNB; c++) {
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, bh[c], acc[c], 0, 0, 0);
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, bl[c], acc[c], 0, 0, 0);
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, bh[c], acc[c], 0, 0, 0);
         }
       }
-      load_a(ri, g + kDxmAR);
+      load_a(ri, g + kDxmG * AR);
     }
   };
   for (int s = 0; s < nsteps; s += kDxmDB) {
 #pragma unroll
     for (int P = 0; P < kDxmDB; P++) step(s + P, P);
   }
-  static_assert(kDxmDB == 4 && kDxmAR % kDxmG == 0 && (kDxmG * kDxmDB) % kDxmAR == 0, "ring indices");
+  static_assert(kDxmDB == 4 && kDxmG == 2 && kDxmDB % AR == 0, "ring indices");
 
+  // the pair's sum: the odd-group waves pass their accumulators through LDS,
+  // two column blocks a round; the even-group waves add and store.
   // D layout: lane l holds column l % 32 of the 32x32 tile, rows
   // (r / 4) 8 + 4 (l / 32) + r % 4
-  if (mt >= mt_n) return;
+  f32x16* red = reinterpret_cast<f32x16*>(&bs[0][0][0][0][0]);
+  static_assert(sizeof(bs) >= 4 * 2 * 64 * sizeof(f32x16), "reduction fits");
   float* dst = gridDim.y == 1 ? dx : part + (int64_t)sl * M * K;
 #pragma unroll
-  for (int c = 0; c < 2; c++) {
-    const int b = b0 + 2 * wi + c;
-    if (b >= nkb) continue;
-    const int col = 32 * b + (lane & 31);
+  for (int h = 0; h < kDxmNB / 2; h++) {
+    __syncthreads();
+    if (kh == 1) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int m = 32 * mt + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
-      if (m < M) dst[(int64_t)m * K + col] = acc[c][r];
+      for (int c = 0; c < 2; c++) red[(wm * 2 + c) * 64 + lane] = acc[2 * h + c];
+    }
+    __syncthreads();
+    if (kh == 0 && mt < mt_n) {
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int b = b0 + 2 * h + c;
+        if (b >= nkb) continue;
+        const f32x16 v = acc[2 * h + c] + red[(wm * 2 + c) * 64 + lane];
+        const int col = 32 * b + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int m = 32 * mt + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
+          if (m < M) dst[(int64_t)m * K + col] = v[r];
+        }
+      }
     }
   }
 }
