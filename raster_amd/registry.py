@@ -13,8 +13,10 @@ raster/compiler/backend/cpu/quant.clj:85-90,206-212) and run on the device:
 
   q4_K : rq_q4k_of (quantize-weight-q4k on the device; rows of `cols` not a
          multiple of 256 are zero-padded as raster.quant.pack/q4k-of does),
-         a resident Q4_K weight, then per call rq_quantize_act_q8k +
-         rq_qmatmul_q8k (quantize-act-q8k + qmatmul-q4k-composable!);
+         a resident Q4_K weight, then per call rq_qmatmul with f32 x, which
+         quantizes x to q8_K and runs the K-quant GEMV in one call
+         (quantize-act-q8k + qmatmul-q4k-composable!, bitwise the same as
+         rq_quantize_act_q8k + rq_qmatmul_q8k);
   q6_K : the same with rq_quantize_weight_q6k and the Q6_K kernel;
   q8_0 : rq_q8_quantize (raster.quant.train/q8-quantize) into a resident Q8_0
          weight, then rq_qmatmul (qlinear-q8's numerics). Raster reaches this
@@ -33,7 +35,7 @@ from typing import Any
 
 import numpy as np
 
-from .quant import QWeight, context, nextpad, q4k_of, q8_quantize, quantize_act_q8k, quantize_weight_q6k
+from .quant import QWeight, context, nextpad, q4k_of, q8_quantize, quantize_weight_q6k
 
 # descriptors as data, as in raster/compiler/backend/cpu/quant.clj
 Q4_K = {"name": "q4_K", "super-block": 256, "subblock": 32, "n-subblocks": 8, "weight-bits": 4, "scale-bits": 6,
@@ -152,12 +154,11 @@ def _quantize_kquant(fmt: str):
     return quantize
 
 
-def _apply_kquant(sub: int):
+def _apply_kquant():
     def apply(qm: QMatrix, x):
         w: QWeight = qm.arrays["weight"]
         xt, host = _device_x(x, qm.cols, qm.arrays["in"])
-        xq = quantize_act_q8k(w.ctx, xt.reshape(-1), qm.arrays["in"], sub)
-        return _finish(w.matmul_q8k(*xq), host, x)
+        return _finish(w.matmul(xt.reshape(-1, qm.arrays["in"])), host, x)
 
     return apply
 
@@ -175,8 +176,8 @@ def _apply_q8(qm: QMatrix, x):
     return _finish(w.matmul(xt), host, x)
 
 
-register_quant("q4_K", {"descriptor": Q4_K, "quantize": _quantize_kquant("q4_K"), "apply": _apply_kquant(32)})
-register_quant("q6_K", {"descriptor": Q6_K, "quantize": _quantize_kquant("q6_K"), "apply": _apply_kquant(16)})
+register_quant("q4_K", {"descriptor": Q4_K, "quantize": _quantize_kquant("q4_K"), "apply": _apply_kquant()})
+register_quant("q6_K", {"descriptor": Q6_K, "quantize": _quantize_kquant("q6_K"), "apply": _apply_kquant()})
 register_quant("q8_0", {"descriptor": Q8_0, "quantize": _quantize_q8, "apply": _apply_q8})
 
 __all__ = ["QMatrix", "register_quant", "registered_formats", "qmatrix", "matmul", "release", "nextpad",
