@@ -515,7 +515,9 @@ class KquantCase:
         else:
             arrs = wl.q6k_weights(n, k, seed)
             self.weights = [raster_amd.QWeight.q6k(*arrs, n, k, ctx) for _ in range(copies)]
-            self.bytes = n * k + n * (k // 256) * 4 + n * (k // 16)
+            # the device packs the 6-bit codes, 12 bytes per 16 (Raster's layout: a byte each)
+            self.bytes = n * k // 4 * 3 + n * (k // 256) * 4 + n * (k // 16)
+            self.raster_bytes = n * k + n * (k // 256) * 4 + n * (k // 16)
         x = torch.randn(m * k, device="cuda")
         self.xq = raster_amd.quantize_act_q8k(ctx, x, k, 32 if fmt == "q4k" else 16)
         self.y = torch.empty((m, n), device="cuda")
@@ -544,7 +546,9 @@ def kquant_lines(torch, ctx, m=1, k=4096, n=14336):
         cold_ms, _ = time_graph(torch, c.step)
         kms = time_kernels(torch, ctx, c.step)
         c.destroy()
-        lines[f"{fmt}_m{m}_{n}x{k}"] = {"weight_bytes": wb, "kernel_us": round(kms * 1e3, 3),
+        lines[f"{fmt}_m{m}_{n}x{k}"] = {"weight_bytes": wb, **({"raster_layout_bytes": one.raster_bytes}
+                                                              if hasattr(one, "raster_bytes") else {}),
+                                          "kernel_us": round(kms * 1e3, 3),
                                           "frac_hbm": round(wb / kms / 1e6 / HBM_PEAK_GBS, 4),
                                           "per_call_us": round(cold_ms * 1e3, 3),
                                           "warm_per_call_us": round(warm_ms * 1e3, 3)}

@@ -273,7 +273,9 @@ int rq_qmatmul_fused(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* 
  * quantize-weight-q4k / quantize-weight-q6k, quant.clj:92-137,214-239):
  *  Q4_K: wq u8[out*in/2] nibbles (w[k] low, w[k+16] high per 32-sub-block),
  *        da, db f32[out*in/256], aq u8[out*in/32] (0..63), bq i8[out*in/32];
- *  Q6_K: wq u8[out*in] (0..63), sc i8[out*in/16], ds f32[out*in/256].
+ *  Q6_K: wq u8[out*in] (0..63: a larger byte fails with RQ_ERR_SHAPE; the
+ *        device keeps the codes packed, 16 to 12 bytes), sc i8[out*in/16],
+ *        ds f32[out*in/256].
  * They take q8_K activations (rq_quantize_act_q8k, rq_qmatmul_q8k); rq_dequant
  * gives dequant-q4k / dequant-q6k bit for bit. rq_qmatmul and
  * rq_qmatmul_noalloc take them with f32 x (quantized to q8_K inside the call);

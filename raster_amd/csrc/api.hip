@@ -670,7 +670,26 @@ int rq_weight_create_q6k(rq_ctx h, const uint8_t* wq, const int8_t* sc, const fl
   if (int s = check_ctx(c)) return s;
   if (!wq || !sc || !ds || !w) return fail(RQ_ERR_NULL, "NULL argument");
   if (int s = check_shape_k(RQ_Q6_K, out, in)) return s;
-  return make_weight_k(c, RQ_Q6_K, out, in, wq, (size_t)(out * in), ds, (size_t)(out * (in / 256)) * 4, sc,
+  // the device keeps the 6-bit codes packed, 12 bytes per 16-code sub-block
+  // (the layout unpack_q6k in kquant.hip reads): 3/4 of Raster's byte per code
+  const size_t n = (size_t)out * (size_t)in;
+  std::vector<uint8_t> packed;
+  try {
+    packed.resize(n / 16 * 12);
+  } catch (const std::bad_alloc&) {
+    return fail(RQ_ERR_OOM, "host allocation failed");
+  }
+  uint8_t bad = 0;
+  for (size_t sb = 0; sb < n / 16; sb++) {
+    const uint8_t* q = wq + 16 * sb;
+    uint8_t* d = packed.data() + 12 * sb;
+    for (int j = 0; j < 16; j++) bad |= q[j];
+    for (int j = 0; j < 8; j++) d[j] = (uint8_t)((q[j] & 15) | ((q[j + 8] & 15) << 4));
+    for (int j = 0; j < 4; j++)
+      d[8 + j] = (uint8_t)((q[j] >> 4) | ((q[j + 4] >> 4) << 2) | ((q[j + 8] >> 4) << 4) | ((q[j + 12] >> 4) << 6));
+  }
+  if (bad & 0xC0) return fail(RQ_ERR_SHAPE, "Q6_K codes must lie in 0..63");
+  return make_weight_k(c, RQ_Q6_K, out, in, packed.data(), packed.size(), ds, (size_t)(out * (in / 256)) * 4, sc,
                        (size_t)(out * (in / 16)), w);
 }
 

@@ -90,6 +90,18 @@ hipError_t launch_quantize_act_q8k(const float* x, int64_t m, int64_t in, int su
   return hipGetLastError();
 }
 
+// Q6_K codes on the device: each 16-code sub-block packed into 12 bytes.
+// Bytes 0..7: byte j holds code j (low nibble) and code j + 8 (high nibble),
+// their low 4 bits; bytes 8..11: byte j holds bits 4..5 of codes j, j + 4,
+// j + 8, j + 12 in its bit pairs 0, 1, 2, 3. p0, p1, p2 are bytes 0..3, 4..7,
+// 8..11 as little-endian words; the result holds codes 4 k .. 4 k + 3 as
+// bytes in word k.
+__device__ __forceinline__ u32x4 unpack_q6k(uint32_t p0, uint32_t p1, uint32_t p2) {
+  return u32x4{(p0 & 0x0F0F0F0Fu) | ((p2 & 0x03030303u) << 4), (p1 & 0x0F0F0F0Fu) | (((p2 >> 2) & 0x03030303u) << 4),
+               ((p0 >> 4) & 0x0F0F0F0Fu) | (((p2 >> 4) & 0x03030303u) << 4),
+               ((p1 >> 4) & 0x0F0F0F0Fu) | (((p2 >> 6) & 0x03030303u) << 4)};
+}
+
 // ---- K-quant GEMV: y[t][o] for MT activation rows t. FMT RQ_Q4_K / RQ_Q6_K.
 // LDS: xq[MT][K] codes, bsums[MT][K/SUB], xs[MT][K/256].
 template <int FMT, int MT, int D>
@@ -118,7 +130,8 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
   const int ngrp = (N + kKqRows - 1) / kKqRows;
   const int ng = gw < ngrp ? (ngrp - 1 - gw) / nwaves + 1 : 0;
   const int nit = (nsub + 63) / 64, nitp = (nit + D - 1) / D * D;
-  constexpr int CODE_ROW = FMT == RQ_Q4_K ? 1 : 2;  // K * CODE_ROW / 2 code bytes per row
+  // code bytes per row: K / 2 (Q4_K nibbles), 3 K / 4 (Q6_K, 12 bytes per 16-code sub-block)
+  const int64_t row_bytes = FMT == RQ_Q4_K ? K / 2 : K / 4 * 3;
   struct Slot {
     u32x4 w[kKqRows];
     uint32_t a[kKqRows], b[kKqRows], c[kKqRows];  // Q4_K: da, db bits, aq | bq << 8; Q6_K: ds bits, sc
@@ -134,7 +147,12 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
 #pragma unroll
     for (int r = 0; r < kKqRows; r++) {
       const int o = min(o0 + r, N - 1);
-      ring[slot].w[r] = *reinterpret_cast<const u32x4*>(wq + (int64_t)o * (K * CODE_ROW / 2) + sb * 16);
+      if (FMT == RQ_Q4_K) {
+        ring[slot].w[r] = *reinterpret_cast<const u32x4*>(wq + (int64_t)o * row_bytes + sb * 16);
+      } else {  // 12 bytes, unpacked when the step computes
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(wq + (int64_t)o * row_bytes + sb * 12);
+        ring[slot].w[r] = u32x4{p[0], p[1], p[2], 0u};
+      }
       if (FMT == RQ_Q4_K) {
         const u32x2 d2 = static_cast<const u32x2*>(sup)[(int64_t)o * nsb + sb / 8];
         ring[slot].a[r] = d2[0];
@@ -204,6 +222,11 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
               f1[r] = 0.0f;
             }
           }
+          // Q6_K: the rows' 16 codes as bytes, unpacked once for all MT rows
+          u32x4 cw[kKqRows];
+#pragma unroll
+          for (int r = 0; r < kKqRows; r++)
+            cw[r] = FMT == RQ_Q6_K ? unpack_q6k(cur.w[r][0], cur.w[r][1], cur.w[r][2]) : cur.w[r];
 #pragma unroll
           for (int t = 0; t < MT; t++) {
             const u32x4 xa = reinterpret_cast<const u32x4*>(lx + t * K)[s * SUB / 16];
@@ -227,7 +250,7 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemv_kernel(
               for (int r = 0; r < kKqRows; r++) {
                 int dp = 0;
 #pragma unroll
-                for (int k = 0; k < 4; k++) dp = __builtin_amdgcn_sdot4((int)cur.w[r][k], (int)xa[k], dp, false);
+                for (int k = 0; k < 4; k++) dp = __builtin_amdgcn_sdot4((int)cw[r][k], (int)xa[k], dp, false);
                 const float v = fmaf(dact * f0[r], (float)(dp - 32 * bs), acc[r][t]);
                 acc[r][t] = live ? v : acc[r][t];
               }
@@ -332,7 +355,10 @@ __global__ __launch_bounds__(256) void kquant_dequant_kernel(const uint8_t* __re
   } else {
     const double a1 = (double)static_cast<const float*>(sup)[o * nsb + k / 256] *
                       (double)static_cast<const int8_t*>(subsc)[o * (K / 16) + k / 16];
-    out[e] = (float)(a1 * (double)((int)wq[o * K + k] - 32));
+    const int64_t s = k / 16, j = k % 16;
+    const uint8_t* sbp = wq + o * (K / 4 * 3) + s * 12;
+    const uint32_t lo = (sbp[j % 8] >> (j < 8 ? 0 : 4)) & 0xFu, hi = (sbp[8 + j % 4] >> (2 * (j / 4))) & 3u;
+    out[e] = (float)(a1 * (double)((int)(lo | (hi << 4)) - 32));
   }
 }
 

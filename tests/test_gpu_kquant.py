@@ -238,6 +238,13 @@ def test_kquant_rejects(torch, ctx, orc):
              zf.ctypes.data_as(C.c_void_p), z8.ctypes.data_as(C.c_void_p), z8.ctypes.data_as(C.c_void_p), 4, 192,
              C.byref(h))
     assert e.value.status == RQ_ERR_SHAPE
+    # Q6_K codes are 6-bit (the device packs them): a byte above 63 is refused
+    wq6, sc6, ds6 = encode(orc, "q6k", 4, 256, seed=2)
+    wq6 = wq6.copy()
+    wq6[5] = 64
+    with pytest.raises(RqError) as e:
+        raster_amd.QWeight.q6k(wq6, sc6, ds6, 4, 256, ctx)
+    assert e.value.status == RQ_ERR_SHAPE
     # in = 32512: four Q6_K activation rows no longer fit the GEMV's LDS
     z8, zs, zf = np.zeros(4 * 32512, np.uint8), np.zeros(4 * 32512 // 16, np.int8), np.zeros(4 * 127, np.float32)
     with pytest.raises(RqError) as e:
