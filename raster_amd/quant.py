@@ -196,7 +196,9 @@ class QWeight:
 
     # ---- compute --------------------------------------------------------------
     def matmul(self, x, y=None, out_dtype=None, stream=None):
-        """y[m, out] = x[m, in] . dequant(W)^T on the device (x: torch f32/bf16 CUDA tensor)."""
+        """y[m, out] = x[m, in] . dequant(W)^T on the device (x: torch f32/bf16 CUDA tensor).
+        K-quant weights (Q4_K, Q6_K) take f32 x, quantized to q8_K inside the
+        call: the same bits as quantize_act_q8k + matmul_q8k."""
         import torch
 
         _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous CUDA tensor")
