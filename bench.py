@@ -439,10 +439,13 @@ def dense_lines(torch, ctx, warmup=20, calls=100):
 
 def dx_lines(torch, ctx, calls=20):
     """Backward-data (qlinear-q8-dx) of the C2 layer's weight (Q8_0, in 4096,
-    out 11008) at m = 16 and m = 512 dy rows: the MFMA GEMM path. `kernel_us`
-    spans the dy packing pass, the GEMM and the slice reduction (librq's kernel
-    timing); `tflops` counts 2 m in out; the GEMM issues three bf16 MFMAs per
-    product (hi/lo operand splits), so `frac_mfma` = 3 x tflops / dense peak."""
+    out 11008) at m = 4, 16 and 512 dy rows. `kernel_us` spans every kernel of
+    the call (librq's kernel timing). m <= 32 runs the f32 MFMA kernel on the
+    weight as stored, read once per 16 dy rows: `frac_hbm` = weight bytes /
+    time / 8 TB/s, `frac_f32_mfma` = the f32 MFMA work it issues (2 x 16 x
+    ceil(m / 16) x in x out) / 157.3 TFLOP/s. m = 512 runs the bf16 MFMA GEMM,
+    three bf16 MFMAs per product (hi/lo operand splits): `frac_mfma` = 3 x
+    tflops / dense bf16 peak."""
     import raster_amd
 
     out_, in_ = 11008, 4096
@@ -450,8 +453,9 @@ def dx_lines(torch, ctx, calls=20):
 
     codes, scales = wl.q8_weights(out_, in_, seed=41)
     w = raster_amd.QWeight.q8(codes, scales, out_, in_, ctx)
+    wbytes = q8_bytes(0, in_, out_, 0, 0)
     lines = {}
-    for m in (16, 512):
+    for m in (4, 16, 512):
         g = torch.Generator(device="cuda").manual_seed(m)
         dy = torch.randn(m, out_, device="cuda", dtype=torch.float32, generator=g)
         dx = torch.empty(m, in_, device="cuda", dtype=torch.float32)
@@ -467,9 +471,16 @@ def dx_lines(torch, ctx, calls=20):
         ctx.set_kernel_timing(False)
         us = total / max(n, 1) * 1e3
         tflops = 2.0 * m * in_ * out_ / us / 1e6
-        lines[f"dx_q8_m{m}_4096x11008"] = {"m": m, "in": in_, "out": out_, "kernel_us": round(us, 3),
-                                           "tflops": round(tflops, 3),
-                                           "frac_mfma": round(3 * tflops / BF16_PEAK_TFLOPS, 4)}
+        ln = {"m": m, "in": in_, "out": out_, "kernel_us": round(us, 3), "tflops": round(tflops, 3)}
+        if m <= 32:
+            issued = 2.0 * 16 * -(-m // 16) * in_ * out_ / us / 1e6
+            ln.update(kernel="rq::dx_fm_kernel (f32 MFMA, weight as stored)", weight_bytes=wbytes,
+                      frac_hbm=round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                      frac_f32_mfma=round(issued / FP32_PEAK_TFLOPS, 4))
+        else:
+            ln.update(kernel="rq::dx_mf_kernel (bf16 MFMA GEMM, hi/lo splits)",
+                      frac_mfma=round(3 * tflops / BF16_PEAK_TFLOPS, 4))
+        lines[f"dx_q8_m{m}_4096x11008"] = ln
     w.destroy()
     return lines
 

@@ -360,15 +360,16 @@ int rq_qlinear_q8(rq_ctx ctx, const float* x, const int8_t* codes, const float* 
  * (raster/quant/train.clj:110-137, the pullback of qlinear-q8,
  * train.clj:143-155): dx[m, in] = dy[m, out] . dequant(W), i.e. dx[m, i] =
  * sum_o scale[o, i/32] * code[o, i] * dy[m, o], each w = scale * code
- * rounded to f32 as Raster does. m < 16: each w * dy rounded to f32, summed
- * in f32 (Raster: double). m >= 16 (a bf16 MFMA GEMM that reads the weight
- * once per 128 dy rows): w and dy each carried as bf16 hi + lo (relative
- * 2^-16), the products hi*hi + hi*lo + lo*hi summed in f32, each within about
- * 3 * 2^-16 of the f32 product. Q8_0 or Q4_0 (code = nibble - 8) weights;
- * device f32 buffers, dx 16-byte aligned, fully overwritten; results do not
- * depend on scheduling. Splits the reduction over `out` into slices whose
- * partial sums, like the m >= 16 path's packed dy, use per-stream scratch
- * (grown outside capture only, like rq_qmatmul). */
+ * rounded to f32 as Raster does. m <= 32 (f32 MFMA on the weight as stored,
+ * read once per 16 dy rows): the products w * dy formed and summed in f32
+ * (Raster: each rounded to f32, summed in double). m > 32 (a bf16 MFMA GEMM
+ * that reads the weight once per 128 dy rows): w and dy each carried as bf16
+ * hi + lo (relative 2^-16), the products hi*hi + hi*lo + lo*hi summed in f32,
+ * each within about 3 * 2^-16 of the f32 product. Q8_0 or Q4_0 (code =
+ * nibble - 8) weights; device f32 buffers, dx 16-byte aligned, fully
+ * overwritten; results do not depend on scheduling. Splits the reduction over
+ * `out` into slices whose partial sums, like the m > 32 path's packed dy, use
+ * per-stream scratch (grown outside capture only, like rq_qmatmul). */
 int rq_qmatmul_dx(rq_ctx ctx, rq_weight w, const float* dy, float* dx, int64_t m, void* stream);
 
 /* qlinear-q8-dx with its own argument list (dy codes scales m in out) on host

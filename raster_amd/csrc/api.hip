@@ -1108,10 +1108,10 @@ int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m,
   if (((uintptr_t)dx & 15) != 0) return fail(RQ_ERR_SHAPE, "dx must be 16-byte aligned");
   if (int s = set_device(c)) return s;
   const hipStream_t st = (hipStream_t)stream;
-  // m >= kDxMfMinRows: the MFMA GEMM (weight read once per 128 dy rows);
-  // below it the VALU kernel, which reads the weight once per few rows
-  const bool mf = m >= kDxMfMinRows;
-  const int slices = mf ? dx_mf_slices(m, w.in, w.npad, c->cu_count) : dx_slices(w.in, w.npad, c->cu_count);
+  // m <= kDxFmMaxRows: f32 MFMA on the weight as stored (weight read once per
+  // 16 dy rows); above it the bf16 MFMA GEMM (once per 128 rows)
+  const bool mf = m > kDxFmMaxRows;
+  const int slices = mf ? dx_mf_slices(m, w.in, w.npad, c->cu_count) : dx_fm_slices(m, w.in, w.npad, c->cu_count);
   float* part = nullptr;
   void* pack = nullptr;
   if (slices > 1) {
@@ -1121,7 +1121,7 @@ int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m,
     if (int s = stream_pack(c, st, dx_mf_pack_bytes(m, w.npad), &pack)) return s;
   const auto ev = timing_pair(c, st);
   if (ev.first) (void)hipEventRecord(ev.first, st);
-  hipError_t e = mf ? launch_dx_mf(w, dy, dx, m, pack, part, slices, st) : launch_dx(w, dy, dx, m, part, slices, st);
+  hipError_t e = mf ? launch_dx_mf(w, dy, dx, m, pack, part, slices, st) : launch_dx_fm(w, dy, dx, m, part, slices, st);
   if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, st);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "dx launch");

@@ -183,15 +183,16 @@ size_t kquant_gemv_lds(int format, int64_t k, int mt);
 hipError_t launch_kquant_gemv(const Weight& w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
                               int y_dtype, int64_t m, int cu_count, hipStream_t stream);
 hipError_t launch_kquant_dequant(const Weight& w, float* out, hipStream_t stream);
-// backward-data (dx.hip): row-group slices and the launch (part: slices * m * in
-// f32 when slices > 1)
-int dx_slices(int64_t in, int64_t npad, int cu_count);
-hipError_t launch_dx(const Weight& w, const float* dy, float* dx, int64_t m, float* part, int slices,
-                     hipStream_t stream);
-// backward-data on bf16 MFMA for m >= kDxMfMinRows (dx_mf.hip): dy packed
+// backward-data on f32 MFMA for m <= kDxFmMaxRows (dx.hip): the weight as
+// stored feeds the MFMA's B operand; column tiles x dy-row tiles x slices of
+// the row groups (part: slices * m * in f32 when slices > 1)
+constexpr int64_t kDxFmMaxRows = 32;
+int dx_fm_slices(int64_t m, int64_t in, int64_t npad, int cu_count);
+hipError_t launch_dx_fm(const Weight& w, const float* dy, float* dx, int64_t m, float* part, int slices,
+                        hipStream_t stream);
+// backward-data on bf16 MFMA for m > kDxFmMaxRows (dx_mf.hip): dy packed
 // into `pack` (dx_mf_pack_bytes), reduction slices (part: slices * m * in f32
 // when slices > 1)
-constexpr int64_t kDxMfMinRows = 16;
 size_t dx_mf_pack_bytes(int64_t m, int64_t npad);
 int dx_mf_slices(int64_t m, int64_t in, int64_t npad, int cu_count);
 hipError_t launch_dx_mf(const Weight& w, const float* dy, float* dx, int64_t m, void* pack, float* part, int slices,

@@ -1,12 +1,13 @@
 """GPU parity of the backward-data matmul (rq_qmatmul_dx, rq_qlinear_q8_dx)
 against the C oracle's qlinear-q8-dx (raster/quant/train.clj:110-137).
 
-dx[m, i] = sum_o scale[o, i/32] * code[o, i] * dy[m, o]. Below 16 dy rows the
-per-term products are rounded to f32 as Raster does and summed in f32 (Raster:
-double); from 16 rows the MFMA GEMM carries w = scale * code (Raster's f32
-product) and dy each as bf16 hi + lo (relative 2^-16) and adds hi*hi + hi*lo +
-lo*hi in f32, so each product is within about 3 * 2^-16 of the f32 one (about
-4e-6 normwise measured). Both: normwise max|dx - ref| / max|ref| < 2e-5. Q4_0
+dx[m, i] = sum_o scale[o, i/32] * code[o, i] * dy[m, o]. Up to 32 dy rows an
+f32 MFMA kernel takes w = scale * code (Raster's f32 product) as stored and
+forms and sums the products w * dy in f32 (Raster: double); above 32 rows the
+bf16 MFMA GEMM carries w and dy each as bf16 hi + lo (relative 2^-16) and adds
+hi*hi + hi*lo + lo*hi in f32, so each product is within about 3 * 2^-16 of
+the f32 one (about 4e-6 normwise measured). Both: normwise max|dx - ref| /
+max|ref| < 2e-5. Q4_0
 (Raster has no Q4 dx) is checked against a float64 product with the bit-exact
 Q4_0 dequant. The adjoint identity <dy, W x> = <dx, x> pins the transpose
 independently of the oracle's dx.
@@ -66,7 +67,7 @@ def test_dx_q8(torch, ctx, orc, m, in_, out):
 
 
 @pytest.mark.parametrize("scale_kind", ["f16", "f32"])
-@pytest.mark.parametrize("m,in_,out", [(1, 4096, 14336), (4, 160, 48)])
+@pytest.mark.parametrize("m,in_,out", [(1, 4096, 14336), (4, 160, 48), (16, 4096, 14336), (25, 512, 96)])
 def test_dx_q4(torch, ctx, orc, m, in_, out, scale_kind):
     import raster_amd
 
@@ -113,14 +114,15 @@ def test_qlinear_q8_dx_host_surface(torch, ctx, orc):
     assert orc.normwise_relerr(dx, ref) < TOL
 
 
-# ------------------------------------------------ MFMA GEMM path (m >= 16)
-@pytest.mark.parametrize("m,in_,out", [(16, 256, 200), (100, 256, 200), (130, 1056, 48), (512, 1024, 2048),
-                                       (33, 4096, 11008)])
+# ---------------------------------- f32 MFMA (m <= 32) and bf16 MFMA GEMM (m > 32)
+@pytest.mark.parametrize("m,in_,out", [(16, 256, 200), (32, 1056, 48), (31, 4096, 11008), (33, 256, 200),
+                                       (100, 256, 200), (130, 1056, 48), (512, 1024, 2048), (48, 4096, 11008)])
 def test_dx_mfma_q8(torch, ctx, orc, m, in_, out):
-    # 16: the smallest m on the MFMA path; 100 / 130: a partial last row tile;
-    # in 1056: 33 blocks, a partial last column tile; out 200 / 48: a partial
-    # last 16-row group and an odd group count; (512, 1024, 2048), (33, ..,
-    # 11008): the reduction cut into slices
+    # f32 MFMA: 16, 32 (two dy-row tiles), 31 (a partial second tile, the C2
+    # layer's weight, slices); bf16 GEMM: 33 (the smallest m there), 100 /
+    # 130 (a partial last row tile), (512, 1024, 2048) and (48, .., 11008)
+    # (the reduction cut into slices); in 1056: 33 blocks, a partial last
+    # column tile; out 200 / 48: a partial last 16-row group
     import raster_amd
 
     codes, scales = wl.q8_weights(out, in_, seed=out + 1)
