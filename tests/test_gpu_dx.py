@@ -180,3 +180,24 @@ def test_dx_mfma_q4(torch, ctx, orc, scale_kind):
     W = orc.dequant_q4(packed, sc16, in_, out).reshape(out, in_).astype(np.float64)
     ref = dy.reshape(m, out).astype(np.float64) @ W
     assert orc.normwise_relerr(dx, ref) < TOL
+
+
+@pytest.mark.parametrize("m", [5, 20])
+def test_dx_dy_4_byte_aligned(torch, ctx, orc, m):
+    # dy only 4-byte aligned (the entry's requirement), out not a multiple of 4:
+    # the f32 MFMA kernel reads dy one float at a time
+    import raster_amd
+
+    in_, out = 512, 201
+    codes, scales = wl.q8_weights(out, in_, seed=51)
+    dy = wl.activations(m, out, seed=52)
+    buf = torch.empty(m * out + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = dev(torch, dy)
+    dyv = buf[1:]
+    assert dyv.data_ptr() % 16 == 4
+    note(f"dx q8 m={m} in={in_} out={out}, dy at a 4-byte offset")
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    dx = w.matmul_dx(dyv).cpu().numpy()
+    w.destroy()
+    ref = orc.qlinear_q8_dx(dy, codes, scales, m, in_, out).reshape(m, in_)
+    assert orc.normwise_relerr(dx, ref) < TOL
