@@ -23,7 +23,7 @@
 //   Q6_K  ds * d_act * sum_j sc_j * (dot_j - 32 * bsum_j)
 // with the sub-block dots exact in int32 (v_dot4 over packed bytes: nibbles
 // and 6-bit codes are non-negative int8). The terms are added in f32 (Raster
-// adds in double). HBM-bound on the codes: a wave takes RW rows at a time,
+// adds in double). HBM-bound on the codes: a wave takes kKqRows rows at a time,
 // its lanes one sub-block each (16 code bytes, one load) strided by 64, the
 // activations of up to 4 rows staged in LDS once per workgroup.
 #include <algorithm>
@@ -36,7 +36,10 @@ namespace rq {
 namespace {
 
 constexpr int kKqThreads = 256;
-constexpr int kKqRows = 4;  // weight rows a wave takes at a time
+// weight rows a wave takes at a time (14336 x 4096, m = 1, cold, rows 1 / 2 /
+// 4 / 8: Q4_K 12.1 / 10.3 / 11.3 / 12.7 us, Q6_K 15.7 / 12.5 / 13.8 / 14.4 us;
+// m = 4 likewise best at 2)
+constexpr int kKqRows = 2;
 
 __device__ __forceinline__ float wave_sum64(float v) {
 #pragma unroll
