@@ -61,7 +61,9 @@ cores (at most 16, the box's share) over a row sample of C2, in TFLOP/s.
 `legs` times B1 and B2 (quantize-act-i8 + the x8 dpbusd GEMV, Raster's
 production int8 route; Q8 and Q4_0 tiles) at 1 thread (Raster's default
 RASTER_DECODE_THREADS) and at all cores, on the C1, C3, C2 and C5 (M = 1)
-shapes, each leg about one second; `cpu_model` names the host CPU.
+shapes, each leg about one second; `cpu_model` names the host CPU. The legs
+re-read one weight buffer, so small shapes run from the host's last-level
+cache (warm), unlike the GPU decode lines (cold).
 
 Multi-GPU runs are not part of this build: --gpus above 1 exits with a message.
 """
@@ -787,7 +789,11 @@ def cpu_baseline(leg_s=1.0, head_s=10.0):
     return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"B1 qlinear-q8 loop (f32 products, f64 accumulation) over {rows} activation rows of the C2 "
                       f"GEMM (K={K}, N={N}) in {dt:.2f} s on {cores} threads; TFLOP/s of that sample",
-            "cpu_model": cpu_model(), "vnni": bool(L.rqb_have_vnni()), "legs": legs}
+            "cpu_model": cpu_model(), "vnni": bool(L.rqb_have_vnni()),
+            "note": ("every leg re-reads one weight buffer: up to tens of MB it stays in the host's last-level "
+                     "cache, so weight_GBs is a warm rate and can exceed DRAM bandwidth; the GPU decode lines "
+                     "rotate copies past the 256 MB MALL (cold)"),
+            "legs": legs}
 
 
 def headline(torch, ctx, args):
