@@ -8,7 +8,9 @@ Without --force only objects older than their source or a shared header are
 rebuilt. Packed-FP32 instruction selection is switched off
 (-packed-fp32-ops) for every device compile; hipcc's host pass warns that it
 does not know that feature, which is harmless. MFMA accumulators are kept in
-VGPRs (-amdgpu-mfma-vgpr-form).
+VGPRs (-amdgpu-mfma-vgpr-form), except in the files of AGPR_SOURCES, whose
+kernels run one wave per SIMD with accumulator tiles larger than the 256
+architectural VGPRs.
 """
 from __future__ import annotations
 
@@ -33,6 +35,8 @@ FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
 ]
+# one wave per SIMD, 192-224 accumulator registers per lane: those live in AGPRs
+AGPR_SOURCES = {"gemm_wide.hip"}
 # the dense f32 GEMM entries call rocBLAS (dense.hip)
 LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 
@@ -55,9 +59,24 @@ def _stale(src: str, obj: str) -> bool:
     return any(os.path.getmtime(p) > t for p in [src, *HEADERS])
 
 
+def flags_for(src: str) -> list[str]:
+    if os.path.basename(src) not in AGPR_SOURCES:
+        return list(FLAGS)
+    out, skip = [], False
+    for i, f in enumerate(FLAGS):
+        if skip:
+            skip = False
+            continue
+        if f == "-mllvm" and i + 1 < len(FLAGS) and FLAGS[i + 1] == "-amdgpu-mfma-vgpr-form":
+            skip = True
+            continue
+        out.append(f)
+    return out
+
+
 def _compile(src: str, obj: str) -> tuple[str, int, list[str]]:
     tmp = obj + ".tmp"
-    r = subprocess.run([hipcc(), *FLAGS, "-c", "-o", tmp, src], capture_output=True, text=True)
+    r = subprocess.run([hipcc(), *flags_for(src), "-c", "-o", tmp, src], capture_output=True, text=True)
     errs = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
     if r.returncode == 0:
         os.replace(tmp, obj)

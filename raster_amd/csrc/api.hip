@@ -4,6 +4,7 @@
 // by one mutex, so a destroyed, double-freed or foreign handle is reported as
 // RQ_ERR_HANDLE instead of being dereferenced. Errors carry a message in a
 // thread-local string (rq_last_error).
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <new>
@@ -45,6 +46,12 @@ struct Ctx {
     size_t attn_bytes = 0;
   };
   std::unordered_map<hipStream_t, StreamScratch> scratch;
+  // Scratch buffers replaced by larger ones. A graph captured on a stream
+  // keeps the addresses it was captured with, so a buffer that grew is kept
+  // until the context is destroyed rather than freed: replaying such a graph
+  // after a larger call still finds its memory. (Growth is by at least 25%
+  // each time, so the retired buffers total at most four times the largest.)
+  std::vector<void*> retired;
   // rocBLAS handle of the dense f32 GEMM entries, created on first use; the
   // mutex covers setting its stream and enqueueing one call
   void* blas = nullptr;
@@ -186,21 +193,17 @@ static const char* kCaptureScratch =
     "call on the stream once before capturing";
 
 // Replaces *buf (sized *have) by a fresh allocation of at least `bytes`
-// (+25%). The old buffer may still be read by kernels queued on the stream.
-static int regrow(hipStream_t stream, size_t bytes, void** buf, size_t* have) {
-  if (*buf) {
-    const hipError_t se = hipStreamSynchronize(stream);
-    if (se != hipSuccess) return hip_fail(se, "hipStreamSynchronize");
-    (void)hipFree(*buf);
-    *buf = nullptr;
-    *have = 0;
-  }
+// (+25%). The old buffer is retired, not freed: kernels queued on the stream
+// and graphs captured earlier may still use it (freed at rq_ctx_destroy).
+// Caller holds g_mu.
+static int regrow(Ctx* c, size_t bytes, void** buf, size_t* have) {
   const size_t want = bytes + bytes / 4;
   void* p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess || !p) {
     (void)hipGetLastError();
     return fail(RQ_ERR_OOM, "hipMalloc of " + std::to_string(want) + " bytes of scratch failed");
   }
+  if (*buf) c->retired.push_back(*buf);
   *buf = p;
   *have = want;
   return RQ_OK;
@@ -212,7 +215,7 @@ static int stream_pack(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
   auto& e = c->scratch[stream];
   if (e.pack_bytes < bytes) {
     if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
-    if (int s = regrow(stream, bytes, &e.pack, &e.pack_bytes)) return s;
+    if (int s = regrow(c, bytes, &e.pack, &e.pack_bytes)) return s;
   }
   *out = e.pack;
   return RQ_OK;
@@ -224,7 +227,7 @@ static int stream_split(Ctx* c, hipStream_t stream, size_t part_bytes, float** p
   auto& e = c->scratch[stream];
   if (e.red_bytes < part_bytes) {
     if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
-    if (int s = regrow(stream, part_bytes, &e.red, &e.red_bytes)) return s;
+    if (int s = regrow(c, part_bytes, &e.red, &e.red_bytes)) return s;
   }
   *part = static_cast<float*>(e.red);
   return RQ_OK;
@@ -236,7 +239,7 @@ static int stream_attn(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
   auto& e = c->scratch[stream];
   if (e.attn_bytes < bytes) {
     if (capturing(stream)) return fail(RQ_ERR_SHAPE, kCaptureScratch);
-    if (int s = regrow(stream, bytes, &e.attn, &e.attn_bytes)) return s;
+    if (int s = regrow(c, bytes, &e.attn, &e.attn_bytes)) return s;
   }
   *out = e.attn;
   return RQ_OK;
@@ -368,6 +371,7 @@ int rq_ctx_destroy(rq_ctx h) {
     (void)hipFree(kv.second.red);
     (void)hipFree(kv.second.attn);
   }
+  for (void* p : c->retired) (void)hipFree(p);
   timing_release(c);
   {
     std::lock_guard<std::mutex> bl(c->blas_mu);
@@ -864,6 +868,11 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   // the m = 1 GEMV also quantizes to int8 blocks itself (act_i8)
   const bool plain_g1 = !dops.norm_gain && !dops.residual && !dops.swiglu;
   const G1Plan g1 = plain_g1 && plan.ok ? plan_gemv1(m, w.in, w.npad, x_dtype, w.format, c->cu_count) : G1Plan{};
+  // bf16 x past the decode and small-m kernels: the 256 x 192 GEMM where its
+  // plan takes the shape
+  const WidePlan wide = !plan.ok && x_dtype == RQ_BF16 && !gemm_sm_takes(w.format, m, w.in)
+                            ? plan_gemm_wide(m, w.in, w.npad, c->cu_count)
+                            : WidePlan{};
   void* part = nullptr;
   if (g1.ok) {
     // the m = 1 GEMV uses no scratch
@@ -874,9 +883,13 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     }
   } else if (plan.ok && plan.ksplit > 1) {
     if (int s = call_scratch(c, fixed, a.stream, plan.part_bytes, 1, &part)) return s;
+  } else if (!plan.ok && x_dtype == RQ_BF16 && wide.ok) {
+    // the 32x32x16 operand copy of x: ceil(m/32)*32 rows
+    if (int s = call_scratch(c, fixed, a.stream, pack_x32_bytes(m, w.in), 0, &a.scratch)) return s;
   } else if (!plan.ok && x_dtype == RQ_BF16) {
-    // fragment-major copy of the activations: ceil(m/16)*16 rows
-    const size_t bytes = (size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2;
+    // fragment-major copy of the activations: ceil(m/16)*16 rows (16x16x32
+    // operands), or ceil(m/32)*32 rows for the 32x32x16 K-pair kernel
+    const size_t bytes = std::max((size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2, pack_x32_bytes(m, w.in));
     if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
     if (gemm_sm_takes(w.format, m, w.in)) {
       a.slices = gemm_sm_slices(w.format, m, w.in, w.npad, c->cu_count);
@@ -901,7 +914,8 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
                  : plan.ok            ? launch_gemv(a, plan)
                  : x_dtype == kXtI8   ? launch_gemm_i8(a, c->cu_count)
                  : x_dtype == RQ_BF16 ? (gemm_sm_takes(w.format, m, w.in) ? launch_gemm_sm(a, a.slices)
-                                                                    : launch_gemm_bf16(a, c->cu_count))
+                                         : wide.ok ? launch_gemm_wide(a, wide)
+                                                 : launch_gemm_bf16(a, c->cu_count))
                                       : launch_gemm(a, c->cu_count);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");

@@ -754,7 +754,10 @@ static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
         best = i;
       }
     }
-    if (best == 0) return launch_wk<FMT, ST, 6>(a);
+    // 256 x 96: the K-pair kernel on 32x32x16 MFMA (gemm_wide.hip; C2 step
+    // 52.5 against 54.2 us for gemm_wk_kernel, same box and data) where K is
+    // a whole number of its 64-k macro steps
+    if (best == 0) return (a.k % 64 == 0) ? launch_gemm_pair(a) : launch_wk<FMT, ST, 6>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
     if (best == 2) return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
     return launch_wk<FMT, ST, 7>(a);

@@ -171,6 +171,18 @@ bool gemm_sm_takes(int format, int64_t m, int64_t k);
 hipError_t launch_gemm_sm(const MatmulArgs& a, int ks);
 // int8 activations (x_dtype kXtI8, scales / sums in a.ops), m > 16 (gemm_i8.hip)
 hipError_t launch_gemm_i8(const MatmulArgs& a, int cu_count);
+// bf16 x, m > 128: 256 x 192 tiles on 32x32x16 MFMA, one wave per SIMD
+// (gemm_wide.hip), where its tiles fill their rounds of the CUs
+struct WidePlan {
+  bool ok;
+  int tiles_m, tiles_n;
+};
+WidePlan plan_gemm_wide(int64_t m, int64_t k, int64_t npad, int cu_count);
+// bytes of the 32x32x16 operand copy of x (rows rounded up to 32)
+size_t pack_x32_bytes(int64_t m, int64_t k);
+hipError_t launch_gemm_wide(const MatmulArgs& a, const WidePlan& p);
+// 256 x 96 tiles, eight waves in K pairs (gemm_wide.hip)
+hipError_t launch_gemm_pair(const MatmulArgs& a);
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).
 hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);
