@@ -161,12 +161,18 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    codes, v_mfma_i32_16x16x64_i8);
  *  - m > 16: bf16 x: the bf16 MFMA GEMM (the weight-stream GEMM for Q4_0
  *    at 16 < m <= 64 and for Q8_0 at 16 < m <= 48, or <= 64 when
- *    in >= 8192); f32 x: the exact-code f32 GEMM;
+ *    in >= 8192; for m > 128 and in % 64 == 0, 256 x 192 tiles with one
+ *    wave per SIMD where they fill their rounds of the CUs to 80%, else the
+ *    cost model's tile, 256 x 96 on the K-pair kernel); f32 x: the
+ *    exact-code f32 GEMM;
  *  - Q4_K / Q6_K weights (f32 x only, any m; bf16 x fails with RQ_ERR_DTYPE):
  *    x is quantized to q8_K in scratch and the K-quant GEMV runs, the same two
  *    kernels as rq_quantize_act_q8k + rq_qmatmul_q8k and bit for bit their
  *    results (QMatrix apply of the built-in :q4_K / :q6_K formats,
- *    raster/quant/core.clj:55-75).
+ *    raster/quant/core.clj:55-75). The GEMV takes four activation rows per
+ *    pass over the weight, so a call streams the weight ceil(m / 4) times:
+ *    meant for decode (m <= 16); at prefill sizes (m = 512: 128 passes) its
+ *    time grows with m.
  *
  * Numerics (all accumulation in f32):
  *  - v_dot4 GEMV and int8-level decode kernel: each 32-block of each
@@ -184,16 +190,16 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    NaN; a non-finite activation makes its row's outputs non-finite.
  *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
  *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA;
- *    on the GEMM's eight-wave tiles (m > 128 where the tile cost model picks
- *    them) K is summed as two f32 partial sums, of the even and of the odd
- *    32-blocks, added at the end.
+ *    on the eight-wave tiles (m > 128 where the tile cost model picks them;
+ *    the K-pair kernel) K is summed as two f32 partial sums, of the even and
+ *    of the odd 32-blocks, added at the end.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
  *    split into two bf16 terms (about 16 mantissa bits).
  *
  * Scratch (per stream, allocated on first use, grown on demand, freed by
  * rq_ctx_destroy; calls on one stream are ordered, calls on different streams
  * do not share it):
- *  - bf16 x with m > 16: the packed activation tile, ceil(m/16)*16*in*2 bytes;
+ *  - bf16 x with m > 16: the packed activation tile, ceil(m/32)*32*in*2 bytes;
  *  - K-slices' partial sums, m * out * 4 bytes per slice, added in slice
  *    order by a second kernel: the int8-level decode kernel when a row of x
  *    does not fit one workgroup's LDS (in above 17472 at m <= 4, 8704 at
@@ -206,7 +212,11 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    bytes (each part rounded up to 256), sub = 32 for Q4_K, 16 for Q6_K.
  * Under HIP graph capture nothing can be allocated: run the same (or a
  * larger) shape once on the capturing stream before capturing, otherwise the
- * call fails with RQ_ERR_SHAPE and a message saying so.
+ * call fails with RQ_ERR_SHAPE and a message saying so. A buffer that grows is
+ * replaced but not freed until rq_ctx_destroy, so a graph captured before a
+ * larger call still replays on its own (still allocated) buffers; graphs and
+ * eager calls on one stream share a buffer only while it has not grown, and
+ * are ordered by the stream.
  */
 int rq_qmatmul(rq_ctx ctx, rq_weight w, const void* x, int x_dtype, void* y, int y_dtype, int64_t m,
                void* stream);
@@ -302,6 +312,17 @@ int rq_quantize_act_q8k(rq_ctx ctx, const float* x, int64_t m, int64_t in, int s
 int rq_qmatmul_q8k(rq_ctx ctx, rq_weight w, const int8_t* xq, const float* xs, const int32_t* bsums, void* y,
                    int y_dtype, int64_t m, void* stream);
 
+/* The raw int8 GEMV core, i8gemv-dp4a! (raster/quant/kernels_k.clj:141-150):
+ * y[o] = (float) sum_w dp4a(wp[o*kw + w], xp[w]) for o < out, where wp is
+ * int32[out*kw] and xp int32[kw], each word four little-endian signed int8
+ * lanes (par/dp4a, raster/par.clj:421-440). The sum is exact (Raster: a
+ * 64-bit long) and converted to f32 once, round to nearest even. Unscaled:
+ * no block scales, no zero point. Device pointers, 4-byte aligned (wp and
+ * xp may be NULL when kw is 0: y is then all zeros); y fully overwritten;
+ * kw <= 2^21. */
+int rq_i8gemv_dp4a(rq_ctx ctx, const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out,
+                   void* stream);
+
 /* Raster's activation quantizer on the device (quantize-act-i8,
  * raster/compiler/backend/cpu/quant.clj:282-305,399-415): per row of x
  * f32[m*in] and 32-element block b, d = max|x| / 127 (in double), q =
@@ -345,8 +366,11 @@ int rq_decode_attention(rq_ctx ctx, const float* q, const float* k, const float*
                         int64_t pos, int64_t n_q, int64_t n_kv, int64_t head_dim, double theta, double scale,
                         float* out, void* stream);
 
-/* Writes the dequantized f32 weight W[out*in] (device pointer) using the same
- * device-side decode as the matmul kernels. Replaces dequant-q8-dense
+/* Writes the dequantized f32 weight W[out*in] (device pointer): the exact f32
+ * product scale * code (one IEEE rounding; Q4_0: scale * (q - 8)). The bf16
+ * GEMMs feed the MFMA this same value rounded to bf16 (RNE); the exact-code
+ * kernels (decode, f32-x GEMM, int8 paths) multiply the codes exactly and
+ * apply the scale to the block's partial sum instead. Replaces dequant-q8-dense
  * (raster/quant/train.clj:60-71) and the Q4_0 dequant
  * (test/raster/compiler/backend/cpu/quant_encode_test.clj:9-24). */
 int rq_dequant(rq_ctx ctx, rq_weight w, float* w_out, void* stream);

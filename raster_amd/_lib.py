@@ -50,6 +50,7 @@ SIGNATURES = {
     "rq_qmatmul_i8": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
     "rq_quantize_act_q8k": ([_p, _p, _i64, _i64, _i, _p, _p, _p, _p], _i),
     "rq_qmatmul_q8k": ([_p, _p, _p, _p, _p, _p, _i, _i64, _p], _i),
+    "rq_i8gemv_dp4a": ([_p, _p, _p, _p, _i64, _i64, _p], _i),
     "rq_decode_attention": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, C.c_double, C.c_double, _p, _p], _i),
     "rq_dequant": ([_p, _p, _p, _p], _i),
     "rq_qlinear_q8": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i),

@@ -776,12 +776,12 @@ static int run_kquant_matmul(Ctx* c, const Weight& w, const float* x, void* y, i
   const int sub = w.format == RQ_Q4_K ? 32 : 16;
   const size_t xq_b = align256((size_t)m * (size_t)w.in), xs_b = align256((size_t)m * (size_t)(w.in / 256) * 4);
   const size_t bs_b = (size_t)m * (size_t)(w.in / sub) * 4;
+  if (int s = set_device(c)) return s;  // before the scratch: growing it allocates on this device
   void* buf = nullptr;
   if (int s = call_scratch(c, fixed, stream, xq_b + xs_b + bs_b, 0, &buf)) return s;
   int8_t* xq = static_cast<int8_t*>(buf);
   float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(buf) + xq_b);
   int32_t* bs = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(buf) + xq_b + xs_b);
-  if (int s = set_device(c)) return s;
   hipError_t e = launch_quantize_act_q8k(x, m, w.in, sub, xq, xs, bs, stream);
   if (e != hipSuccess) return hip_fail(e, "quantizer launch");
   const auto ev = fixed ? std::pair<hipEvent_t, hipEvent_t>{nullptr, nullptr} : timing_pair(c, stream);
@@ -1218,6 +1218,23 @@ int rq_qlinear_i8(rq_ctx h, const float* x, const uint8_t* wqi, const float* wsi
   rq_weight_destroy(w);
   if (s) t_err = keep;
   return s;
+}
+
+int rq_i8gemv_dp4a(rq_ctx h, const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out,
+                   void* stream) {
+  Ctx* c = reinterpret_cast<Ctx*>(h);
+  if (int s = check_ctx(c)) return s;
+  if (kw < 0 || out < 0) return fail(RQ_ERR_SHAPE, "negative dimension");
+  if (out == 0) return RQ_OK;
+  if (!y || (kw > 0 && (!wp || !xp))) return fail(RQ_ERR_NULL, "wp, xp or y is NULL");
+  if (kw > ((int64_t)1 << 21)) return fail(RQ_ERR_SHAPE, "kw above 2^21 words (the lanes' int32 partial sums)");
+  if (out > ((int64_t)1 << 40) / std::max<int64_t>(kw, 1)) return fail(RQ_ERR_SHAPE, "out * kw too large");
+  if ((((uintptr_t)wp | (uintptr_t)xp) & 3) != 0 || ((uintptr_t)y & 3) != 0)
+    return fail(RQ_ERR_SHAPE, "wp, xp and y must be 4-byte aligned");
+  if (int s = set_device(c)) return s;
+  const hipError_t e = launch_i8gemv_dp4a(wp, xp, y, kw, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "i8gemv launch");
+  return RQ_OK;
 }
 
 int rq_stream_read(rq_ctx h, const void* src, size_t bytes, int wg_per_cu, uint32_t* sink, void* stream) {

@@ -3,7 +3,9 @@
 // the GPU: a plain library GEMM, so rocBLAS does the product (Raster hands
 // the same call to MKL / OpenBLAS cblas_sgemm). Row-major operands map to
 // rocBLAS's column-major call with the operands swapped: C^T = op(B)^T op(A)^T.
-// rocBLAS atomics stay off (its default), so results repeat bit for bit.
+// rocBLAS allows atomics by default (split-K and Stream-K solutions may then
+// sum partial tiles in arrival order); the handle turns them off, so results
+// repeat bit for bit.
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
@@ -26,8 +28,13 @@ __global__ __launch_bounds__(256) void bias_rows_kernel(const float* __restrict_
 
 int dense_create(void** handle) {
   rocblas_handle h = nullptr;
-  const rocblas_status st = rocblas_create_handle(&h);
+  rocblas_status st = rocblas_create_handle(&h);
   if (st != rocblas_status_success) return (int)st;
+  st = rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
+  if (st != rocblas_status_success) {
+    (void)rocblas_destroy_handle(h);
+    return (int)st;
+  }
   *handle = h;
   return 0;
 }

@@ -230,6 +230,9 @@ hipError_t launch_q4k_encode(const float* W, int64_t out, int64_t in, int64_t in
                              uint8_t* aq, int8_t* bq, hipStream_t stream);
 hipError_t launch_q6k_encode(const float* W, int64_t out, int64_t in, uint8_t* wq, int8_t* sc, float* ds,
                              hipStream_t stream);
+// y[o] = (float) sum_w dp4a(wp[o * kw + w], xp[w]) (i8gemv.hip)
+hipError_t launch_i8gemv_dp4a(const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out,
+                              hipStream_t stream);
 // Streaming read of `bytes` (a multiple of 16) for the read-ceiling
 // measurement (stream.hip): `grid` workgroups of 256 threads; sink holds
 // grid * 256 words.

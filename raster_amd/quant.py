@@ -375,6 +375,25 @@ def quantize_act_q8k(ctx: Context, x, in_: int, sub: int, out=None, stream=None)
     return xq, xs, bsums
 
 
+def i8gemv_dp4a(ctx: Context, wp, xp, kw: int, out: int, y=None, stream=None):
+    """rq_i8gemv_dp4a (i8gemv-dp4a!, raster/quant/kernels_k.clj:141-150):
+    y[o] = (float) sum_w dp4a(wp[o*kw + w], xp[w]); wp int32 [out*kw], xp int32
+    [kw] CUDA tensors (four little-endian int8 lanes per word) -> y f32 [out]."""
+    import torch
+
+    _need(wp.is_cuda and xp.is_cuda and wp.dtype == torch.int32 and xp.dtype == torch.int32,
+          "wp and xp must be int32 CUDA tensors")
+    _need(wp.is_contiguous() and xp.is_contiguous() and wp.numel() == out * kw and xp.numel() == kw,
+          "wp must hold out*kw words and xp kw words, contiguous")
+    if y is None:
+        y = torch.empty(out, dtype=torch.float32, device=wp.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(wp.device)
+    call("rq_i8gemv_dp4a", ctx.handle, C.c_void_p(wp.data_ptr()), C.c_void_p(xp.data_ptr()),
+         C.c_void_p(y.data_ptr()), kw, out, _stream_ptr(stream))
+    return y
+
+
 def decode_attention(ctx: Context, q, k, v, kcache, vcache, pos: int, n_q: int, n_kv: int, head_dim: int,
                      theta: float, scale: float, out=None, stream=None):
     """rq_decode_attention: RoPE of q [n_q*head_dim] and k [n_kv*head_dim] at

@@ -269,10 +269,10 @@ def test_decode_attention_rejects_bad_shapes(torch, ctx):
 @pytest.mark.parametrize("n_q,n_kv,hd,pos", [(16, 16, 128, 512), (32, 8, 128, 1000), (4, 4, 16, 300),
                                              (64, 8, 128, 4096)])
 def test_decode_attention_split_repeats_and_graph(torch, ctx, orc, n_q, n_kv, hd, pos):
-    # shapes that split the cached rows over several workgroups per head: the
-    # per-head counters must be zero again after every call, so repeated calls,
-    # and replays of a captured call with eager work in between, give the first
-    # call's output bit for bit
+    # shapes that split the cached rows over several workgroups per head: each
+    # range writes its softmax record, decode_attention_merge_kernel merges the
+    # ranges in range order, so repeated calls, and replays of a captured call
+    # with eager work in between, give the first call's output bit for bit
     import raster_amd
 
     kvd = n_kv * hd
