@@ -241,7 +241,7 @@ class ReadCeiling:
         from raster_amd import _lib
 
         self.torch, self.ctx, self.C, self._lib = torch, ctx, C, _lib
-        self.buf = torch.empty(600 << 20, dtype=torch.uint8, device="cuda")
+        self.buf = torch.zeros(600 << 20, dtype=torch.uint8, device="cuda")
         self.sink = torch.empty(ctx.device_info()["cu_count"] * 16 * 256, dtype=torch.int32, device="cuda")
         self.cache = {}
 
@@ -268,12 +268,50 @@ class ReadCeiling:
                 kms = time_kernels(self.torch, self.ctx, self.step_fn(nbytes, wg))
                 if best is None or kms < best[1]:
                     best = (ms, kms, wg)
+            vms = self.vendor_ms(nbytes)
+            cms = self.vendor_copy_ms(nbytes)
             self.cache[nbytes] = {"bytes": nbytes, "per_call_us": round(best[0] * 1e3, 3),
                                   "kernel_us": round(best[1] * 1e3, 3),
                                   "GBs": round(nbytes / best[1] / 1e6, 1),
                                   "frac_hbm": round(nbytes / best[1] / 1e6 / HBM_PEAK_GBS, 4),
-                                  "wg_per_cu": best[2]}
+                                  "wg_per_cu": best[2],
+                                  "vendor_sum_per_call_us": round(vms * 1e3, 3),
+                                  "vendor_sum_GBs_per_call": round(nbytes / vms / 1e6, 1),
+                                  "vendor_copy_per_call_us": round(cms * 1e3, 3),
+                                  "vendor_copy_read_GBs_per_call": round(nbytes / cms / 1e6, 1)}
         return self.cache[nbytes]
+
+    def vendor_ms(self, nbytes):
+        """torch.sum (PyTorch's own reduction kernel) over the same rotation of
+        cold slices, f32 view: the vendor's read of those bytes, per call in a
+        graph of CALLS launches (launch gaps included, like per_call_us)."""
+        nb = (nbytes + 255) // 256 * 256
+        slots = max(1, self.buf.numel() // nb)
+        views = [self.buf[i * nb:(i + 1) * nb].view(self.torch.float32) for i in range(slots)]
+        acc = self.torch.empty((), dtype=self.torch.float32, device="cuda")
+        st = {"i": 0}
+
+        def step():
+            self.torch.sum(views[st["i"] % slots], dim=0, out=acc)
+            st["i"] += 1
+        ms, _ = time_graph(self.torch, step)
+        return ms
+
+    def vendor_copy_ms(self, nbytes):
+        """Device-to-device copy (the runtime's copy of a tensor) of the same
+        rotation of cold slices into one destination buffer, per call in a graph
+        of CALLS launches: it reads the slice's bytes and writes as many."""
+        nb = (nbytes + 255) // 256 * 256
+        slots = max(1, self.buf.numel() // nb)
+        views = [self.buf[i * nb:(i + 1) * nb] for i in range(slots)]
+        dst = self.torch.empty(nb, dtype=self.torch.uint8, device="cuda")
+        st = {"i": 0}
+
+        def step():
+            dst.copy_(views[st["i"] % slots])
+            st["i"] += 1
+        ms, _ = time_graph(self.torch, step)
+        return ms
 
 
 def path_numerics(fmt, m, k, n, xdt):
@@ -321,15 +359,25 @@ def hbm_line(torch, ctx, name, weights_cold, weights_warm, m, xdt, ydt, ceiling=
     return out
 
 
-def mfma_line(torch, ctx, name, weights, m, xdt, ydt, steps=50, warmup=5):
+def mfma_line(torch, ctx, name, weights, m, xdt, ydt, steps=CALLS, warmup=5, cold=None):
+    """An MFMA-bound shape on one resident weight (warm: it stays in the MALL
+    when it fits) and, given `cold` (a rotation past 2x the MALL), the same
+    shape reading every call's weight from HBM."""
     c = Case(torch, ctx, weights, m, xdt, ydt)
     ms = time_eager(torch, c.step, steps, warmup)
     kms = time_kernels(torch, ctx, c.step, calls=steps)
     tf = c.flops / kms / 1e9
-    return {"workload": name, "fmt": weights.fmt, "m": m, "k": weights.k, "n": weights.n, "x": xdt, "y": ydt,
-            "per_call_us": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3), "TFLOPs": round(tf, 2),
-            "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
-            "TFLOPs_per_call": round(c.flops / ms / 1e9, 2)}
+    out = {"workload": name, "fmt": weights.fmt, "m": m, "k": weights.k, "n": weights.n, "x": xdt, "y": ydt,
+           "calls": steps, "per_call_us": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3), "TFLOPs": round(tf, 2),
+           "frac_bf16_mfma": round(tf / BF16_PEAK_TFLOPS, 4), "TFLOPs_per_call": round(c.flops / ms / 1e9, 2)}
+    if cold is not None:
+        cc = Case(torch, ctx, cold, m, xdt, ydt)
+        cms, cv = time_graph(torch, cc.step)
+        ckms = time_kernels(torch, ctx, cc.step)
+        out["cold"] = {"copies": len(cold.ws), "calls": CALLS, "per_call_us": round(cms * 1e3, 3),
+                       "kernel_us": round(ckms * 1e3, 3), "TFLOPs": round(cc.flops / ckms / 1e9, 2),
+                       "frac_bf16_mfma": round(cc.flops / ckms / 1e9 / BF16_PEAK_TFLOPS, 4), "cv": round(cv, 4)}
+    return out
 
 
 def config_lines(torch, ctx, ceiling):
@@ -354,10 +402,11 @@ def config_lines(torch, ctx, ceiling):
             log(f"C5 {fmt} m={m}: kernel {ln['kernel_us']} us ({ln['frac_hbm']:.3f} of HBM), "
                 f"per call {ln['per_call_us']} us")
             lines.append(ln)
-        cold.destroy()
-        ln = mfma_line(torch, ctx, "C5 70B MLP", one, 256, "bf16", "bf16")
-        log(f"C5 {fmt} m=256: kernel {ln['kernel_us']} us, {ln['TFLOPs']} TFLOP/s ({ln['frac_bf16_mfma']:.3f})")
+        ln = mfma_line(torch, ctx, "C5 70B MLP", one, 256, "bf16", "bf16", cold=cold)
+        log(f"C5 {fmt} m=256: kernel {ln['kernel_us']} us, {ln['TFLOPs']} TFLOP/s ({ln['frac_bf16_mfma']:.3f}); "
+            f"cold {ln['cold']['kernel_us']} us ({ln['cold']['frac_bf16_mfma']:.3f})")
         lines.append(ln)
+        cold.destroy()
         one.destroy()
     return lines
 
@@ -761,11 +810,74 @@ def cpu_baseline(leg_s=1.0, head_s=10.0):
         one()
         return _timed(one, budget)
 
+    def c4_step(route, threads, budget):
+        """The two-layer C4 decode step on the host: per layer RMSNorm, the q / k
+        / v GEMVs, RoPE, attention over the 128 cached rows, the o GEMV and
+        residual, RMSNorm, gate / up, SwiGLU, down and residual. The glue is the
+        oracle's C restatement of Raster's (nn.clj, attention.clj), one thread;
+        the 14 GEMVs run B1 (qlinear-q8 loop) or B2 (quantize-act-i8 + x8
+        dpbusd) on `threads`."""
+        cfg = wl.DECODER
+        d, nq, nkv, hd, ffn, cached = cfg["d"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"], cfg["ffn"], cfg["cached"]
+        shapes_ = [(d, nq * hd), (d, nkv * hd), (d, nkv * hd), (nq * hd, d), (d, ffn), (d, ffn), (ffn, d)]
+        rng = np.random.default_rng(0)
+        mats = []
+        for k, n in shapes_:
+            if route == "B1":
+                codes, scales = wl.q8_weights(n, k, seed=k + n)
+                mats.append((k, n, codes, scales))
+            else:
+                nb = k // 32
+                wqi = rng.integers(0, 256, size=(n // 8) * nb * 256, dtype=np.uint8)
+                wsi = rng.uniform(0.002, 0.02, (n // 8) * nb * 8).astype(np.float32)
+                mats.append((k, n, wqi, wsi))
+        kc = rng.standard_normal((cached + 1) * nkv * hd).astype(np.float32)
+        vc = rng.standard_normal((cached + 1) * nkv * hd).astype(np.float32)
+        gain = np.ones(d, np.float32)
+        x0 = wl.activations(1, d, seed=1)
+        bufs = {n: np.empty(n, np.float32) for _, n in shapes_}
+        xq, xs, xsum = np.empty(ffn, np.int8), np.empty(ffn // 32, np.float32), np.empty(ffn // 32, np.int32)
+
+        def gemv(i, v):
+            k, n, a, b = mats[i]
+            y = np.empty(n, np.float32)
+            v = np.ascontiguousarray(v, np.float32)
+            if route == "B1":
+                L.rqb_qlinear_q8(ptr(v), ptr(a), ptr(b), 1, k, n, ptr(y), threads)
+            else:
+                L.rqb_quantize_act_i8(ptr(v), 1, k, ptr(xq), ptr(xs), ptr(xsum), threads)
+                L.rqb_qmatmul_q8_x8(ptr(xq), ptr(xs), ptr(xsum), ptr(a), ptr(b), ptr(y), k, n, threads)
+            return y
+
+        def step():
+            x = x0
+            for _ in range(cfg["layers"]):
+                h = oracle.rms_norm(x, gain, 1, d, cfg["eps"], 0.0)
+                q = oracle.rope_pos(gemv(0, h), 1, nq, hd, cfg["theta"], cached)
+                kc[cached * nkv * hd:] = oracle.rope_pos(gemv(1, h), 1, nkv, hd, cfg["theta"], cached)
+                vc[cached * nkv * hd:] = gemv(2, h)
+                att = oracle.gqa_decode_attention(q, kc, vc, cached + 1, nq, nkv, hd, 1.0 / hd ** 0.5)
+                x1 = oracle.residual_add(x, gemv(3, att), d)
+                h2 = oracle.rms_norm(x1, gain, 1, d, cfg["eps"], 0.0)
+                f = oracle.silu_mul(gemv(4, h2), gemv(5, h2), ffn)
+                x = oracle.residual_add(x1, gemv(6, f), d)
+        _ = bufs
+        step()
+        return _timed(step, budget)
+
     legs = []
-    # C5 at M = 1 only: B2 takes one row per call, so its per-row time holds for M = 32 and 256 as well
+    # B2 takes one activation row per call (as qlinear-i8! does): an M-row leg is M calls
     shapes = [("C1", "q8", 1, 4096, 4096), ("C3", "q4", 1, 4096, 14336), ("C3", "q4", 4, 4096, 14336),
               ("C3", "q4", 16, 4096, 14336), ("C2", "q8", 512, 4096, 11008), ("C5", "q8", 1, 8192, 28672),
-              ("C5", "q4", 1, 8192, 28672)]
+              ("C5", "q4", 1, 8192, 28672), ("C5", "q8", 32, 8192, 28672), ("C5", "q4", 32, 8192, 28672),
+              ("C5", "q8", 256, 8192, 28672), ("C5", "q4", 256, 8192, 28672)]
+    for route in ("B1", "B2"):
+        for threads in (1, cores):
+            steps_, dt = c4_step(route, threads, leg_s)
+            legs.append({"config": "C4", "route": f"{route} two-layer decode step (14 GEMVs + glue)", "m": 1,
+                         "threads": threads, "steps_timed": steps_, "seconds": round(dt, 3),
+                         "us_per_step": round(dt / steps_ * 1e6, 2),
+                         "tokens_per_s": round(steps_ / dt, 2)})
     for cfg, fmt, m, k, n in shapes:
         for threads in (1, cores):
             if fmt == "q8":
@@ -827,7 +939,26 @@ def headline(torch, ctx, args):
     ms = e0.elapsed_time(e1) / args.steps
     kern_ms = kern_total / max(kern_n, 1)
     w.destroy()
-    return head.flops, ms, kern_ms, kern_n
+    cold = None
+    if not args.only_gemm:
+        cold = mfma_cold(torch, ctx, "q8", M, K, N)
+    return head.flops, ms, kern_ms, kern_n, cold
+
+
+def mfma_cold(torch, ctx, fmt, m, k, n, seed=0):
+    """A GEMM shape over weight copies rotated past 2x the MALL (each call reads
+    its weight from HBM): CALLS launches per captured graph (per call, launch
+    gaps included) and the kernels' average duration over the same rotation."""
+    one = q8_bytes(0, k, n, 0, 0) if fmt == "q8" else q4_bytes(0, k, n, 0, 0)
+    ws = Weights(ctx, fmt, k, n, copies_for_cold(one), seed=seed)
+    c = Case(torch, ctx, ws, m, "bf16", "bf16")
+    per_ms, cv = time_graph(torch, c.step)
+    kern_ms = time_kernels(torch, ctx, c.step)
+    out = {"copies": len(ws.ws), "weight_bytes_per_copy": one, "calls": CALLS, "per_call_us": round(per_ms * 1e3, 3),
+           "kernel_us": round(kern_ms * 1e3, 3), "TFLOPs": round(c.flops / kern_ms / 1e9, 2),
+           "frac_bf16_mfma": round(c.flops / kern_ms / 1e9 / BF16_PEAK_TFLOPS, 4), "cv": round(cv, 4)}
+    ws.destroy()
+    return out
 
 
 def main():
@@ -897,7 +1028,7 @@ def main():
         print(json.dumps({"decode": lines, "decoder": dec}), flush=True)
         return
 
-    flops, ms, kern_ms, kern_n = headline(torch, ctx, args)
+    flops, ms, kern_ms, kern_n, head_cold = headline(torch, ctx, args)
     tflops, kern_tflops = flops / ms / 1e9, flops / kern_ms / 1e9
     log(f"headline: {ms * 1e3:.2f} us/call, {tflops:.1f} TFLOP/s; "
         f"GEMM kernel {kern_ms * 1e3:.2f} us avg over {kern_n} launches, {kern_tflops:.1f} TFLOP/s")
@@ -924,6 +1055,10 @@ def main():
                      "kernel": "rq::gemm_pair_kernel", "flop_per_launch": flops,
                      "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
+    if head_cold is not None:
+        result["roofline"]["cold"] = head_cold
+        log(f"headline cold ({head_cold['copies']} weight copies): {head_cold['per_call_us']} us/call, kernel "
+            f"{head_cold['kernel_us']} us ({head_cold['frac_bf16_mfma']:.3f} of peak)")
 
     if not args.only_gemm:
         result["roofline"]["dense_bf16_library"] = lib = dense_library_line(torch)

@@ -84,7 +84,9 @@ int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz
  * events around its main kernel (hipExtLaunchKernel; not on a stream that is
  * being captured): for the bf16 prefill GEMM, the end of the packing pass
  * and the end of the GEMM, which follows it directly; for the other kernels,
- * the dispatch's own start and end.
+ * the dispatch's own start and end. A call whose partial sums a second kernel
+ * adds counts as one launch timed as the sum of its two kernels' own
+ * durations (the gap between them excluded).
  * rq_ctx_kernel_time waits for the pending pairs, returns their summed
  * duration and count, and clears them. Disabling frees the events. */
 int rq_ctx_set_kernel_timing(rq_ctx ctx, int enable);

@@ -26,6 +26,16 @@ static constexpr size_t kNoAllocScratchBytes = (size_t)RQ_NOALLOC_SCRATCH_MAX;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 static constexpr int kMaxDevices = 64;
 
+// Timing events of one call: e[0], e[1] bracket the main kernel (for the
+// bf16 GEMM: the packing pass's end and the GEMM's end); on calls whose
+// partial sums a second kernel adds, e[2], e[3] bracket that kernel (n = 4).
+// The call's time is the sum of its kernels' own durations, without the gap
+// between them.
+struct EvSet {
+  hipEvent_t e[4] = {nullptr, nullptr, nullptr, nullptr};
+  int n = 0;
+};
+
 struct Ctx {
   uint32_t magic;
   int device;
@@ -61,7 +71,7 @@ struct Ctx {
   // pool of spares.
   std::atomic<bool> timing{false};
   std::mutex timing_mu;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_pending, ev_pool;
+  std::vector<EvSet> ev_pending, ev_pool;
 };
 
 static constexpr uint32_t kCtxMagic = 0x52514358u;     // "RQCX"
@@ -245,41 +255,42 @@ static int stream_attn(Ctx* c, hipStream_t stream, size_t bytes, void** out) {
   return RQ_OK;
 }
 
-// An event pair for timing the main kernel of one call on `stream`, or
-// {nullptr, nullptr} when timing is off or the stream is being captured.
-static std::pair<hipEvent_t, hipEvent_t> timing_pair(Ctx* c, hipStream_t stream) {
-  if (!c->timing.load(std::memory_order_relaxed)) return {nullptr, nullptr};
+// Timing events for one call on `stream` (two kernels when `two`), or an empty
+// set when timing is off or the stream is being captured.
+static EvSet timing_set(Ctx* c, hipStream_t stream, bool two = false) {
+  if (!c->timing.load(std::memory_order_relaxed)) return {};
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return {nullptr, nullptr};
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return {};
   std::lock_guard<std::mutex> lk(c->timing_mu);
+  EvSet set;
   if (!c->ev_pool.empty()) {
-    auto p = c->ev_pool.back();
+    set = c->ev_pool.back();
     c->ev_pool.pop_back();
-    return p;
+  } else {
+    // timing-only events (no system-scope fence: nothing is synchronised through them)
+    for (int i = 0; i < 4; i++) {
+      if (hipEventCreateWithFlags(&set.e[i], hipEventDisableSystemFence) != hipSuccess) {
+        for (int j = 0; j < i; j++) (void)hipEventDestroy(set.e[j]);
+        return {};
+      }
+    }
   }
-  // timing-only events (no system-scope fence: nothing is synchronised through them)
-  hipEvent_t a = nullptr, b = nullptr;
-  if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return {nullptr, nullptr};
-  if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
-    (void)hipEventDestroy(a);
-    return {nullptr, nullptr};
-  }
-  return {a, b};
+  set.n = two ? 4 : 2;
+  return set;
 }
 
-static void timing_done(Ctx* c, std::pair<hipEvent_t, hipEvent_t> p, bool launched) {
-  if (!p.first) return;
+static void timing_done(Ctx* c, EvSet set, bool launched) {
+  if (!set.n) return;
   std::lock_guard<std::mutex> lk(c->timing_mu);
-  (launched ? c->ev_pending : c->ev_pool).push_back(p);
+  (launched ? c->ev_pending : c->ev_pool).push_back(set);
 }
 
 static void timing_release(Ctx* c) {
   std::lock_guard<std::mutex> lk(c->timing_mu);
   for (auto* v : {&c->ev_pending, &c->ev_pool}) {
-    for (auto& p : *v) {
-      (void)hipEventSynchronize(p.second);
-      (void)hipEventDestroy(p.first);
-      (void)hipEventDestroy(p.second);
+    for (auto& set : *v) {
+      if (set.n) (void)hipEventSynchronize(set.e[set.n - 1]);
+      for (hipEvent_t e : set.e) (void)hipEventDestroy(e);
     }
     v->clear();
   }
@@ -411,17 +422,19 @@ int rq_ctx_kernel_time(rq_ctx h, double* total_ms, int64_t* launches) {
   double sum = 0.0;
   int64_t n = 0;
   hipError_t err = hipSuccess;
-  for (auto& p : c->ev_pending) {
-    float ms = 0.0f;
-    hipError_t e = hipEventSynchronize(p.second);
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.first, p.second);
+  for (auto& set : c->ev_pending) {
+    float ms = 0.0f, ms2 = 0.0f;
+    hipError_t e = hipEventSynchronize(set.e[set.n - 1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, set.e[0], set.e[1]);
+    if (e == hipSuccess && set.n == 4) e = hipEventElapsedTime(&ms2, set.e[2], set.e[3]);
     if (e == hipSuccess) {
-      sum += ms;
+      sum += (double)ms + (double)ms2;
       n++;
     } else if (err == hipSuccess) {
       err = e;
     }
-    c->ev_pool.push_back(p);
+    set.n = 0;
+    c->ev_pool.push_back(set);
   }
   c->ev_pending.clear();
   *total_ms = sum;
@@ -784,10 +797,10 @@ static int run_kquant_matmul(Ctx* c, const Weight& w, const float* x, void* y, i
   int32_t* bs = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(buf) + xq_b + xs_b);
   hipError_t e = launch_quantize_act_q8k(x, m, w.in, sub, xq, xs, bs, stream);
   if (e != hipSuccess) return hip_fail(e, "quantizer launch");
-  const auto ev = fixed ? std::pair<hipEvent_t, hipEvent_t>{nullptr, nullptr} : timing_pair(c, stream);
-  if (ev.first) (void)hipEventRecord(ev.first, stream);
+  const EvSet ev = fixed ? EvSet{} : timing_set(c, stream);
+  if (ev.n) (void)hipEventRecord(ev.e[0], stream);
   e = launch_kquant_gemv(w, xq, xs, bs, y, y_dtype, m, c->cu_count, stream);
-  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, stream);
+  if (ev.n && e == hipSuccess) (void)hipEventRecord(ev.e[1], stream);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "K-quant GEMV launch");
   return RQ_OK;
@@ -905,10 +918,16 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
     if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
   }
   a.part = static_cast<float*>(part);
-  // no timing events for calls that allocate nothing (creating one allocates)
-  const auto ev = fixed ? std::pair<hipEvent_t, hipEvent_t>{nullptr, nullptr} : timing_pair(c, a.stream);
-  a.ev_main[0] = ev.first;
-  a.ev_main[1] = ev.second;
+  // no timing events for calls that allocate nothing (creating one allocates);
+  // calls whose partial sums a second kernel adds time both kernels
+  const bool two = (mf.ok && mf.ks > 1) || (!mf.ok && !g1.ok && plan.ok && plan.ksplit > 1) || a.slices > 1;
+  const EvSet ev = fixed ? EvSet{} : timing_set(c, a.stream, two);
+  a.ev_main[0] = ev.e[0];
+  a.ev_main[1] = ev.e[1];
+  if (ev.n == 4) {
+    a.ev_aux[0] = ev.e[2];
+    a.ev_aux[1] = ev.e[3];
+  }
   hipError_t e = g1.ok                ? launch_gemv1(a, g1)
                  : mf.ok              ? launch_gemv_mf(a, mf)
                  : plan.ok            ? launch_gemv(a, plan)
@@ -1038,10 +1057,10 @@ int rq_qmatmul_q8k(rq_ctx h, rq_weight wh, const int8_t* xq, const float* xs, co
   if (((uintptr_t)xs & 3) != 0 || ((uintptr_t)bsums & 3) != 0) return fail(RQ_ERR_SHAPE, "xs / bsums misaligned");
   if (((uintptr_t)y & (y_dtype == RQ_F32 ? 3 : 1)) != 0) return fail(RQ_ERR_SHAPE, "y misaligned");
   if (int s = set_device(c)) return s;
-  const auto ev = timing_pair(c, (hipStream_t)stream);
-  if (ev.first) (void)hipEventRecord(ev.first, (hipStream_t)stream);
+  const EvSet ev = timing_set(c, (hipStream_t)stream);
+  if (ev.n) (void)hipEventRecord(ev.e[0], (hipStream_t)stream);
   hipError_t e = launch_kquant_gemv(w, xq, xs, bsums, y, y_dtype, m, c->cu_count, (hipStream_t)stream);
-  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, (hipStream_t)stream);
+  if (ev.n && e == hipSuccess) (void)hipEventRecord(ev.e[1], (hipStream_t)stream);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "K-quant GEMV launch");
   return RQ_OK;
@@ -1133,10 +1152,10 @@ int rq_qmatmul_dx(rq_ctx h, rq_weight wh, const float* dy, float* dx, int64_t m,
   }
   if (mf)
     if (int s = stream_pack(c, st, dx_mf_pack_bytes(m, w.npad), &pack)) return s;
-  const auto ev = timing_pair(c, st);
-  if (ev.first) (void)hipEventRecord(ev.first, st);
+  const EvSet ev = timing_set(c, st);
+  if (ev.n) (void)hipEventRecord(ev.e[0], st);
   hipError_t e = mf ? launch_dx_mf(w, dy, dx, m, pack, part, slices, st) : launch_dx_fm(w, dy, dx, m, part, slices, st);
-  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, st);
+  if (ev.n && e == hipSuccess) (void)hipEventRecord(ev.e[1], st);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "dx launch");
   return RQ_OK;
@@ -1245,10 +1264,10 @@ int rq_stream_read(rq_ctx h, const void* src, size_t bytes, int wg_per_cu, uint3
     return fail(RQ_ERR_SHAPE, "bytes must be a positive multiple of 16 and src 16-byte aligned");
   if (wg_per_cu < 1 || wg_per_cu > 16) return fail(RQ_ERR_SHAPE, "wg_per_cu must be 1 .. 16");
   if (int s = set_device(c)) return s;
-  const auto ev = timing_pair(c, (hipStream_t)stream);
-  if (ev.first) (void)hipEventRecord(ev.first, (hipStream_t)stream);
+  const EvSet ev = timing_set(c, (hipStream_t)stream);
+  if (ev.n) (void)hipEventRecord(ev.e[0], (hipStream_t)stream);
   hipError_t e = launch_stream_read(src, bytes, c->cu_count * wg_per_cu, sink, (hipStream_t)stream);
-  if (ev.second && e == hipSuccess) (void)hipEventRecord(ev.second, (hipStream_t)stream);
+  if (ev.n && e == hipSuccess) (void)hipEventRecord(ev.e[1], (hipStream_t)stream);
   timing_done(c, ev, e == hipSuccess);
   if (e != hipSuccess) return hip_fail(e, "stream read launch");
   return RQ_OK;

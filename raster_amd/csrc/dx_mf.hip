@@ -287,7 +287,7 @@ static hipError_t launch_dx_mf_t(const Weight& w, const float* dy, float* dx, in
                      dim3(kDxmThreads), 0, stream, w.q, static_cast<const ST*>(w.scales), dyf, dx, part, (int)m,
                      (int)w.in, (int)w.npad, tiles_m, gps);
   if (hipError_t e = hipGetLastError()) return e;
-  if (slices > 1) return launch_split_reduce(part, dx, m * w.in, slices, RQ_F32, stream, nullptr);
+  if (slices > 1) return launch_split_reduce(part, dx, m * w.in, slices, RQ_F32, stream, nullptr, nullptr);
   return hipSuccess;
 }
 

@@ -323,14 +323,14 @@ __global__ __launch_bounds__(256) void gemm_sm_reduce_kernel(const float* __rest
 }
 
 hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
-                               hipEvent_t stop) {
+                               hipEvent_t start, hipEvent_t stop) {
   const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(y) & (y_dtype == RQ_F32 ? 15 : 1)) == 0;
   if (vec)
     hipExtLaunchKernelGGL(gemm_sm_reduce_kernel<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, stream,
-                          nullptr, stop, 0, part, y, n, ks, y_dtype);
+                          start, stop, 0, part, y, n, ks, y_dtype);
   else
-    hipExtLaunchKernelGGL(gemm_sm_reduce_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, nullptr,
+    hipExtLaunchKernelGGL(gemm_sm_reduce_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, start,
                           stop, 0, part, y, n, ks, y_dtype);
   return hipGetLastError();
 }
@@ -347,11 +347,11 @@ static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
   if (hipError_t e = launch_pack_x(a)) return e;
   const dim3 grid((unsigned)((a.npad / 16 + 4 * NTW - 1) / (4 * NTW)), (unsigned)ks);
   hipExtLaunchKernelGGL((gemm_sm_kernel<FMT, ST, MT, NTW, KC>), grid, dim3(256), 0, a.stream, nullptr,
-                        ks > 1 ? nullptr : a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, a.part, (int)a.m, (int)a.k, (int)a.n,
                         (int)a.npad, a.y_dtype);
   if (hipError_t e = hipGetLastError()) return e;
-  if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_main[1]);
+  if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_aux[0], a.ev_aux[1]);
   return hipSuccess;
 }
 

@@ -665,13 +665,13 @@ static hipError_t launch_t(const MatmulArgs& a, const DecodePlan& p) {
   }
   const bool split = p.ksplit > 1;
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(64 * WAVES), (unsigned)p.lds_bytes, a.stream,
-                        a.ev_main[0], split ? nullptr : a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales_rb), a.x,
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales_rb), a.x,
                         a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, p.ksplit, a.part, a.ops);
   if (hipError_t e = hipGetLastError()) return e;
   if (split) {
     const int ngroups = (int)(a.npad / 16);
     hipExtLaunchKernelGGL(skinny_reduce_kernel<MT>, dim3((unsigned)((ngroups + 3) / 4)), dim3(256), 0, a.stream,
-                          nullptr, a.ev_main[1], 0, a.part, a.y, (int)a.m, (int)a.k, (int)a.n, ngroups, p.ksplit,
+                          a.ev_aux[0], a.ev_aux[1], 0, a.part, a.y, (int)a.m, (int)a.k, (int)a.n, ngroups, p.ksplit,
                           a.y_dtype, a.ops);
   }
   return hipGetLastError();

@@ -440,7 +440,7 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
 }
 
 hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
-                               hipEvent_t stop);
+                               hipEvent_t start, hipEvent_t stop);
 
 // One configuration: ks K-slices, gcols workgroup columns per slice.
 template <int FMT, typename ST, int XT, int KW, int GW, int WD>
@@ -466,10 +466,10 @@ hipError_t launch_gemv_mf_t(const MatmulArgs& a, int ks, int gcols) {
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
   hipExtLaunchKernelGGL(kernel, dim3((unsigned)(gcols * ks)), dim3(64 * KW * GW), (unsigned)lds, a.stream,
-                        a.ev_main[0], ks > 1 ? nullptr : a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        a.ev_main[0], a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         a.x, a.y, a.part, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype, ks);
   if (hipError_t e = hipGetLastError()) return e;
-  if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_main[1]);
+  if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_aux[0], a.ev_aux[1]);
   return hipSuccess;
 }
 

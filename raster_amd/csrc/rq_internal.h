@@ -110,8 +110,10 @@ struct MatmulArgs {
   float* part;      // decode with K-split: partial sums, DecodePlan::part_bytes
   DecodeOps ops = {nullptr, 0.0f, nullptr, 0, 0, nullptr, nullptr};
   // kernel timing: when set, the main kernel is launched with hipExtLaunchKernel
-  // and these events take that dispatch's own start and end timestamps
+  // and these events take that dispatch's own start and end timestamps; on a
+  // call whose partial sums a second kernel adds, ev_aux brackets that kernel
   hipEvent_t ev_main[2] = {nullptr, nullptr};
+  hipEvent_t ev_aux[2] = {nullptr, nullptr};
   int slices = 1;  // K-slices of the small-m GEMM (partial sums in `part`)
 };
 
@@ -158,7 +160,7 @@ hipError_t launch_gemv1(const MatmulArgs& a, const G1Plan& p);
 
 // y[e] = sum over s < ks of part[s * n + e] (f32 or bf16 y), in slice order
 hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, int y_dtype, hipStream_t stream,
-                               hipEvent_t stop);
+                               hipEvent_t start, hipEvent_t stop);
 
 // Kernel launchers (each returns a hipError_t from hipGetLastError after launch).
 hipError_t launch_gemv(const MatmulArgs& a, const DecodePlan& p);
