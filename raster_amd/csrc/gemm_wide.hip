@@ -723,15 +723,9 @@ hipError_t launch_pack_x32(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-#ifndef PR_RA
-#define PR_RA 4
-#endif
-#ifndef PR_RW
-#define PR_RW 4
-#endif
-#ifndef PR_NB
-#define PR_NB 3
-#endif
+// K-pair ring depths: activation slots (loads RA - 1 macro steps ahead),
+// weight units in flight, LDS buffers of dequantized fragments
+constexpr int kPairRA = 4, kPairRW = 4, kPairNB = 3;
 template <int FMT, typename ST>
 static hipError_t launch_wide_t(const MatmulArgs& a, const WidePlan& p) {
   hipExtLaunchKernelGGL((gemm_wide_kernel<FMT, ST, 6, 2, 4>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(256), 0,
@@ -743,7 +737,7 @@ static hipError_t launch_wide_t(const MatmulArgs& a, const WidePlan& p) {
 
 template <int FMT, typename ST>
 static hipError_t launch_pair_t(const MatmulArgs& a, int tiles_m, int tiles_n) {
-  hipExtLaunchKernelGGL((gemm_pair_kernel<FMT, ST, PR_RA, PR_RW, PR_NB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
+  hipExtLaunchKernelGGL((gemm_pair_kernel<FMT, ST, kPairRA, kPairRW, kPairNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
                         a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m, (uint32_t)pack_x32_bytes(a.m, a.k));
