@@ -321,7 +321,7 @@ int rq_qmatmul_q8k(rq_ctx ctx, rq_weight w, const int8_t* xq, const float* xs, c
  * 64-bit long) and converted to f32 once, round to nearest even. Unscaled:
  * no block scales, no zero point. Device pointers, 4-byte aligned (wp and
  * xp may be NULL when kw is 0: y is then all zeros); y fully overwritten;
- * kw <= 2^21. */
+ * kw <= 2^20. */
 int rq_i8gemv_dp4a(rq_ctx ctx, const int32_t* wp, const int32_t* xp, float* y, int64_t kw, int64_t out,
                    void* stream);
 

@@ -1246,7 +1246,7 @@ int rq_i8gemv_dp4a(rq_ctx h, const int32_t* wp, const int32_t* xp, float* y, int
   if (kw < 0 || out < 0) return fail(RQ_ERR_SHAPE, "negative dimension");
   if (out == 0) return RQ_OK;
   if (!y || (kw > 0 && (!wp || !xp))) return fail(RQ_ERR_NULL, "wp, xp or y is NULL");
-  if (kw > ((int64_t)1 << 21)) return fail(RQ_ERR_SHAPE, "kw above 2^21 words (the lanes' int32 partial sums)");
+  if (kw > ((int64_t)1 << 20)) return fail(RQ_ERR_SHAPE, "kw above 2^20 words (the lanes' int32 partial sums)");
   if (out > ((int64_t)1 << 40) / std::max<int64_t>(kw, 1)) return fail(RQ_ERR_SHAPE, "out * kw too large");
   if ((((uintptr_t)wp | (uintptr_t)xp) & 3) != 0 || ((uintptr_t)y & 3) != 0)
     return fail(RQ_ERR_SHAPE, "wp, xp and y must be 4-byte aligned");

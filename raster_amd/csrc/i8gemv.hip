@@ -7,9 +7,10 @@
 // signed int8 lanes (par/dp4a, raster/par.clj:421-440). Raster accumulates in
 // a 64-bit long and converts the exact sum to float once; here each lane
 // accumulates its words with v_dot4_i32_i8 in int32 (a lane takes at most
-// ceil(kw / 64) words, |partial| <= 65536 per word, so int32 holds up to
-// 32768 words per lane) and the wave adds the lanes' partials in int64,
-// then converts once (round to nearest even, as Java's (float) long).
+// ceil(kw / 64) words and one word's dot is at most 4 * 128 * 128 = 2^16 in
+// magnitude, so with kw <= 2^20, the entry's limit, a lane's partial stays
+// within 2^30) and the wave adds the lanes' partials in int64, then converts
+// once (round to nearest even, as Java's (float) long).
 //
 // One wave per output row, four rows per workgroup; xp is read through the
 // caches (it is kw * 4 bytes, shared by every row). Rows of wp stream as

@@ -78,4 +78,4 @@ def test_i8gemv_dp4a_rejects_bad_shapes(torch, ctx):
     assert L.rq_i8gemv_dp4a(ctx.handle, p, p, p, -1, 4, None) == _lib.RQ_ERR_SHAPE
     assert L.rq_i8gemv_dp4a(ctx.handle, None, p, p, 4, 4, None) == _lib.RQ_ERR_NULL
     assert L.rq_i8gemv_dp4a(ctx.handle, p, p, C.c_void_p(buf.data_ptr() + 2), 4, 4, None) == _lib.RQ_ERR_SHAPE
-    assert L.rq_i8gemv_dp4a(ctx.handle, p, p, p, (1 << 21) + 1, 1, None) == _lib.RQ_ERR_SHAPE
+    assert L.rq_i8gemv_dp4a(ctx.handle, p, p, p, (1 << 20) + 1, 1, None) == _lib.RQ_ERR_SHAPE
