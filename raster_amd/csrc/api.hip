@@ -66,9 +66,9 @@ struct Ctx {
   // mutex covers setting its stream and enqueueing one call
   void* blas = nullptr;
   std::mutex blas_mu;
-  // Kernel timing (rq_ctx_set_kernel_timing): event pairs holding the start and
-  // end timestamps of each rq_qmatmul's main kernel, waiting to be read, and a
-  // pool of spares.
+  // Kernel timing (rq_ctx_set_kernel_timing): per timed call an event set (a
+  // start / end pair per kernel, EvSet), waiting to be read, and a pool of
+  // spares.
   std::atomic<bool> timing{false};
   std::mutex timing_mu;
   std::vector<EvSet> ev_pending, ev_pool;

@@ -603,36 +603,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
 #undef PR_LOAD_W
 #undef PR_LOAD_A
 
-  // pair sum and output, one m fragment (32 rows) per round: the second-k
-  // waves write their accumulators, the first-k waves add them and stage
-  // the rows; acc[f][c] register e: m = m0 + 32 f + lane % 32,
+  // pair sum and output, one m fragment (32 rows) per round. The two waves of
+  // a pair each finish half of every 32-column fragment: the first-k wave
+  // columns 0..15 (registers e < 8), the second-k wave columns 16..31 (e >= 8).
+  // Each hands the other half to its partner through LDS, adds the half it
+  // receives (a + b in either order is the same f32 sum) and stages its
+  // columns of all 32 rows; then each stores 16 of the rows as whole-row
+  // pieces. acc[f][c] register e: m = m0 + 32 f + lane % 32,
   // n = n0 + 32 c + 8 (e / 4) + 4 g + e % 4
   const int mrow = lane & 31;
   const int ncols = min(32 * NF, N - n0);
   const int ebytes = y_dtype == RQ_F32 ? 4 : 2;
   const bool staged = ((int64_t)N * ebytes) % 16 == 0 && (ncols * ebytes) % 16 == 0 &&
                       (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  // per row block: the first-k waves' columns 16..31 at [0, 2 NF), the
+  // second-k waves' columns 0..15 at [2 NF, 4 NF) (f32x4 slots of 64 lanes)
   f32x4* red = reinterpret_cast<f32x4*>(lds) + wm * (NF * 4 * 64) + lane;
+  f32x4* give = red + (kh == 0 ? 0 : 2 * NF * 64);
+  const f32x4* take = red + (kh == 0 ? 2 * NF * 64 : 0);
+  const int q0 = kh == 0 ? 0 : 2;  // first register quad this wave keeps
   uint8_t* st = lds + kLo + wm * (32 * RS);
   const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
 #pragma unroll
   for (int f = 0; f < 2; f++) {
-    __syncthreads();  // the ring (or the previous round's sums) is no longer read
-    if (kh == 1) {
-#pragma unroll
-      for (int c = 0; c < NF; c++)
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++)
-          red[(c * 4 + qq) * 64] =
-              f32x4{acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
-    }
-    __syncthreads();
-    if (kh == 1) continue;
+    __syncthreads();  // the ring (or the previous round's staging) is no longer read
 #pragma unroll
     for (int c = 0; c < NF; c++)
 #pragma unroll
-      for (int qq = 0; qq < 4; qq++) {
-        const f32x4 p = red[(c * 4 + qq) * 64];
+      for (int h = 0; h < 2; h++) {
+        const int qq = 2 - q0 + h;  // the quads the partner keeps
+        give[(c * 2 + h) * 64] =
+            f32x4{acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
+      }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NF; c++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int qq = q0 + h;
+        const f32x4 p = take[(c * 2 + h) * 64];
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[f][c][4 * qq + e] += p[e];
       }
@@ -640,7 +649,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
 #pragma unroll
       for (int c = 0; c < NF; c++)
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
+        for (int h = 0; h < 2; h++) {
+          const int qq = q0 + h;
           const int col = 32 * c + 8 * qq + 4 * g;
           if (y_dtype == RQ_F32)
             *reinterpret_cast<f32x4*>(st + mrow * RS + col * 4) =
@@ -650,26 +660,24 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
                 u32x2{pack2_bf16(acc[f][c][4 * qq], acc[f][c][4 * qq + 1]),
                       pack2_bf16(acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3])};
         }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
-      __builtin_amdgcn_wave_barrier();
+      __syncthreads();  // both halves of every row staged
       const int ppr = 32 * NF * ebytes / 16, vpr = ncols * ebytes / 16;
-      for (int p = lane; p < 32 * ppr; p += 64) {
-        const int r = p / ppr, pc = p - r * ppr;
+      for (int p = lane; p < 16 * ppr; p += 64) {
+        const int r = 16 * kh + p / ppr, pc = p % ppr;
         const int m = m0 + 32 * f + r;
         if (m < M && pc < vpr) {
           const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RS + pc * 16);
           *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(y) + ((int64_t)m * N + n0) * ebytes + pc * 16) = v;
         }
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
     } else {
       const int m = m0 + 32 * f + mrow;
       if (m >= M) continue;
 #pragma unroll
       for (int c = 0; c < NF; c++)
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
+        for (int h = 0; h < 2; h++) {
+          const int qq = q0 + h;
           const int n = n0 + 32 * c + 8 * qq + 4 * g;
           const float v[4] = {acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
           if (vec && n + 3 < N) {
