@@ -506,7 +506,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
   } while (0)
 #define PR_LOAD_W(ms_, slot_)                                                                   \
   do {                                                                                          \
-    if (has_unit) wd_load<FMT, ST>(wc[slot_], qr, sr, w_lo, w_so, (uint32_t)(2 * min((ms_), steps - 1)) + w_ks); \
+    wd_load<FMT, ST>(wc[slot_], qr, sr, w_lo, w_so, (uint32_t)(2 * min((ms_), steps - 1)) + w_ks);    \
   } while (0)
 #define PR_DEQUANT(slot_, buf_)                                                                 \
   do {                                                                                          \
@@ -535,15 +535,34 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[bb_][c], a[aslot_][f][j_], acc[f][c], 0, 0, 0); \
   } while (0)
 
-#pragma unroll
-  for (int st = 0; st < RA - 1; st++) PR_LOAD_A(st, st);
-#pragma unroll
-  for (int st = 0; st < RW; st++) PR_LOAD_W(st, st);
+  // Prologue loads in the order the steps keep them in flight (the weights of
+  // the first three macro steps, then activations and weights interleaved),
+  // so that the loop's first step has as many younger loads behind each
+  // operand as any later step: the compiler's wait counts at the loop head
+  // (the merge of the prologue and the back edge) then stay as deep as inside
+  // the loop instead of draining the ring once per unrolled turn. The weight
+  // loads are unconditional for the same reason (waves 6 and 7 fetch wave
+  // 5's unit and do not dequantize it): every path issues the same loads.
+  static_assert(RA == 4 && RW == 4 && NB == 3, "prologue order written for these ring depths");
+  PR_LOAD_W(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_W(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_W(2, 2);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_A(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_W(3, 3);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_A(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
   PR_DEQUANT(0, 0);
-  if (NB == 3) {
-    PR_DEQUANT(1 % RW, 1);
-    PR_LOAD_W(RW, 0);  // the steps load from RW + 1 on
-  }
+  PR_DEQUANT(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_W(4, 0);  // the steps load from RW + 1 on
+  __builtin_amdgcn_sched_barrier(0);
+  PR_LOAD_A(2, 2);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   PR_READ_B(0, 0, 0);
 
