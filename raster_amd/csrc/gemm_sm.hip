@@ -23,6 +23,14 @@
 // v_permlane16_swap) hand lane (r, q) dword q of row r of each of the four
 // chunks, k = 4q .. 4q+3 (low nibbles) and 4q+16 .. 4q+19 (high nibbles). The
 // activation fragments are staged into LDS in that k order.
+//
+// Loads go through buffer resources (the workgroup's weight groups, the
+// packed activations) with the k position and the group as uniform offsets:
+// no 64-bit address arithmetic per load, and a load past a resource's end
+// reads zeros. The loop is then bound by the dequantization's VALU work: at
+// M = 32, K = 8192, N = 28672, Q4_0 it measured 64 VALU instructions per
+// k-step and wave (80 with per-lane 64-bit addresses and per-nibble bit-field
+// extracts) and 51.7 against 56.7 us per call.
 #include <algorithm>
 
 #include "rq_internal.h"
@@ -35,6 +43,11 @@ struct WCodesSm {
   u32x2 v;
   uint32_t s;  // scale bits, converted at dequantization
 };
+
+// buffer resource over bytes [p, p + bytes): loads past the end return zero
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sm_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
 struct WQuadSm {
   u32x4 v;     // row r of chunk q of the quad
@@ -73,19 +86,15 @@ __device__ __forceinline__ void bcast4_rows(uint32_t s, uint32_t (&b)[4]) {
 template <typename ST>
 __device__ __forceinline__ bf16x8 dequant_q4_dword(uint32_t d, uint32_t sbits) {
   const float s = scale_from_bits<ST>(sbits), off = -8.0f * s;
-  const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+  uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+  // opaque to the known-bits fold, which would extract each nibble with its
+  // own v_bfe before a byte-0 conversion: the byte-select conversions then
+  // take the four bytes of lo and hi directly
+  asm("" : "+v"(lo), "+v"(hi));
   auto two = [&](uint32_t v, int b) {
     return pack2_bf16(fmaf((float)((v >> (8 * b)) & 0xFFu), s, off), fmaf((float)((v >> (8 * b + 8)) & 0xFFu), s, off));
   };
   return __builtin_bit_cast(bf16x8, u32x4{two(lo, 0), two(lo, 2), two(hi, 0), two(hi, 2)});
-}
-
-// Q8_0: lane (fr, fg) takes codes 8fg .. 8fg+7 of row fr
-template <typename ST>
-__device__ __forceinline__ void load_wc_q8(WCodesSm& c, const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                           int64_t chunk, int fr, int fg) {
-  c.v = *reinterpret_cast<const u32x2*>(q + chunk * 512 + fr * 32 + 8 * fg);
-  c.s = load_scale_bits<ST>(sc, chunk * 16 + fr);
 }
 
 // 8 bf16 of the lane's Q8_0 fragment share: exact f32 scale * code, one RNE
@@ -125,9 +134,19 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   const int fr = lane & 15, fg = lane >> 4;
   const int n0 = (int)blockIdx.x * 64 * NTW;
   const int g_last = npad / 16 - 1, mt_last = (M + 15) / 16 - 1;
-  int64_t wchunk[NTW];
+  // buffer resources: this workgroup's weight groups (codes, scales) and the
+  // packed activations. A load's k position and group are uniform offsets;
+  // groups past the last one read zeros (their outputs are never stored).
+  constexpr uint32_t CB = FMT == RQ_Q8_0 ? 512u : 256u;
+  const int gq0 = n0 / 16, ngr = min(4 * NTW, g_last + 1 - gq0);
+  const __amdgpu_buffer_rsrc_t qr = sm_rsrc(q + (int64_t)gq0 * nkb * CB, (uint32_t)(ngr * nkb) * CB);
+  const __amdgpu_buffer_rsrc_t sr =
+      sm_rsrc(sc + (int64_t)gq0 * nkb * 16, (uint32_t)(ngr * nkb) * 16u * (uint32_t)sizeof(ST));
+  const __amdgpu_buffer_rsrc_t xr = sm_rsrc(xf, (uint32_t)((mt_last + 1) * nkb) * 1024u);
+  const int nstm = max(nst - 1, 0);
+  uint32_t gofs[NTW];  // chunk row of group j (uniform)
 #pragma unroll
-  for (int j = 0; j < NTW; j++) wchunk[j] = (int64_t)min(n0 / 16 + wave * NTW + j, g_last) * nkb;
+  for (int j = 0; j < NTW; j++) gofs[j] = (uint32_t)__builtin_amdgcn_readfirstlane((wave * NTW + j) * nkb + kb0);
 
   // activation pieces of a chunk: piece p = tid + 256 i is step p / (64 MT),
   // tile (p / 64) % MT, lane p % 64 (tiles past the packed rows are clamped:
@@ -136,9 +155,12 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   auto load_a = [&](int c) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
-      const int p = tid + 256 * i, u = p / (64 * MT), t = (p / 64) % MT, l = p % 64;
-      const int kb = min(kb0 + min(c * KC + u, max(nst - 1, 0)), nkb - 1);
-      areg[i] = *reinterpret_cast<const u32x4*>(xf + (((int64_t)min(t, mt_last) * nkb + kb) * 64 + l) * 8);
+      const int p = tid + 256 * i, t = (p / 64) % MT, l = p % 64;
+      const int u = __builtin_amdgcn_readfirstlane(p / (64 * MT));  // the same in a wave
+      const uint32_t kb = (uint32_t)(kb0 + min(c * KC + u, nstm));
+      areg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              xr, (int)(((uint32_t)(min(t, mt_last) * nkb) * 64u + (uint32_t)l) * 16u),
+                                              (int)(kb * 1024u), 0));
     }
   };
   auto store_a = [&](int buf) {
@@ -166,17 +188,27 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
     if constexpr (FMT == RQ_Q4_0) {
       // quad slot / 4 of steps s .. s+3 (slot, s multiples of 4): lane
       // (fr, fg) loads step s + fg
-      const int kb = min(kb0 + min(s + fg, max(nst - 1, 0)), nkb - 1);
+      const uint32_t kl = (uint32_t)min(s + fg, nstm);
+      const uint32_t vq = kl * 256u + (uint32_t)fr * 16u, vs = (kl * 16u + (uint32_t)fr) * (uint32_t)sizeof(ST);
 #pragma unroll
       for (int j = 0; j < NTW; j++) {
-        const int64_t ch = wchunk[j] + kb;
-        wq[slot / 4][j].v = *reinterpret_cast<const u32x4*>(q + ch * 256 + fr * 16);
-        wq[slot / 4][j].s = load_scale_bits<ST>(sc, ch * 16 + fr);
+        wq[slot / 4][j].v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, (int)vq, (int)(gofs[j] * 256u), 0));
+        if constexpr (sizeof(ST) == 4)
+          wq[slot / 4][j].s = __builtin_amdgcn_raw_buffer_load_b32(sr, (int)vs, (int)(gofs[j] * 64u), 0);
+        else
+          wq[slot / 4][j].s = __builtin_amdgcn_raw_buffer_load_b16(sr, (int)vs, (int)(gofs[j] * 32u), 0);
       }
     } else {
-      const int kb = min(kb0 + min(s, max(nst - 1, 0)), nkb - 1);
+      const uint32_t kl = (uint32_t)min(s, nstm);  // uniform
+      const uint32_t vq = (uint32_t)fr * 32u + 8u * (uint32_t)fg, vs = (uint32_t)fr * (uint32_t)sizeof(ST);
 #pragma unroll
-      for (int j = 0; j < NTW; j++) load_wc_q8<ST>(wc[slot][j], q, sc, wchunk[j] + kb, fr, fg);
+      for (int j = 0; j < NTW; j++) {
+        wc[slot][j].v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(qr, (int)vq, (int)((gofs[j] + kl) * 512u), 0));
+        if constexpr (sizeof(ST) == 4)
+          wc[slot][j].s = __builtin_amdgcn_raw_buffer_load_b32(sr, (int)vs, (int)((gofs[j] + kl) * 64u), 0);
+        else
+          wc[slot][j].s = __builtin_amdgcn_raw_buffer_load_b16(sr, (int)vs, (int)((gofs[j] + kl) * 32u), 0);
+      }
     }
   };
 
@@ -379,13 +411,18 @@ int gemm_sm_slices(int format, int64_t m, int64_t k, int64_t npad, int cu_count)
 // 81 us against 92 / 84 / 88 / 87; K = 4096, N = 11008: m = 17 / 32 / 48 / 64
 // 24.3 / 25.3 / 28.4 / 29.1 against 27.9 / 29.1 / 29.4 / 29.3; K = 4096,
 // N = 14336: m = 17 / 32 / 64 26.5 / 27.7 / 32.5 against 30.3 / 30.1 / 31.0.
+// The buffer offsets are 32-bit: K is bounded so that a workgroup's weight
+// rows (8 groups x K/32 chunks of up to 512 bytes) and the packed activations
+// (4 tiles x K/32 x 1 KB) stay far below 2^32 bytes.
+constexpr int64_t kSmMaxK = int64_t(1) << 22;
+
 bool gemm_sm_takes(int format, int64_t m, int64_t k) {
-  if (m <= 16 || m > 64) return false;
+  if (m <= 16 || m > 64 || k > kSmMaxK) return false;
   return format == RQ_Q4_0 || m <= 48 || k >= 8192;
 }
 
 hipError_t launch_gemm_sm(const MatmulArgs& a, int ks) {
-  if (a.m <= 16 || a.m > 64) return hipErrorInvalidValue;
+  if (a.m <= 16 || a.m > 64 || a.k > kSmMaxK) return hipErrorInvalidValue;
 #define RQ_SM(FMT_, ST_) return a.m <= 32 ? launch_sm_t<FMT_, ST_, 2>(a, ks) : launch_sm_t<FMT_, ST_, 4>(a, ks);
   if (a.format == RQ_Q8_0) { RQ_SM(RQ_Q8_0, float) }
   if (a.scale_dtype == RQ_F16) { RQ_SM(RQ_Q4_0, uint16_t) }
