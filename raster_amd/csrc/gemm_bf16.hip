@@ -69,6 +69,9 @@ __device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
     const int sh = fg >= 2 ? 4 : 0;
     d[0] = (c.v[0] >> sh) & 0x0F0F0F0Fu;
     d[1] = (c.v[1] >> sh) & 0x0F0F0F0Fu;
+    // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
+    // conversions below then read the bytes of d directly
+    asm("" : "+v"(d[0]), "+v"(d[1]));
     off = -8.0f * s;
   }
   uint32_t o[4];

@@ -79,6 +79,9 @@ __device__ __forceinline__ void wd_dequant(const WdCodes& c, int g, bf16x8& f0, 
     const int sh = 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; i++) d[i] = (c.v[i] >> sh) & 0x0F0F0F0Fu;
+    // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
+    // conversions below then read the bytes of d directly
+    asm("" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]));
     off = -8.0f * s;
   }
   uint32_t o[8];
@@ -105,6 +108,7 @@ __device__ __forceinline__ bf16x8 wd_dequant_half(const WdCodes& c, int g, int h
     const int sh = 4 * g;
     d[0] = (c.v[2 * h] >> sh) & 0x0F0F0F0Fu;
     d[1] = (c.v[2 * h + 1] >> sh) & 0x0F0F0F0Fu;
+    asm("" : "+v"(d[0]), "+v"(d[1]));  // as in wd_dequant
     off = -8.0f * s;
   }
   uint32_t o[4];
