@@ -732,8 +732,8 @@ static hipError_t launch_wk(const MatmulArgs& a) {
 // or one after another, so a tiling costs that count times the tile area.
 // Candidates, ties to the first: 8 waves x 256 x 96 (two fragments of rows
 // each, one workgroup per CU), 4 waves x 256 x 64 and 4 waves x 256 x 48 (two
-// per CU), 8 waves x 256 x 112. (256 x 128 would never be chosen: it costs
-// at least what 256 x 64 does.) Measured (Q8, clocks settled): M = 512,
+// per CU), 8 waves x 256 x 112. (256 x 128 in this kernel would never be
+// chosen: it costs at least what 256 x 64 does.) Measured (Q8, clocks settled): M = 512,
 // K = 4096, N = 11008: 52.6 / 56.1 / 54.5 / 54.9 us (8 waves x 512 x 48, the
 // same area: 54.8 us, its activation traffic from L2 twice that of 256 x 96);
 // M = 256, K = 8192, N = 28672: 256 x 112 (256 tiles, one per CU) 122 us,
@@ -743,26 +743,34 @@ static hipError_t launch_wk(const MatmulArgs& a) {
 // same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
 // (twice the workgroups of 64 x 128) measured 126 against 151 us (Q4) and 68
 // against 81 us (Q8) at M = 32, K = 8192, N = 28672.
+// The K-pair kernel (gemm_wide.hip, 32x32x16 MFMA, K a multiple of 64) takes
+// the 256 x 96 tile and a fifth candidate, 256 x 128, at 0.85 of the cost of
+// its area: at M = 256, K = 8192, N = 28672 (cold, same box) its 224 tiles of
+// 256 x 128 took 125.5 us (Q8) / 121.5 us (Q4, f16 scales) against 130.5 /
+// 123.0 us for the 256 tiles of 256 x 112, 0.84 / 0.87 of the time per tile
+// area; M = 300: 227 against 235 us.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   if (a.m > 128) {
-    const int64_t bm[4] = {256, 256, 256, 256}, bn[4] = {96, 64, 48, 112};
+    const bool pair = a.k % 64 == 0;
+    const int64_t bm[5] = {256, 256, 256, 256, 256}, bn[5] = {96, 64, 48, 112, 128};
+    const int64_t pct[5] = {pair ? 85 : 100, 100, 100, 100, 85};
     int best = 0;
     int64_t best_cost = INT64_MAX;
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < (pair ? 5 : 4); i++) {
       const int64_t tiles = (a.m + bm[i] - 1) / bm[i] * ((a.npad + bn[i] - 1) / bn[i]);
-      const int64_t cost = (tiles + cu_count - 1) / std::max(cu_count, 1) * bm[i] * bn[i];
+      const int64_t cost = (tiles + cu_count - 1) / std::max(cu_count, 1) * bm[i] * bn[i] * pct[i];
       if (cost < best_cost) {
         best_cost = cost;
         best = i;
       }
     }
-    // 256 x 96: the K-pair kernel on 32x32x16 MFMA (gemm_wide.hip; C2 step
-    // 52.5 against 54.2 us for gemm_wk_kernel, same box and data) where K is
-    // a whole number of its 64-k macro steps
-    if (best == 0) return (a.k % 64 == 0) ? launch_gemm_pair(a) : launch_wk<FMT, ST, 6>(a);
+    // 256 x 96: the K-pair kernel on 32x32x16 MFMA (C2 step 52.5 against
+    // 54.2 us for gemm_wk_kernel, same box and data)
+    if (best == 0) return pair ? launch_gemm_pair(a, 3) : launch_wk<FMT, ST, 6>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
     if (best == 2) return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
+    if (best == 4) return launch_gemm_pair(a, 4);
     return launch_wk<FMT, ST, 7>(a);
   }
   if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);

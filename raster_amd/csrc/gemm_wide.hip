@@ -425,32 +425,35 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 }
 
 // K-pair variant for shapes whose 256 x 192 tiles are too few for the CUs
-// (C2: M 512, N 11008): 256 x 96 tiles, eight waves, two per SIMD. Waves w and
-// w + 4 share a SIMD and rows 64 (w % 4) .. + 63 (two 32-row fragments) and
-// split each macro step's two 32-k steps: wave w takes the first, w + 4 the
-// second, so each holds a 64 x 96 accumulator tile (96 AGPRs) and the two
-// waves of a SIMD hide each other's waits. The 6 dequant units of a macro
-// step (3 n fragments x 2 k-steps) go to waves 0..5. At the end the
+// (C2: M 512, N 11008): 256 x 32 NF tiles (NF 3: 96 columns; NF 4: 128, for
+// shapes whose 128-column tiles fill the CUs in whole rounds, C5 at M 256),
+// eight waves, two per SIMD. Waves w and w + 4 share a SIMD and rows
+// 64 (w % 4) .. + 63 (two 32-row fragments) and split each macro step's two
+// 32-k steps: wave w takes the first, w + 4 the second, so each holds a
+// 64 x 32 NF accumulator tile and the two waves of a SIMD hide each other's
+// waits. The 2 NF dequant units of a macro step (NF n fragments x 2 k-steps)
+// go to waves 0 .. 2 NF - 1. At the end the
 // second-k waves pass their accumulators through LDS to the first-k waves,
 // which add them (two interleaved partial sums of K) and stage the tile for
 // whole-row stores.
 // Per macro step a wave: issues its activation loads RA - 1 macro steps ahead
 // and its weight unit RW ahead, reads its k-step's half-0 fragments (read at
-// the end of the previous step), runs 6 MFMAs while dequantizing, then after
+// the end of the previous step), runs 2 NF MFMAs while dequantizing, then after
 // the barrier reads the next step's half-0 fragments and runs the half-1 MFMAs.
-template <int FMT, typename ST, int RA, int RW, int NB>
+template <int FMT, typename ST, int RA, int RW, int NB, int NF>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void gemm_pair_kernel(
     const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
     int M, int K, int N, int npad, int y_dtype, int tiles_m, uint32_t xf_bytes) {
-  constexpr int NF = 3, NU = 2 * NF;
+  constexpr int NU = 2 * NF;
+  static_assert(NF == 3 || NF == 4, "column fragments per tile");
   constexpr int U = (RA == 3 || RW == 3 || NB == 3) ? ((RA == 4 || RW == 4) ? 12 : 6) : 4;
   static_assert((RA == 2 || RA == 3 || RA == 4) && (RW == 2 || RW == 3 || RW == 4), "ring depths");
   static_assert(NB == 2 || NB == 3, "LDS ring: 2 or 3 buffers");
   static_assert(U % RA == 0 && U % RW == 0 && U % NB == 0, "unroll covers the rings");
-  // LDS: the weight ring Bs[buf][k-step][half][n frag][lane] (NB x 12 KB), or at
-  // the end the pair reduction (4 waves x 12 KB) and the staging (4 waves x
-  // 32 rows x RS)
-  constexpr int RS = 400;
+  // LDS: the weight ring Bs[buf][k-step][half][n frag][lane] (NB x 4 NF KB), or
+  // at the end the pair reduction (4 waves x 4 NF KB) and the staging (4 waves
+  // x 32 rows x RS: a row of 32 NF f32 and 16 bytes against bank conflicts)
+  constexpr int RS = 32 * NF * 4 + 16;
   constexpr int kRing = NB * 2 * 2 * NF * 64 * 16, kRed = 4 * NF * 4 * 64 * 16, kStage = 4 * 32 * RS;
   constexpr int kLo = kRing > kRed ? kRing : kRed;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLo + kStage];
@@ -766,21 +769,25 @@ static hipError_t launch_wide_t(const MatmulArgs& a, const WidePlan& p) {
   return hipGetLastError();
 }
 
-template <int FMT, typename ST>
+template <int FMT, typename ST, int NF>
 static hipError_t launch_pair_t(const MatmulArgs& a, int tiles_m, int tiles_n) {
-  hipExtLaunchKernelGGL((gemm_pair_kernel<FMT, ST, kPairRA, kPairRW, kPairNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
+  hipExtLaunchKernelGGL((gemm_pair_kernel<FMT, ST, kPairRA, kPairRW, kPairNB, NF>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
                         a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, tiles_m, (uint32_t)pack_x32_bytes(a.m, a.k));
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_pair(const MatmulArgs& a) {
-  const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.npad + 95) / 96);
+hipError_t launch_gemm_pair(const MatmulArgs& a, int nf) {
+  if ((nf != 3 && nf != 4) || a.k % 64 != 0) return hipErrorInvalidValue;
+  const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.npad + 32 * nf - 1) / (32 * nf));
   if (hipError_t e = launch_pack_x32(a)) return e;
-  if (a.format == RQ_Q8_0) return launch_pair_t<RQ_Q8_0, float>(a, tiles_m, tiles_n);
-  if (a.scale_dtype == RQ_F16) return launch_pair_t<RQ_Q4_0, uint16_t>(a, tiles_m, tiles_n);
-  return launch_pair_t<RQ_Q4_0, float>(a, tiles_m, tiles_n);
+#define RQ_PAIR(FMT_, ST_) \
+  return nf == 3 ? launch_pair_t<FMT_, ST_, 3>(a, tiles_m, tiles_n) : launch_pair_t<FMT_, ST_, 4>(a, tiles_m, tiles_n);
+  if (a.format == RQ_Q8_0) { RQ_PAIR(RQ_Q8_0, float) }
+  if (a.scale_dtype == RQ_F16) { RQ_PAIR(RQ_Q4_0, uint16_t) }
+  RQ_PAIR(RQ_Q4_0, float)
+#undef RQ_PAIR
 }
 
 hipError_t launch_gemm_wide(const MatmulArgs& a, const WidePlan& p) {
