@@ -125,8 +125,9 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   __shared__ __attribute__((aligned(16))) bf16x8 As[2][KC][MT][64];
   const int nkb = K / 32;
   const int ks = (int)gridDim.y, sl = (int)blockIdx.y;
-  // this workgroup's K-slice: steps [kb0, kb0 + nst), a whole number of chunks
-  const int spl = ((nkb + ks - 1) / ks + KC - 1) / KC * KC;
+  // this workgroup's K-slice: steps [kb0, kb0 + nst); slices are whole pairs
+  // of chunks (the last one may be shorter)
+  const int spl = ((nkb + ks - 1) / ks + 2 * KC - 1) / (2 * KC) * (2 * KC);
   const int kb0 = min(nkb, sl * spl), nst = min(nkb, kb0 + spl) - kb0;
   const int nch = (nst + KC - 1) / KC;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -163,10 +164,11 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
                                               (int)(kb * 1024u), 0));
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](int buf, int c) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int p = tid + 256 * i;
+      if (c * KC + p / (64 * MT) >= nst) areg[i] = u32x4{0u, 0u, 0u, 0u};  // a step past the slice adds nothing
       if (FMT == RQ_Q4_0) {
         // the piece of lane (r, g) holds k = 8g .. 8g+7: k = 8g .. 8g+3 go
         // to lane group 2 (g & 1), 8g+4 .. 8g+7 to the next one, the upper
@@ -223,10 +225,14 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   load_a(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int s = 0; s < WD; s += FMT == RQ_Q4_0 ? 4 : 1) load_w(s, s);
+  for (int s = 0; s < KC; s += FMT == RQ_Q4_0 ? 4 : 1) load_w(s, s);
   __builtin_amdgcn_sched_barrier(0);
-  store_a(0);
-  if (nch > 1) load_a(1);
+  store_a(0, 0);
+  load_a(1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = KC; s < WD; s += FMT == RQ_Q4_0 ? 4 : 1) load_w(s, s);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 
   // chunk c (LDS buffer c % 2, ring slots (c % 2) KC ..): first stage chunk
@@ -234,16 +240,23 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   // c+2; then its steps, each computing from the LDS activations and the
   // weights in its ring slot, whose refill (step s + WD) goes out at once;
   // one barrier at the end (the other buffer is complete, this one is free).
+  // Nothing in the loop is conditional: steps past the slice get zero
+  // activations (store_a) and clamped weights, and an odd chunk count runs
+  // one such chunk more. With conditional loads or early exits the compiler's
+  // wait counts at the merges drained every load in flight once or twice per
+  // loop turn (measured at C5, M = 32: Q4_0 51.0 -> 48.9 us per call with
+  // even chunk counts, 50.7 -> 52.0 with the padded chunk of an odd count).
+  // A padded step multiplies zeros by finite weights; a non-finite scale
+  // already makes its column non-finite.
   auto chunk = [&](int c, const int buf) {
-    if (c + 1 < nch) {
-      store_a(buf ^ 1);
-      if (c + 2 < nch) load_a(c + 2);
-    }
+    store_a(buf ^ 1, c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t dq[NTW][4], sq[NTW][4];  // the current quad, after the swaps
 #pragma unroll
     for (int u = 0; u < KC; u++) {
       const int s = c * KC + u;
-      if (s >= nst) break;
       const int slot = buf * KC + u;
       bf16x8 wf[NTW];
       if constexpr (FMT == RQ_Q4_0) {
@@ -252,7 +265,10 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
           for (int j = 0; j < NTW; j++) {
 #pragma unroll
             for (int b = 0; b < 4; b++) dq[j][b] = wq[slot / 4][j].v[b];
-            sq[j][0] = wq[slot / 4][j].s;
+            // the scale as f32 before the broadcast: one conversion per
+            // quad, and no zero-extension of the loaded half word ahead
+            // of its use
+            sq[j][0] = __float_as_uint(scale_from_bits<ST>(wq[slot / 4][j].s));
           }
           load_w(slot, s + WD);
 #pragma unroll
@@ -262,7 +278,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
           }
         }
 #pragma unroll
-        for (int j = 0; j < NTW; j++) wf[j] = dequant_q4_dword<ST>(dq[j][u % 4], sq[j][u % 4]);
+        for (int j = 0; j < NTW; j++) wf[j] = dequant_q4_dword<float>(dq[j][u % 4], sq[j][u % 4]);
       } else {
 #pragma unroll
         for (int j = 0; j < NTW; j++) wf[j] = dequant_sm_q8<ST>(wc[slot][j]);
@@ -281,8 +297,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   };
   for (int c = 0; c < nch; c += 2) {
     chunk(c, 0);
-    if (c + 1 >= nch) break;
-    chunk(c + 1, 1);
+    chunk(c + 1, 1);  // past the end at an odd count: zero activations
   }
 
   // acc[i][j] holds y[m][n .. n+3] with m = row fr of tile i, n = 4 fg of
@@ -402,7 +417,13 @@ int gemm_sm_slices(int format, int64_t m, int64_t k, int64_t npad, int cu_count)
   const int64_t want = (int64_t)cu_count * (format == RQ_Q8_0 || m > 32 ? 12 : 24);
   int64_t ks = std::max<int64_t>(1, want / std::max<int64_t>(waves, 1));
   ks = std::min<int64_t>(ks, std::max<int64_t>(1, (k / 32) / (8 * kSmKC)));
-  return (int)std::min<int64_t>(ks, 8);
+  // slices of whole chunk pairs: the nearest multiple of 2 KC steps to the
+  // even split, then as many slices as that takes (C5 Q4_0 M = 32: 6 -> 7
+  // slices of 40 steps; Q8_0 3 slices of 88)
+  const int64_t nkb = k / 32, pair = 2 * kSmKC;
+  const int64_t len = std::max<int64_t>(pair, ((nkb + ks - 1) / ks + pair / 2) / pair * pair);
+  ks = (nkb + len - 1) / len;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ks, 8));
 }
 
 // Q4_0 at 16 < m <= 64. Q8_0 at 16 < m <= 48, and up to 64 from K = 8192:
