@@ -365,12 +365,15 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
       for (int u0 = 0; u0 < spp; u0 += WD) {
 #pragma unroll
         for (int t = 0; t < WD / 4; t++) {
+          // one quad after the other: hoisting the next quad's lane swaps
+          // above this quad's work would make the loop wait for the whole
+          // ring at its head
+          __builtin_amdgcn_sched_barrier(0);
           uint32_t d[4] = {wq[t].v[0], wq[t].v[1], wq[t].v[2], wq[t].v[3]};
-          uint32_t sb;
-          if constexpr (sizeof(ST) == 2)
-            sb = wq[t].s;
-          else
-            sb = __builtin_bit_cast(uint32_t, wq[t].s);
+          // the scale as f32 bits before the broadcast: a 16-bit scale's
+          // zero extension would otherwise sit at the loop head and wait
+          // for the whole ring there
+          const uint32_t sb = __float_as_uint(scale_value(wq[t].s));
           mf_xpose4(d);
           uint32_t s4[4];
           mf_bcast4(sb, s4);
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(64 * KW * GW) void gemv_mf_kernel(const uint8_t* __
             ah[jj] = *reinterpret_cast<const bf16x8*>(smem + ab + aoff);
             if (P == 2) al[jj] = *reinterpret_cast<const bf16x8*>(smem + ab + M * 64 + aoff);
             xo[jj] = *reinterpret_cast<const f32x4*>(smem + xs_off + (su * 16 + 4 * qd) * 4);
-            sv[jj] = live ? scale_from_bits<ST>(s4[jj]) : 0.0f;
+            sv[jj] = live ? __uint_as_float(s4[jj]) : 0.0f;
           }
           f32x4 blk[4];
 #pragma unroll
