@@ -249,6 +249,10 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   // A padded step multiplies zeros by finite weights; a non-finite scale
   // already makes its column non-finite.
   auto chunk = [&](int c, const int buf) {
+    // keeps the zeroing selects of store_a (pure VALU on the registers that
+    // load_a filled a chunk ago) from being hoisted into the previous chunk,
+    // where they would wait for those loads
+    __builtin_amdgcn_sched_barrier(0);
     store_a(buf ^ 1, c + 1);
     __builtin_amdgcn_sched_barrier(0);
     load_a(c + 2);
@@ -270,7 +274,6 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
             // of its use
             sq[j][0] = __float_as_uint(scale_from_bits<ST>(wq[slot / 4][j].s));
           }
-          load_w(slot, s + WD);
 #pragma unroll
           for (int j = 0; j < NTW; j++) {
             xpose4_rows(dq[j]);
@@ -292,6 +295,11 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int i = 0; i < MT; i++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[i][j], 0, 0, 0);
+      // Q4_0: the quad slot's refill after the quad's last step, when the
+      // swapped copy is dead, so that the load can land in the same registers
+      // (issued while the copy is live, it gets other registers, and the
+      // loop's end copies them back, waiting for the load)
+      if (FMT == RQ_Q4_0 && u % 4 == 3) load_w(slot - 3, s - 3 + WD);
     }
     __syncthreads();
   };
