@@ -57,23 +57,17 @@ __device__ __forceinline__ void load_wcodes(WCodes& c, const uint8_t* __restrict
 template <int FMT, typename ST>
 __device__ __forceinline__ bf16x8 dequant_frag(const WCodes& c, int fg) {
   const float s = scale_from_bits<ST>(c.s);
-  uint32_t d[2];
-  float off;
   if (FMT == RQ_Q8_0) {
-    // signed code = u - 128 with u = byte ^ 0x80: fma(u, s, -128 s) = s * code, rounded once
-    d[0] = c.v[0] ^ 0x80808080u;
-    d[1] = c.v[1] ^ 0x80808080u;
-    off = -128.0f * s;
-  } else {
-    // nibble q, zero-point 8: fma(q, s, -8 s) = s * (q - 8), rounded once
-    const int sh = fg >= 2 ? 4 : 0;
-    d[0] = (c.v[0] >> sh) & 0x0F0F0F0Fu;
-    d[1] = (c.v[1] >> sh) & 0x0F0F0F0Fu;
-    // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
-    // conversions below then read the bytes of d directly
-    asm("" : "+v"(d[0]), "+v"(d[1]));
-    off = -8.0f * s;
+    const u32x2 p0 = q8_dword_bf16(c.v[0], s), p1 = q8_dword_bf16(c.v[1], s);
+    return __builtin_bit_cast(bf16x8, u32x4{p0[0], p0[1], p1[0], p1[1]});
   }
+  // Q4_0: nibble q, zero-point 8: fma(q, s, -8 s) = s * (q - 8), rounded once
+  const int sh = fg >= 2 ? 4 : 0;
+  uint32_t d[2] = {(c.v[0] >> sh) & 0x0F0F0F0Fu, (c.v[1] >> sh) & 0x0F0F0F0Fu};
+  // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
+  // conversions below then read the bytes of d directly
+  asm("" : "+v"(d[0]), "+v"(d[1]));
+  const float off = -8.0f * s;
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 2; i++) {

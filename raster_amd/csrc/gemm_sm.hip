@@ -102,15 +102,8 @@ __device__ __forceinline__ bf16x8 dequant_q4_dword(uint32_t d, uint32_t sbits) {
 template <typename ST>
 __device__ __forceinline__ bf16x8 dequant_sm_q8(const WCodesSm& c) {
   const float s = scale_from_bits<ST>(c.s);
-  const uint32_t d[2] = {c.v[0] ^ 0x80808080u, c.v[1] ^ 0x80808080u};
-  const float off = -128.0f * s;
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    o[2 * i] = pack2_bf16(fmaf((float)(d[i] & 0xFFu), s, off), fmaf((float)((d[i] >> 8) & 0xFFu), s, off));
-    o[2 * i + 1] = pack2_bf16(fmaf((float)((d[i] >> 16) & 0xFFu), s, off), fmaf((float)(d[i] >> 24), s, off));
-  }
-  return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+  const u32x2 p0 = q8_dword_bf16(c.v[0], s), p1 = q8_dword_bf16(c.v[1], s);
+  return __builtin_bit_cast(bf16x8, u32x4{p0[0], p0[1], p1[0], p1[1]});
 }
 
 }  // namespace

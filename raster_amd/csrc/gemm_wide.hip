@@ -66,24 +66,24 @@ __device__ __forceinline__ void wd_load(WdCodes& c, __amdgpu_buffer_rsrc_t qr, _
 template <int FMT, typename ST>
 __device__ __forceinline__ void wd_dequant(const WdCodes& c, int g, bf16x8& f0, bf16x8& f1) {
   const float s = scale_from_bits<ST>(c.s);
-  uint32_t d[4];
-  float off;
   if (FMT == RQ_Q8_0) {
-    // signed code = u - 128 with u = byte ^ 0x80: fma(u, s, -128 s) = s * code, rounded once
+    u32x2 p[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) d[i] = c.v[i] ^ 0x80808080u;
-    off = -128.0f * s;
-  } else {
-    // lanes of half g = 0 take the low nibbles (elements 0..15 of the block),
-    // g = 1 the high nibbles (16..31): fma(q, s, -8 s) = s * (q - 8)
-    const int sh = 4 * g;
-#pragma unroll
-    for (int i = 0; i < 4; i++) d[i] = (c.v[i] >> sh) & 0x0F0F0F0Fu;
-    // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
-    // conversions below then read the bytes of d directly
-    asm("" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]));
-    off = -8.0f * s;
+    for (int i = 0; i < 4; i++) p[i] = q8_dword_bf16(c.v[i], s);
+    f0 = __builtin_bit_cast(bf16x8, u32x4{p[0][0], p[0][1], p[1][0], p[1][1]});
+    f1 = __builtin_bit_cast(bf16x8, u32x4{p[2][0], p[2][1], p[3][0], p[3][1]});
+    return;
   }
+  // Q4_0: lanes of half g = 0 take the low nibbles (elements 0..15 of the
+  // block), g = 1 the high nibbles (16..31): fma(q, s, -8 s) = s * (q - 8)
+  const int sh = 4 * g;
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) d[i] = (c.v[i] >> sh) & 0x0F0F0F0Fu;
+  // opaque to the known-bits fold (a v_bfe per nibble): the byte-select
+  // conversions below then read the bytes of d directly
+  asm("" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]));
+  const float off = -8.0f * s;
   uint32_t o[8];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -98,19 +98,14 @@ __device__ __forceinline__ void wd_dequant(const WdCodes& c, int g, bf16x8& f0, 
 template <int FMT, typename ST>
 __device__ __forceinline__ bf16x8 wd_dequant_half(const WdCodes& c, int g, int h) {
   const float s = scale_from_bits<ST>(c.s);
-  uint32_t d[2];
-  float off;
   if (FMT == RQ_Q8_0) {
-    d[0] = c.v[2 * h] ^ 0x80808080u;
-    d[1] = c.v[2 * h + 1] ^ 0x80808080u;
-    off = -128.0f * s;
-  } else {
-    const int sh = 4 * g;
-    d[0] = (c.v[2 * h] >> sh) & 0x0F0F0F0Fu;
-    d[1] = (c.v[2 * h + 1] >> sh) & 0x0F0F0F0Fu;
-    asm("" : "+v"(d[0]), "+v"(d[1]));  // as in wd_dequant
-    off = -8.0f * s;
+    const u32x2 p0 = q8_dword_bf16(c.v[2 * h], s), p1 = q8_dword_bf16(c.v[2 * h + 1], s);
+    return __builtin_bit_cast(bf16x8, u32x4{p0[0], p0[1], p1[0], p1[1]});
   }
+  const int sh = 4 * g;
+  uint32_t d[2] = {(c.v[2 * h] >> sh) & 0x0F0F0F0Fu, (c.v[2 * h + 1] >> sh) & 0x0F0F0F0Fu};
+  asm("" : "+v"(d[0]), "+v"(d[1]));  // as in wd_dequant
+  const float off = -8.0f * s;
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 2; i++) {

@@ -262,6 +262,15 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// A dword of Q8_0 codes (signed bytes) as two packed bf16 pairs: RNE of the
+// f32 product scale * code (one rounding, as Raster's dequant). Each byte is
+// converted with its sign by a byte-select conversion (v_cvt_f32_i32 with a
+// sign-extended byte operand), so no bias or offset is needed.
+__device__ __forceinline__ u32x2 q8_dword_bf16(uint32_t v, float s) {
+  return u32x2{pack2_bf16(s * (float)(int8_t)v, s * (float)(int8_t)(v >> 8)),
+               pack2_bf16(s * (float)(int8_t)(v >> 16), s * (float)(int8_t)(v >> 24))};
+}
+
 // Round-to-nearest-even f32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
