@@ -6,10 +6,15 @@ MFMA decode kernel, the GEMM tile chosen by its cost model), so each route is
 checked where it is timed:
 
   Q4_0 (fp16 scales)   m = 1 (v_dot4 GEMV), 6 and 16 (MFMA decode, 4 / 8 K-slices),
-                       32 and 64 (small-m GEMM with K-slices), 256 (prefill GEMM)
+                       32 and 64 (small-m GEMM with K-slices), 256 and 300
+                       (prefill GEMM: K-pair 256 x 128 tiles, 300 with a
+                       partial second row tile)
   Q8_0 (f32 scales)    m = 1 (int8-level decode), 12 and 16 (int8-level decode:
                        the weight is above the MFMA decode's 32 Mi elements),
-                       32 (small-m GEMM with K-slices), 256 (prefill GEMM)
+                       32 (small-m GEMM with K-slices), 256 and 300 (prefill GEMM)
+
+and the K-pair 256 x 128 tiles with a partial last column tile (K = 4096,
+N = 28656, m = 300).
 
 bf16 activations as the workload defines them, plus f32 activations at the
 decode sizes. Each output is checked against the C oracle (qlinear-q8's loop,
@@ -96,7 +101,7 @@ def run(torch, w, x, m, xdt, ydt):
 
 
 @pytest.mark.parametrize("m,xdt", [(1, "bf16"), (1, "f32"), (6, "bf16"), (6, "f32"), (16, "bf16"), (16, "f32"),
-                                   (32, "bf16"), (64, "bf16"), (256, "bf16")])
+                                   (32, "bf16"), (64, "bf16"), (256, "bf16"), (300, "bf16")])
 def test_c5_q4(torch, orc, q4, m, xdt):
     w, (pk, sc) = q4
     x = wl.activations(m, K, seed=500 + m, dtype=xdt)
@@ -112,7 +117,8 @@ def test_c5_q4(torch, orc, q4, m, xdt):
         assert orc.normwise_relerr(y32[:, ROWS], ref) < (TOL_F32 if m <= 16 else TOL_BF16)
 
 
-@pytest.mark.parametrize("m,xdt", [(1, "bf16"), (1, "f32"), (12, "f32"), (16, "bf16"), (32, "bf16"), (256, "bf16")])
+@pytest.mark.parametrize("m,xdt", [(1, "bf16"), (1, "f32"), (12, "f32"), (16, "bf16"), (32, "bf16"), (256, "bf16"),
+                                   (300, "bf16")])
 def test_c5_q8(torch, orc, q8, m, xdt):
     w, (cs, ss) = q8
     x = wl.activations(m, K, seed=600 + m, dtype=xdt)
@@ -128,3 +134,41 @@ def test_c5_q8(torch, orc, q8, m, xdt):
         dense = orc.dequant_q8_dense(cs, ss, K, len(ROWS))
         bound = decomposition_bound(x.reshape(m, K), dense, m, K, len(ROWS))
         assert np.all(np.abs(y[:, ROWS] - ref) <= bound)
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_kpair_128_partial_tiles(torch, ctx, orc, fmt):
+    # m = 300, K = 4096, N = 28656: the tile cost model takes the K-pair
+    # kernel's 256 x 128 tiles (448 tiles, two rounds of the CUs, against 512
+    # of 256 x 112); the second row tile holds 44 rows and the last column
+    # tile 112 columns. Checked against the oracle on rows at both tile edges,
+    # bf16 y against the RNE of f32 y, repeated calls bitwise.
+    import raster_amd
+
+    m, k2, n2 = 300, 4096, 28656
+    edges = [0, 1, 127, 128, 255, 256, 14335, 14336, n2 - 113, n2 - 112, n2 - 17, n2 - 16, n2 - 1]
+    rows = np.unique(np.concatenate([edges, np.linspace(0, n2 - 1, 97).astype(np.int64)]))
+    note(f"K-pair 256x128 partial tiles {fmt} m={m} {n2}x{k2}")
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(n2, k2, seed=71)
+        w = raster_amd.QWeight.q8(codes, scales, n2, k2, ctx)
+        sub = (codes.reshape(n2, k2)[rows].ravel(), scales.reshape(n2, k2 // 32)[rows].ravel())
+    else:
+        packed, sc16 = wl.q4_weights(n2, k2, seed=72)
+        w = raster_amd.QWeight.q4(packed, sc16.view(np.float16), n2, k2, ctx)
+        sub = (packed.reshape(n2, k2 // 2)[rows].ravel(), sc16.reshape(n2, k2 // 32)[rows].ravel())
+    x = wl.activations(m, k2, seed=73, dtype="bf16")
+    xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda().reshape(m, k2).to(torch.bfloat16)
+    yb = w.matmul(xt, out_dtype=torch.bfloat16)
+    yb2 = w.matmul(xt, out_dtype=torch.bfloat16)
+    yf = w.matmul(xt, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    w.destroy()
+    assert torch.equal(yb, yb2), "repeated calls must agree bitwise"
+    assert torch.equal(yb, yf.to(torch.bfloat16)), "bf16 y must be the RNE of f32 y"
+    y = yf.cpu().numpy()
+    if fmt == "q8":
+        ref = orc.qlinear_q8(x, sub[0], sub[1], m, k2, len(rows))
+    else:
+        ref = orc.qlinear_q4(x, sub[0], sub[1], m, k2, len(rows))
+    assert orc.normwise_relerr(y[:, rows], ref.reshape(m, len(rows))) < TOL_BF16
