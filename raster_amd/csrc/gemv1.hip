@@ -23,8 +23,10 @@
 //
 // Work: a workgroup decomposes x into LDS once, then takes 16-row groups
 // g = blockIdx.x + i * gridDim.x; its W waves split each group's blocks
-// (steps of BPL blocks, spw per wave, padded to whole turns of a D-step
-// register ring). The ring streams loads across group boundaries; a group
+// (steps of BPL blocks, interleaved: wave w takes steps w, w + W, ..., so the
+// W waves read adjacent kilobytes at a time; measured 1-3% per call against
+// contiguous runs per wave at K = 8192, N = 28672; spw per wave, padded to
+// whole turns of a D-step register ring). The ring streams loads across group boundaries; a group
 // ends with a shuffle over the lanes of a row, one LDS exchange between the
 // waves (double-buffered, one barrier) and the store, in wave order.
 #include <algorithm>
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
       u = spp - 1;
     }
     const int g = (int)blockIdx.x + gi * (int)gridDim.x;
-    const int st = min(wave * spw + min(u, spw - 1), nsteps - 1);
+    const int st = min(min(u, spw - 1) * W + wave, nsteps - 1);
     const int b0 = min(st * BPL, nb - BPL);  // first block of the load (a short tail rereads)
     const int64_t chunk = (int64_t)g * nb + b0;
     wc[slot].v = *reinterpret_cast<const u32x4*>(q + chunk * (CB / 16) * 16 + lofs);
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_kernel(const uint8_t* __restrict
         const float s = scale_value(wc[i].s);
         load_w(i, lg, lu);
         advance(lg, lu);
-        const int st = wave * spw + u;
+        const int st = u * W + wave;
         if (u < spw && st < nsteps) {
           const int b = min(st * BPL, nb - BPL) + j;
           // a short tail load (shifted back to stay inside the row) rereads
