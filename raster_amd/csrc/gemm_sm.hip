@@ -383,15 +383,21 @@ hipError_t launch_split_reduce(const float* part, void* y, int64_t n, int ks, in
   return hipGetLastError();
 }
 
-// Two weight fragments per wave (128 columns per workgroup) and chunks of 4
-// k-steps (an 8-step weight ring): with the Q4_0 quads, at M = 32 / 64,
-// K = 8192, N = 28672 51.5 / 69.1 us against 55.7 / 78.1 us for one fragment
-// and 8-step chunks.
-constexpr int kSmNTW = 2, kSmKC = 4;
+// Chunks of 4 k-steps (an 8-step weight ring). Weight fragments per wave:
+// two (128 columns per workgroup) for Q4_0 and at m > 32: with the Q4_0
+// quads, at M = 32 / 64, K = 8192, N = 28672 51.5 / 69.1 us against 55.7 /
+// 78.1 us for one fragment and 8-step chunks; Q8_0 at m > 32: M = 48 / 64
+// 72.7 / 75.1 us against 78.8 / 79.5 for one. Q8_0 at m <= 32 takes one
+// fragment (64 columns, twice the workgroups, fewer K-slices: C5 M = 17 / 32
+// in one slice, no reduction): K = 8192, N = 28672, M = 17 / 32 60.9 / 63.1
+// -> 59.1 / 60.6 us per call; K = 4096, N = 11008, M = 32 23.4 -> 21.1;
+// N = 14336, M = 24 24.8 -> 24.4.
+constexpr int kSmKC = 4;
+static int sm_ntw(int format, int64_t m) { return format == RQ_Q8_0 && m <= 32 ? 1 : 2; }
 
-template <int FMT, typename ST, int MT>
+template <int FMT, typename ST, int MT, int NTW>
 static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
-  constexpr int NTW = kSmNTW, KC = kSmKC;
+  constexpr int KC = kSmKC;
   if (hipError_t e = launch_pack_x(a)) return e;
   const dim3 grid((unsigned)((a.npad / 16 + 4 * NTW - 1) / (4 * NTW)), (unsigned)ks);
   hipExtLaunchKernelGGL((gemm_sm_kernel<FMT, ST, MT, NTW, KC>), grid, dim3(256), 0, a.stream, nullptr,
@@ -414,7 +420,7 @@ static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
 // 90.7 / 86.7.
 int gemm_sm_slices(int format, int64_t m, int64_t k, int64_t npad, int cu_count) {
   // Q8_0 moves twice the bytes per step: 12 waves per CU at every m
-  const int64_t waves = (npad / (64 * kSmNTW)) * 4;
+  const int64_t waves = (npad / (64 * sm_ntw(format, m))) * 4;
   const int64_t want = (int64_t)cu_count * (format == RQ_Q8_0 || m > 32 ? 12 : 24);
   int64_t ks = std::max<int64_t>(1, want / std::max<int64_t>(waves, 1));
   ks = std::min<int64_t>(ks, std::max<int64_t>(1, (k / 32) / (8 * kSmKC)));
@@ -445,8 +451,9 @@ bool gemm_sm_takes(int format, int64_t m, int64_t k) {
 
 hipError_t launch_gemm_sm(const MatmulArgs& a, int ks) {
   if (a.m <= 16 || a.m > 64 || a.k > kSmMaxK) return hipErrorInvalidValue;
-#define RQ_SM(FMT_, ST_) return a.m <= 32 ? launch_sm_t<FMT_, ST_, 2>(a, ks) : launch_sm_t<FMT_, ST_, 4>(a, ks);
-  if (a.format == RQ_Q8_0) { RQ_SM(RQ_Q8_0, float) }
+#define RQ_SM(FMT_, ST_) return a.m <= 32 ? launch_sm_t<FMT_, ST_, 2, 2>(a, ks) : launch_sm_t<FMT_, ST_, 4, 2>(a, ks);
+  if (a.format == RQ_Q8_0)
+    return a.m <= 32 ? launch_sm_t<RQ_Q8_0, float, 2, 1>(a, ks) : launch_sm_t<RQ_Q8_0, float, 4, 2>(a, ks);
   if (a.scale_dtype == RQ_F16) { RQ_SM(RQ_Q4_0, uint16_t) }
   RQ_SM(RQ_Q4_0, float)
 #undef RQ_SM
