@@ -82,9 +82,9 @@ int rq_ctx_device_info(rq_ctx ctx, int* cu_count, int* wave_size, int* clock_khz
  * kernel) from the small activation-packing pass of the bf16 GEMM.
  * While enabled, every rq_qmatmul on this context records a pair of HIP
  * events around its main kernel (hipExtLaunchKernel; not on a stream that is
- * being captured): for the bf16 prefill GEMM, the end of the packing pass
- * and the end of the GEMM, which follows it directly; for the other kernels,
- * the dispatch's own start and end. A call whose partial sums a second kernel
+ * being captured): for the bf16 prefill GEMM with a packing pass, the end of
+ * that pass and the end of the GEMM, which follows it directly; for the other
+ * kernels, the dispatch's own start and end. A call whose partial sums a second kernel
  * adds counts as one launch timed as the sum of its two kernels' own
  * durations (the gap between them excluded).
  * rq_ctx_kernel_time waits for the pending pairs, returns their summed
@@ -201,7 +201,8 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  * Scratch (per stream, allocated on first use, grown on demand, freed by
  * rq_ctx_destroy; calls on one stream are ordered, calls on different streams
  * do not share it):
- *  - bf16 x with m > 16: the packed activation tile, ceil(m/32)*32*in*2 bytes;
+ *  - bf16 x with m > 16, except in the weight-stream GEMM (which reads x as
+ *    it is): the packed activation tile, ceil(m/32)*32*in*2 bytes;
  *  - K-slices' partial sums, m * out * 4 bytes per slice, added in slice
  *    order by a second kernel: the int8-level decode kernel when a row of x
  *    does not fit one workgroup's LDS (in above 17472 at m <= 4, 8704 at

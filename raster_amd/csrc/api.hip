@@ -899,18 +899,18 @@ static int run_matmul(Ctx* c, const Weight& w, const DecodePlan& plan, const voi
   } else if (!plan.ok && x_dtype == RQ_BF16 && wide.ok) {
     // the 32x32x16 operand copy of x: ceil(m/32)*32 rows
     if (int s = call_scratch(c, fixed, a.stream, pack_x32_bytes(m, w.in), 0, &a.scratch)) return s;
+  } else if (!plan.ok && x_dtype == RQ_BF16 && gemm_sm_takes(w.format, m, w.in)) {
+    // the weight-stream GEMM reads x as it is; K-slices' partial sums
+    a.slices = gemm_sm_slices(w.format, m, w.in, w.npad, c->cu_count);
+    if (a.slices > 1) {
+      if (int s = call_scratch(c, fixed, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, 1, &part))
+        return s;
+    }
   } else if (!plan.ok && x_dtype == RQ_BF16) {
     // fragment-major copy of the activations: ceil(m/16)*16 rows (16x16x32
     // operands), or ceil(m/32)*32 rows for the 32x32x16 K-pair kernel
     const size_t bytes = std::max((size_t)((m + 15) / 16 * 16) * (size_t)w.in * 2, pack_x32_bytes(m, w.in));
     if (int s = call_scratch(c, fixed, a.stream, bytes, 0, &a.scratch)) return s;
-    if (gemm_sm_takes(w.format, m, w.in)) {
-      a.slices = gemm_sm_slices(w.format, m, w.in, w.npad, c->cu_count);
-      if (a.slices > 1) {
-        if (int s = call_scratch(c, fixed, a.stream, (size_t)a.slices * (size_t)m * (size_t)w.out * 4, 1, &part))
-          return s;
-      }
-    }
   } else if (!plan.ok && x_dtype == kXtI8) {
     // fragment-major int8 activations with their scales and sums: 640 B per
     // 16-row tile and 32-block

@@ -9,10 +9,18 @@
 // but its activation loads are consumed 3 steps after issue, and loads
 // complete in issue order: waiting for an activation load also waits for
 // every older weight load, so the weights get ~3 steps of slack whatever WD
-// is. Here the activations (the fragment-major copy of pack_x_kernel) come in
-// chunks of KC k-steps staged in LDS (double-buffered, one burst of loads per
-// chunk, consumed a whole chunk after issue), so the weight ring can be
-// WD = 2 KC steps deep. Each wave owns NTW 16-row weight fragments; the 4
+// is. Here the activations come in chunks of KC k-steps staged in LDS
+// (double-buffered, one burst of loads per chunk, consumed a whole chunk after
+// issue), so the weight ring can be WD = 2 KC steps deep. They are read from
+// row-major x itself, no packing pass: a wave's load takes 4 rows x 256
+// contiguous bytes (the chunk's 4 blocks), and the LDS slots are rotated per
+// lane group so that these stores, like the MFMA reads, hit every bank
+// (against the packing kernel's fragment-major copy: C5 Q8_0 M = 32 61.5 ->
+// 59.4 us per call, Q4_0 49.4 -> 48.2, K = 4096, N = 11008 Q8_0 M = 32 21.0 ->
+// 19.0; Q4_0 at M = 64 61.1 -> 62.3). Loading 16 rows x 64 bytes per wave
+// instead (each lane's natural piece) measured C5 Q8_0 M = 32 65.3 us, and
+// 4 x 256 bytes without the rotated slots (4-way bank conflicts on the
+// stores) Q4_0 M = 64 67.7. Each wave owns NTW 16-row weight fragments; the 4
 // waves of a workgroup cover 64 NTW columns and all of m (MT 16-row tiles).
 // K may be cut into ks slices (grid.y) whose f32 partial sums a second kernel
 // adds in slice order (deterministic), for more waves in flight.
@@ -106,11 +114,18 @@ __device__ __forceinline__ bf16x8 dequant_sm_q8(const WCodesSm& c) {
   return __builtin_bit_cast(bf16x8, u32x4{p0[0], p0[1], p1[0], p1[1]});
 }
 
+// The 16-byte slot of lane (r, g) of the activation fragment of step u in
+// LDS: within each 256-byte lane group the rows are rotated by 4 g + 4 (u % 2).
+// The MFMA reads stay one permutation of each lane group (no bank conflicts),
+// and a staging store of 4 rows x 4 lane groups x 4 steps (16 bytes each), or
+// of their 8-byte halves (Q4_0), spreads over all banks.
+__device__ __forceinline__ int sm_slot(int u, int g, int r) { return 16 * g + ((r + 4 * g + 4 * (u & 1)) & 15); }
+
 }  // namespace
 
 template <int FMT, typename ST, int MT, int NTW, int KC>
 __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict__ q, const ST* __restrict__ sc,
-                                                     const uint16_t* __restrict__ xf, void* __restrict__ y,
+                                                     const uint16_t* __restrict__ x, void* __restrict__ y,
                                                      float* __restrict__ part, int M, int K, int N, int npad,
                                                      int y_dtype) {
   constexpr int WD = 2 * KC;             // weight ring depth (steps)
@@ -127,7 +142,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
   const int n0 = (int)blockIdx.x * 64 * NTW;
-  const int g_last = npad / 16 - 1, mt_last = (M + 15) / 16 - 1;
+  const int g_last = npad / 16 - 1;
   // buffer resources: this workgroup's weight groups (codes, scales) and the
   // packed activations. A load's k position and group are uniform offsets;
   // groups past the last one read zeros (their outputs are never stored).
@@ -136,47 +151,49 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
   const __amdgpu_buffer_rsrc_t qr = sm_rsrc(q + (int64_t)gq0 * nkb * CB, (uint32_t)(ngr * nkb) * CB);
   const __amdgpu_buffer_rsrc_t sr =
       sm_rsrc(sc + (int64_t)gq0 * nkb * 16, (uint32_t)(ngr * nkb) * 16u * (uint32_t)sizeof(ST));
-  const __amdgpu_buffer_rsrc_t xr = sm_rsrc(xf, (uint32_t)((mt_last + 1) * nkb) * 1024u);
+  const __amdgpu_buffer_rsrc_t xr = sm_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
   const int nstm = max(nst - 1, 0);
   uint32_t gofs[NTW];  // chunk row of group j (uniform)
 #pragma unroll
   for (int j = 0; j < NTW; j++) gofs[j] = (uint32_t)__builtin_amdgcn_readfirstlane((wave * NTW + j) * nkb + kb0);
 
-  // activation pieces of a chunk: piece p = tid + 256 i is step p / (64 MT),
-  // tile (p / 64) % MT, lane p % 64 (tiles past the packed rows are clamped:
-  // they only feed outputs that are never stored)
+  // activation pieces of a chunk, straight from row-major x: piece
+  // p = tid + 256 i holds the 16 bytes k = 32 kb + 8 g .. + 7 of row R = p / 16
+  // (tile R / 16, row r = R % 16), kb the chunk's step u, with
+  // (u, g) = (p % 16 / 4, p % 4): a wave's load reads 4 rows of 256
+  // contiguous bytes each. Rows past m read zeros (they only feed outputs that
+  // are never stored); steps past the slice reread its last step (zeroed when
+  // staged).
   u32x4 areg[AP];
   auto load_a = [&](int c) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
-      const int p = tid + 256 * i, t = (p / 64) % MT, l = p % 64;
-      const int u = __builtin_amdgcn_readfirstlane(p / (64 * MT));  // the same in a wave
-      const uint32_t kb = (uint32_t)(kb0 + min(c * KC + u, nstm));
-      areg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              xr, (int)(((uint32_t)(min(t, mt_last) * nkb) * 64u + (uint32_t)l) * 16u),
-                                              (int)(kb * 1024u), 0));
+      const int p = tid + 256 * i, q = p & 15;
+      const uint32_t kb = (uint32_t)(kb0 + min(c * KC + (q >> 2), nstm));
+      areg[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     xr, (int)((uint32_t)(p >> 4) * (uint32_t)K * 2u + kb * 64u + 16u * (uint32_t)(q & 3)), 0, 0));
     }
   };
   auto store_a = [&](int buf, int c) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
-      const int p = tid + 256 * i;
-      if (c * KC + p / (64 * MT) >= nst) areg[i] = u32x4{0u, 0u, 0u, 0u};  // a step past the slice adds nothing
+      const int p = tid + 256 * i, q = p & 15, u = q >> 2, g = q & 3, t = p >> 8, r = (p >> 4) & 15;
+      if (c * KC + u >= nst) areg[i] = u32x4{0u, 0u, 0u, 0u};  // a step past the slice adds nothing
       if (FMT == RQ_Q4_0) {
         // the piece of lane (r, g) holds k = 8g .. 8g+7: k = 8g .. 8g+3 go
         // to lane group 2 (g & 1), 8g+4 .. 8g+7 to the next one, the upper
         // half of the block (g >= 2) to the upper 8 bytes of each
-        const int l = p & 63, r = l & 15, g = l >> 4;
-        uint8_t* base = reinterpret_cast<uint8_t*>(&As[buf][0][0][0]) + (p >> 6) * 1024;
-        const int o0 = ((2 * (g & 1)) * 16 + r) * 16 + 8 * (g >> 1);
-        *reinterpret_cast<u32x2*>(base + o0) = u32x2{areg[i][0], areg[i][1]};
-        *reinterpret_cast<u32x2*>(base + o0 + 256) = u32x2{areg[i][2], areg[i][3]};
+        const int g0 = 2 * (g & 1);
+        uint8_t* base = reinterpret_cast<uint8_t*>(&As[buf][u][t][0]) + 8 * (g >> 1);
+        *reinterpret_cast<u32x2*>(base + 16 * sm_slot(u, g0, r)) = u32x2{areg[i][0], areg[i][1]};
+        *reinterpret_cast<u32x2*>(base + 16 * sm_slot(u, g0 + 1, r)) = u32x2{areg[i][2], areg[i][3]};
       } else {
-        reinterpret_cast<u32x4*>(&As[buf][0][0][0])[p] = areg[i];
+        *reinterpret_cast<u32x4*>(&As[buf][u][t][sm_slot(u, g, r)]) = areg[i];
       }
     }
   };
-  static_assert(KC % 4 == 0, "chunks of whole Q4_0 quads");
+  static_assert(KC == 4, "a chunk is one Q4_0 quad, and 16 activation pieces per row");
   WCodesSm wc[FMT == RQ_Q4_0 ? 1 : WD][NTW];
   WQuadSm wq[FMT == RQ_Q4_0 ? WD / 4 : 1][NTW];
   auto load_w = [&](int slot, int s) {  // step s of the slice (clamped)
@@ -282,7 +299,7 @@ __global__ __launch_bounds__(256) void gemm_sm_kernel(const uint8_t* __restrict_
       }
       bf16x8 af[MT];
 #pragma unroll
-      for (int i = 0; i < MT; i++) af[i] = As[buf][u][i][lane];
+      for (int i = 0; i < MT; i++) af[i] = As[buf][u][i][sm_slot(u, fg, fr)];
 #pragma unroll
       for (int j = 0; j < NTW; j++)
 #pragma unroll
@@ -398,12 +415,10 @@ static int sm_ntw(int format, int64_t m) { return format == RQ_Q8_0 && m <= 32 ?
 template <int FMT, typename ST, int MT, int NTW>
 static hipError_t launch_sm_t(const MatmulArgs& a, int ks) {
   constexpr int KC = kSmKC;
-  if (hipError_t e = launch_pack_x(a)) return e;
   const dim3 grid((unsigned)((a.npad / 16 + 4 * NTW - 1) / (4 * NTW)), (unsigned)ks);
-  hipExtLaunchKernelGGL((gemm_sm_kernel<FMT, ST, MT, NTW, KC>), grid, dim3(256), 0, a.stream, nullptr,
-                        a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
-                        static_cast<const uint16_t*>(a.scratch), a.y, a.part, (int)a.m, (int)a.k, (int)a.n,
-                        (int)a.npad, a.y_dtype);
+  hipExtLaunchKernelGGL((gemm_sm_kernel<FMT, ST, MT, NTW, KC>), grid, dim3(256), 0, a.stream, a.ev_main[0],
+                        a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales), static_cast<const uint16_t*>(a.x),
+                        a.y, a.part, (int)a.m, (int)a.k, (int)a.n, (int)a.npad, a.y_dtype);
   if (hipError_t e = hipGetLastError()) return e;
   if (ks > 1) return launch_split_reduce(a.part, a.y, a.m * a.n, ks, a.y_dtype, a.stream, a.ev_aux[0], a.ev_aux[1]);
   return hipSuccess;
