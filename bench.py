@@ -1060,9 +1060,9 @@ def main():
                    "m": 512, "k": 4096, "n": 11008, "weights": "q8_0 resident in HBM"},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": read_traffic("gemm_pair_q8_C2"),
+                     "traffic": read_traffic("gemm_rs_q8_C2"),
                      "peak_from_device_props": round(peak_props, 1),
-                     "kernel": "rq::gemm_pair_kernel", "flop_per_launch": flops,
+                     "kernel": "rq::gemm_rs_kernel", "flop_per_launch": flops,
                      "kernel_avg_us": round(kern_ms * 1e3, 3), "kernel_launches": kern_n},
     }
     if head_cold is not None:

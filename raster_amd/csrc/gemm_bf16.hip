@@ -737,12 +737,13 @@ static hipError_t launch_wk(const MatmulArgs& a) {
 // same way. For M <= 64 the weight stream is latency-bound: 64 x 64 tiles
 // (twice the workgroups of 64 x 128) measured 126 against 151 us (Q4) and 68
 // against 81 us (Q8) at M = 32, K = 8192, N = 28672.
-// The K-pair kernel (gemm_wide.hip, 32x32x16 MFMA, K a multiple of 64) takes
-// the 256 x 96 tile and a fifth candidate, 256 x 128, at 0.85 of the cost of
-// its area: at M = 256, K = 8192, N = 28672 (cold, same box) its 224 tiles of
-// 256 x 128 took 125.5 us (Q8) / 121.5 us (Q4, f16 scales) against 130.5 /
-// 123.0 us for the 256 tiles of 256 x 112, 0.84 / 0.87 of the time per tile
-// area; M = 300: 227 against 235 us.
+// The 32x32x16 kernels of gemm_wide.hip (K a multiple of 64) take the
+// 256 x 96 tile and a fifth candidate, 256 x 128, at 0.85 of the cost of its
+// area: at M = 256, K = 8192, N = 28672 (cold, same box) the 224 tiles of
+// 256 x 128 took 125.5 us (Q8) / 121.5 us (Q4, f16 scales) in the K-pair
+// kernel that preceded the role-split one, against 130.5 / 123.0 us for the
+// 256 tiles of 256 x 112, 0.84 / 0.87 of the time per tile area; M = 300: 227
+// against 235 us. The role-split kernel is 4-10% faster again there.
 template <int FMT, typename ST>
 static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
   if (a.m > 128) {
@@ -759,12 +760,12 @@ static hipError_t launch_mt(const MatmulArgs& a, int cu_count) {
         best = i;
       }
     }
-    // 256 x 96: the K-pair kernel on 32x32x16 MFMA (C2 step 52.5 against
-    // 54.2 us for gemm_wk_kernel, same box and data)
-    if (best == 0) return pair ? launch_gemm_pair(a, 3) : launch_wk<FMT, ST, 6>(a);
+    // 256 x 96: the role-split kernel on 32x32x16 MFMA (C2 step 52.5 against
+    // 54.2 us for gemm_wk_kernel with its K-pair predecessor, same box and data)
+    if (best == 0) return pair ? launch_gemm_rs(a, 3) : launch_wk<FMT, ST, 6>(a);
     if (best == 1) return launch_wl<FMT, ST, 4, 4, 4, 2>(a);
     if (best == 2) return launch_wl<FMT, ST, 4, 3, 4, 2>(a);
-    if (best == 4) return launch_gemm_pair(a, 4);
+    if (best == 4) return launch_gemm_rs(a, 4);
     return launch_wk<FMT, ST, 7>(a);
   }
   if (a.m <= 64) return launch_t<FMT, ST, 4, 1>(a);

@@ -94,27 +94,6 @@ __device__ __forceinline__ void wd_dequant(const WdCodes& c, int g, bf16x8& f0, 
   f1 = __builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]});
 }
 
-// one half (codes 0..7 or 8..15) of wd_dequant
-template <int FMT, typename ST>
-__device__ __forceinline__ bf16x8 wd_dequant_half(const WdCodes& c, int g, int h) {
-  const float s = scale_from_bits<ST>(c.s);
-  if (FMT == RQ_Q8_0) {
-    const u32x2 p0 = q8_dword_bf16(c.v[2 * h], s), p1 = q8_dword_bf16(c.v[2 * h + 1], s);
-    return __builtin_bit_cast(bf16x8, u32x4{p0[0], p0[1], p1[0], p1[1]});
-  }
-  const int sh = 4 * g;
-  uint32_t d[2] = {(c.v[2 * h] >> sh) & 0x0F0F0F0Fu, (c.v[2 * h + 1] >> sh) & 0x0F0F0F0Fu};
-  asm("" : "+v"(d[0]), "+v"(d[1]));  // as in wd_dequant
-  const float off = -8.0f * s;
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    o[2 * i] = pack2_bf16(fmaf((float)(d[i] & 0xFFu), s, off), fmaf((float)((d[i] >> 8) & 0xFFu), s, off));
-    o[2 * i + 1] = pack2_bf16(fmaf((float)((d[i] >> 16) & 0xFFu), s, off), fmaf((float)(d[i] >> 24), s, off));
-  }
-  return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
-}
-
 }  // namespace
 
 // x[M][K] (bf16) -> xf[M/32][K/32][2][64][8]: fragment (tile, kb, j), lane l =
@@ -419,39 +398,35 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   }
 }
 
-// K-pair variant for shapes whose 256 x 192 tiles are too few for the CUs
-// (C2: M 512, N 11008): 256 x 32 NF tiles (NF 3: 96 columns; NF 4: 128, for
-// shapes whose 128-column tiles fill the CUs in whole rounds, C5 at M 256),
-// eight waves, two per SIMD. Waves w and w + 4 share a SIMD and rows
-// 64 (w % 4) .. + 63 (two 32-row fragments) and split each macro step's two
-// 32-k steps: wave w takes the first, w + 4 the second, so each holds a
-// 64 x 32 NF accumulator tile and the two waves of a SIMD hide each other's
-// waits. The 2 NF dequant units of a macro step (NF n fragments x 2 k-steps)
-// go to waves 0 .. 2 NF - 1. At the end the
-// second-k waves pass their accumulators through LDS to the first-k waves,
-// which add them (two interleaved partial sums of K) and stage the tile for
-// whole-row stores.
-// Per macro step a wave: issues its activation loads RA - 1 macro steps ahead
-// and its weight unit RW ahead, reads its k-step's half-0 fragments (read at
-// the end of the previous step), runs 2 NF MFMAs while dequantizing, then after
-// the barrier reads the next step's half-0 fragments and runs the half-1 MFMAs.
-template <int FMT, typename ST, int RA, int RW, int NB, int NF>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void gemm_pair_kernel(
+// Role-split variant of the 256 x 32 NF tile: eight waves, two per SIMD, one
+// of each kind. Waves 0..3 (consumers) own rows 64 w .. + 63 and all of K: each
+// issues only its activation loads (RA - 1 macro steps ahead, straight into
+// registers), the LDS reads of the dequantized weight fragments (one 16-k
+// sub-step ahead) and the MFMAs, so its SIMD's matrix pipe never waits behind
+// dequantization. Waves 4..7 (producers) load the weight units RW - 1 macro
+// steps ahead and dequantize the units of macro step s + 2 into LDS buffer
+// (s + 2) % 3 while the consumers run step s; their VALU work issues beside the
+// partner consumer's MFMAs. One barrier per macro step: a buffer is written two
+// barriers before its first read and one barrier after its last, so the
+// consumers also read the next step's first fragments before the barrier.
+// The 2 NF units of a macro step (n fragment, k-step) go to producer p as
+// units p and p + 4. At the end each consumer stages its tile through LDS, 32
+// rows at a time, and it and its SIMD's producer each store 16 of the rows.
+template <int FMT, typename ST, int NF, int RA, int RW>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2))) void gemm_rs_kernel(
     const uint8_t* __restrict__ q, const ST* __restrict__ sc, const uint16_t* __restrict__ xf, void* __restrict__ y,
     int M, int K, int N, int npad, int y_dtype, int tiles_m, uint32_t xf_bytes) {
+  constexpr int NB = 3;
   constexpr int NU = 2 * NF;
   static_assert(NF == 3 || NF == 4, "column fragments per tile");
-  constexpr int U = (RA == 3 || RW == 3 || NB == 3) ? ((RA == 4 || RW == 4) ? 12 : 6) : 4;
-  static_assert((RA == 2 || RA == 3 || RA == 4) && (RW == 2 || RW == 3 || RW == 4), "ring depths");
-  static_assert(NB == 2 || NB == 3, "LDS ring: 2 or 3 buffers");
-  static_assert(U % RA == 0 && U % RW == 0 && U % NB == 0, "unroll covers the rings");
-  // LDS: the weight ring Bs[buf][k-step][half][n frag][lane] (NB x 4 NF KB), or
-  // at the end the pair reduction (4 waves x 4 NF KB) and the staging (4 waves
-  // x 32 rows x RS: a row of 32 NF f32 and 16 bytes against bank conflicts)
+  static_assert(NU <= 8, "two units per producer at most");
+  // unrolled macro steps: whole turns of the rings (lcm of the depths)
+  constexpr int UC = RA % NB == 0 ? RA : RA * NB;
+  constexpr int UP = RW % NB == 0 ? RW : RW * NB;
+  static_assert(UC % RA == 0 && UC % NB == 0 && UP % RW == 0 && UP % NB == 0, "unroll covers the rings");
   constexpr int RS = 32 * NF * 4 + 16;
-  constexpr int kRing = NB * 2 * 2 * NF * 64 * 16, kRed = 4 * NF * 4 * 64 * 16, kStage = 4 * 32 * RS;
-  constexpr int kLo = kRing > kRed ? kRing : kRed;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLo + kStage];
+  constexpr int kRing = NB * 2 * 2 * NF * 64 * 16, kStage = 4 * 32 * RS;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kRing + kStage];
   typedef bf16x8 RingT[2][2][NF][64];
   RingT* Bs = reinterpret_cast<RingT*>(lds);
 
@@ -461,244 +436,149 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
   const int tm = tord % tiles_m, tn = tord / tiles_m;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 3, kh = wave >> 2;  // row block, k-step of the macro step
+  const int wm = wave & 3;
   const int nkb = K / 32;
   const int steps = nkb / 2;
   const int m0 = tm * 256 + wm * 64;
   const int n0 = tn * 32 * NF;
   const int g = lane >> 5;
-
-  const int r32_last = (M + 31) / 32 - 1;
-  const __amdgpu_buffer_rsrc_t xr = wd_rsrc(xf, xf_bytes);
-  const uint32_t a_lo = 16u * lane;
-  uint32_t a_row[2];
-#pragma unroll
-  for (int f = 0; f < 2; f++)
-    a_row[f] = (uint32_t)__builtin_amdgcn_readfirstlane((min(m0 / 32 + f, r32_last) * nkb + kh) * 2048);
-  constexpr uint32_t CB = FMT == RQ_Q8_0 ? 512u : 256u, RB = FMT == RQ_Q8_0 ? 32u : 16u;
-  const __amdgpu_buffer_rsrc_t qr = wd_rsrc(q, (uint32_t)(npad / 16) * (uint32_t)nkb * CB);
-  const __amdgpu_buffer_rsrc_t sr = wd_rsrc(sc, (uint32_t)npad * (uint32_t)nkb * (uint32_t)sizeof(ST));
-  // this wave's dequant unit (waves 0..5): n fragment wave % NF, k-step wave / NF
-  const bool has_unit = wave < NU;
-  const int uu = min(wave, NU - 1);
-  const int g_last = npad / 16 - 1;
-  const uint32_t grp = (uint32_t)min(n0 / 16 + 2 * (uu % NF) + ((lane & 31) >> 4), g_last);
-  const uint32_t w_lo = grp * (uint32_t)nkb * CB + (uint32_t)(lane & 15) * RB + (FMT == RQ_Q8_0 ? 16u * (uint32_t)g : 0u);
-  const uint32_t w_so = (grp * (uint32_t)nkb * 16u + (uint32_t)(lane & 15)) * (uint32_t)sizeof(ST);
-  const uint32_t w_ks = (uint32_t)__builtin_amdgcn_readfirstlane(uu / NF);
-
-  f32x16 acc[2][NF];
-#pragma unroll
-  for (int f = 0; f < 2; f++)
-#pragma unroll
-    for (int c = 0; c < NF; c++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[f][c][e] = 0.0f;
-
-  bf16x8 a[RA][2][2];  // [slot][m frag][half] of this wave's k-step
-  WdCodes wc[RW];
-  bf16x8 b[2][NF];
-
-#define PR_LOAD_A(ms_, slot_)                                                                   \
-  do {                                                                                          \
-    const uint32_t ko_ = (uint32_t)(2 * min((ms_), steps - 1)) * 2048u;                         \
-    _Pragma("unroll") for (int f = 0; f < 2; f++)                                               \
-      _Pragma("unroll") for (int j = 0; j < 2; j++) a[slot_][f][j] = __builtin_bit_cast(        \
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(a_lo + 1024u * j), (int)(a_row[f] + ko_), 0)); \
-  } while (0)
-#define PR_LOAD_W(ms_, slot_)                                                                   \
-  do {                                                                                          \
-    wd_load<FMT, ST>(wc[slot_], qr, sr, w_lo, w_so, (uint32_t)(2 * min((ms_), steps - 1)) + w_ks);    \
-  } while (0)
-#define PR_DEQUANT(slot_, buf_)                                                                 \
-  do {                                                                                          \
-    if (has_unit) {                                                                             \
-      bf16x8 f0_, f1_;                                                                          \
-      wd_dequant<FMT, ST>(wc[slot_], g, f0_, f1_);                                              \
-      Bs[buf_][uu / NF][0][uu % NF][lane] = f0_;                                                \
-      Bs[buf_][uu / NF][1][uu % NF][lane] = f1_;                                                \
-    }                                                                                           \
-  } while (0)
-#define PR_DEQUANT_H(slot_, buf_, h_)                                                           \
-  do {                                                                                          \
-    if (has_unit) {                                                                             \
-      const bf16x8 fh_ = wd_dequant_half<FMT, ST>(wc[slot_], g, h_);                            \
-      Bs[buf_][uu / NF][h_][uu % NF][lane] = fh_;                                               \
-    }                                                                                           \
-  } while (0)
-#define PR_READ_B(buf_, j_, bb_)                                                                \
-  do {                                                                                          \
-    _Pragma("unroll") for (int c = 0; c < NF; c++) b[bb_][c] = Bs[buf_][kh][j_][c][lane];       \
-  } while (0)
-#define PR_MFMA(aslot_, j_, bb_)                                                                \
-  do {                                                                                          \
-    _Pragma("unroll") for (int c = 0; c < NF; c++)                                              \
-      _Pragma("unroll") for (int f = 0; f < 2; f++) acc[f][c] =                                 \
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[bb_][c], a[aslot_][f][j_], acc[f][c], 0, 0, 0); \
-  } while (0)
-
-  // Prologue loads in the order the steps keep them in flight (the weights of
-  // the first three macro steps, then activations and weights interleaved),
-  // so that the loop's first step has as many younger loads behind each
-  // operand as any later step: the compiler's wait counts at the loop head
-  // (the merge of the prologue and the back edge) then stay as deep as inside
-  // the loop instead of draining the ring once per unrolled turn. The weight
-  // loads are unconditional for the same reason (waves 6 and 7 fetch wave
-  // 5's unit and do not dequantize it): every path issues the same loads.
-  static_assert(RA == 4 && RW == 4 && NB == 3, "prologue order written for these ring depths");
-  PR_LOAD_W(0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_W(1, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_W(2, 2);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_A(0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_W(3, 3);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_A(1, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_DEQUANT(0, 0);
-  PR_DEQUANT(1, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_W(4, 0);  // the steps load from RW + 1 on
-  __builtin_amdgcn_sched_barrier(0);
-  PR_LOAD_A(2, 2);
-  __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();
-  PR_READ_B(0, 0, 0);
-
-#define PR_SCHED(nds_, nvm_, nv_, ndw_)                                                         \
-  do {                                                                                          \
-    __builtin_amdgcn_sched_group_barrier(0x100, (nds_), 0);                                     \
-    __builtin_amdgcn_sched_group_barrier(0x020, (nvm_), 0);                                     \
-    _Pragma("unroll") for (int i_ = 0; i_ < 2 * NF; i_++) {                                     \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                        \
-      __builtin_amdgcn_sched_group_barrier(0x002, (nv_), 0);                                    \
-    }                                                                                           \
-    __builtin_amdgcn_sched_group_barrier(0x200, (ndw_), 0);                                     \
-  } while (0)
-// NB 2: the next macro step's unit is dequantized in phase 0, before the
-// barrier that makes it visible. NB 3: the unit two steps ahead is
-// dequantized, half in each phase (one barrier later is soon enough).
-#define PR_STEP(ms_, u_)                                                                        \
-  do {                                                                                          \
-    PR_READ_B((u_) % NB, 1, 1);                                                                 \
-    PR_LOAD_A((ms_) + RA - 1, ((u_) + RA - 1) % RA);                                            \
-    PR_MFMA((u_) % RA, 0, 0);                                                                   \
-    if (NB == 2) {                                                                              \
-      PR_LOAD_W((ms_) + RW, (u_) % RW);                                                         \
-      PR_DEQUANT(((u_) + 1) % RW, ((u_) + 1) % NB);                                             \
-      PR_SCHED(NF, 6, 8, 2);                                                                    \
-    } else {                                                                                    \
-      PR_DEQUANT_H(((u_) + 2) % RW, ((u_) + 2) % NB, 0);                                        \
-      PR_SCHED(NF, 4, 4, 1);                                                                    \
-    }                                                                                           \
-    __builtin_amdgcn_sched_barrier(0);                                                          \
-    __syncthreads();                                                                            \
-    __builtin_amdgcn_sched_barrier(0);                                                          \
-    PR_READ_B(((u_) + 1) % NB, 0, 0);                                                           \
-    PR_MFMA((u_) % RA, 1, 1);                                                                   \
-    if (NB == 3) {                                                                              \
-      PR_LOAD_W((ms_) + RW + 1, ((u_) + RW + 1) % RW);                                          \
-      PR_DEQUANT_H(((u_) + 2) % RW, ((u_) + 2) % NB, 1);                                        \
-      PR_SCHED(NF, 2, 4, 1);                                                                    \
-    }                                                                                           \
-    __builtin_amdgcn_sched_barrier(0);                                                          \
-  } while (0)
-
-  int ms = 0;
-  for (; ms + U <= steps; ms += U) {
-#pragma unroll
-    for (int u = 0; u < U; u++) PR_STEP(ms + u, u);
-  }
-#pragma unroll
-  for (int u = 0; u < U - 1; u++)
-    if (ms + u < steps) PR_STEP(ms + u, u);
-#undef PR_STEP
-#undef PR_SCHED
-#undef PR_DEQUANT_H
-#undef PR_MFMA
-#undef PR_READ_B
-#undef PR_DEQUANT
-#undef PR_LOAD_W
-#undef PR_LOAD_A
-
-  // pair sum and output, one m fragment (32 rows) per round. The two waves of
-  // a pair each finish half of every 32-column fragment: the first-k wave
-  // columns 0..15 (registers e < 8), the second-k wave columns 16..31 (e >= 8).
-  // Each hands the other half to its partner through LDS, adds the half it
-  // receives (a + b in either order is the same f32 sum) and stages its
-  // columns of all 32 rows; then each stores 16 of the rows as whole-row
-  // pieces. acc[f][c] register e: m = m0 + 32 f + lane % 32,
-  // n = n0 + 32 c + 8 (e / 4) + 4 g + e % 4
   const int mrow = lane & 31;
   const int ncols = min(32 * NF, N - n0);
   const int ebytes = y_dtype == RQ_F32 ? 4 : 2;
   const bool staged = ((int64_t)N * ebytes) % 16 == 0 && (ncols * ebytes) % 16 == 0 &&
                       (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-  // per row block: the first-k waves' columns 16..31 at [0, 2 NF), the
-  // second-k waves' columns 0..15 at [2 NF, 4 NF) (f32x4 slots of 64 lanes)
-  f32x4* red = reinterpret_cast<f32x4*>(lds) + wm * (NF * 4 * 64) + lane;
-  f32x4* give = red + (kh == 0 ? 0 : 2 * NF * 64);
-  const f32x4* take = red + (kh == 0 ? 2 * NF * 64 : 0);
-  const int q0 = kh == 0 ? 0 : 2;  // first register quad this wave keeps
-  uint8_t* st = lds + kLo + wm * (32 * RS);
-  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  uint8_t* st = lds + kRing + wm * (32 * RS);
+  const int ppr = 32 * NF * ebytes / 16, vpr = ncols * ebytes / 16;
+
+  if (wave < 4) {
+    // ---- consumer ----
+    const int r32_last = (M + 31) / 32 - 1;
+    const __amdgpu_buffer_rsrc_t xr = wd_rsrc(xf, xf_bytes);
+    const uint32_t a_lo = 16u * lane;
+    uint32_t a_row[2];
 #pragma unroll
-  for (int f = 0; f < 2; f++) {
-    __syncthreads();  // the ring (or the previous round's staging) is no longer read
+    for (int f = 0; f < 2; f++)
+      a_row[f] = (uint32_t)__builtin_amdgcn_readfirstlane(min(m0 / 32 + f, r32_last) * nkb * 2048);
+
+    f32x16 acc[2][NF];
 #pragma unroll
-    for (int c = 0; c < NF; c++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int qq = 2 - q0 + h;  // the quads the partner keeps
-        give[(c * 2 + h) * 64] =
-            f32x4{acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
-      }
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < NF; c++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int qq = q0 + h;
-        const f32x4 p = take[(c * 2 + h) * 64];
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[f][c][4 * qq + e] += p[e];
-      }
-    if (staged) {
+    for (int f = 0; f < 2; f++)
 #pragma unroll
       for (int c = 0; c < NF; c++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const int qq = q0 + h;
-          const int col = 32 * c + 8 * qq + 4 * g;
-          if (y_dtype == RQ_F32)
-            *reinterpret_cast<f32x4*>(st + mrow * RS + col * 4) =
-                f32x4{acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
-          else
-            *reinterpret_cast<u32x2*>(st + mrow * RS + col * 2) =
-                u32x2{pack2_bf16(acc[f][c][4 * qq], acc[f][c][4 * qq + 1]),
-                      pack2_bf16(acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3])};
-        }
-      __syncthreads();  // both halves of every row staged
-      const int ppr = 32 * NF * ebytes / 16, vpr = ncols * ebytes / 16;
-      for (int p = lane; p < 16 * ppr; p += 64) {
-        const int r = 16 * kh + p / ppr, pc = p % ppr;
-        const int m = m0 + 32 * f + r;
-        if (m < M && pc < vpr) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RS + pc * 16);
-          *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(y) + ((int64_t)m * N + n0) * ebytes + pc * 16) = v;
+        for (int e = 0; e < 16; e++) acc[f][c][e] = 0.0f;
+    bf16x8 a[RA][2][2][2];  // [slot][m frag][k-step][half]
+    bf16x8 b[2][NF];
+
+#define SC_LOAD_A(ms_, slot_, ks_)                                                              \
+  do {                                                                                          \
+    const uint32_t ko_ = (uint32_t)(2 * min((ms_), steps - 1) + (ks_)) * 2048u;                 \
+    _Pragma("unroll") for (int f = 0; f < 2; f++)                                               \
+      _Pragma("unroll") for (int j = 0; j < 2; j++) a[slot_][f][ks_][j] = __builtin_bit_cast(   \
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(a_lo + 1024u * j), (int)(a_row[f] + ko_), 0)); \
+  } while (0)
+#define SC_READ_B(buf_, t_, bb_)                                                                \
+  do {                                                                                          \
+    _Pragma("unroll") for (int c = 0; c < NF; c++) b[bb_][c] = Bs[buf_][(t_) / 2][(t_) % 2][c][lane]; \
+  } while (0)
+#define SC_MFMA(slot_, t_, bb_)                                                                 \
+  do {                                                                                          \
+    _Pragma("unroll") for (int c = 0; c < NF; c++)                                              \
+      _Pragma("unroll") for (int f = 0; f < 2; f++) acc[f][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( \
+          b[bb_][c], a[slot_][f][(t_) / 2][(t_) % 2], acc[f][c], 0, 0, 0);                      \
+  } while (0)
+  // one 16-k sub-step: the next sub-step's LDS reads first, then the loads,
+  // then the MFMAs
+#define SC_SCHED(nvm_)                                                                          \
+  do {                                                                                          \
+    __builtin_amdgcn_sched_group_barrier(0x100, NF, 0);                                         \
+    __builtin_amdgcn_sched_group_barrier(0x020, (nvm_), 0);                                     \
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NF, 0);                                     \
+  } while (0)
+#define SC_STEP(ms_, u_)                                                                        \
+  do {                                                                                          \
+    SC_READ_B((u_) % NB, 1, 1);                                                                 \
+    SC_LOAD_A((ms_) + RA - 1, ((u_) + RA - 1) % RA, 0);                                         \
+    SC_MFMA((u_) % RA, 0, 0);                                                                   \
+    SC_SCHED(4);                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+    SC_READ_B((u_) % NB, 2, 0);                                                                 \
+    SC_LOAD_A((ms_) + RA - 1, ((u_) + RA - 1) % RA, 1);                                         \
+    SC_MFMA((u_) % RA, 1, 1);                                                                   \
+    SC_SCHED(4);                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+    SC_READ_B((u_) % NB, 3, 1);                                                                 \
+    SC_MFMA((u_) % RA, 2, 0);                                                                   \
+    SC_SCHED(0);                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+    SC_READ_B(((u_) + 1) % NB, 0, 0);                                                           \
+    SC_MFMA((u_) % RA, 3, 1);                                                                   \
+    SC_SCHED(0);                                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+    __syncthreads();                                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+  } while (0)
+
+#pragma unroll
+    for (int s = 0; s < RA - 1; s++) {
+      SC_LOAD_A(s, s, 0);
+      SC_LOAD_A(s, s, 1);
+    }
+    __syncthreads();  // buffers 0 and 1 dequantized
+    SC_READ_B(0, 0, 0);
+    int ms = 0;
+    for (; ms + UC <= steps; ms += UC) {
+#pragma unroll
+      for (int u = 0; u < UC; u++) SC_STEP(ms + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < UC - 1; u++)
+      if (ms + u < steps) SC_STEP(ms + u, u);
+#undef SC_STEP
+#undef SC_SCHED
+#undef SC_MFMA
+#undef SC_READ_B
+#undef SC_LOAD_A
+
+    // acc[f][c] register e: m = m0 + 32 f + lane % 32, n = n0 + 32 c + 8 (e / 4) + 4 g + e % 4
+    if (staged) {
+#pragma unroll
+      for (int f = 0; f < 2; f++) {
+        __syncthreads();  // the previous round's rows are stored
+#pragma unroll
+        for (int c = 0; c < NF; c++)
+#pragma unroll
+          for (int qq = 0; qq < 4; qq++) {
+            const int col = 32 * c + 8 * qq + 4 * g;
+            if (y_dtype == RQ_F32)
+              *reinterpret_cast<f32x4*>(st + mrow * RS + col * 4) =
+                  f32x4{acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
+            else
+              *reinterpret_cast<u32x2*>(st + mrow * RS + col * 2) =
+                  u32x2{pack2_bf16(acc[f][c][4 * qq], acc[f][c][4 * qq + 1]),
+                        pack2_bf16(acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3])};
+          }
+        __syncthreads();  // rows staged
+        for (int p = lane; p < 16 * ppr; p += 64) {
+          const int r = p / ppr, pc = p % ppr;
+          const int m = m0 + 32 * f + r;
+          if (m < M && pc < vpr) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RS + pc * 16);
+            *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(y) + ((int64_t)m * N + n0) * ebytes + pc * 16) = v;
+          }
         }
       }
-    } else {
+      return;
+    }
+    const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+    for (int f = 0; f < 2; f++) {
       const int m = m0 + 32 * f + mrow;
       if (m >= M) continue;
 #pragma unroll
       for (int c = 0; c < NF; c++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const int qq = q0 + h;
+        for (int qq = 0; qq < 4; qq++) {
           const int n = n0 + 32 * c + 8 * qq + 4 * g;
           const float v[4] = {acc[f][c][4 * qq], acc[f][c][4 * qq + 1], acc[f][c][4 * qq + 2], acc[f][c][4 * qq + 3]};
           if (vec && n + 3 < N) {
@@ -718,6 +598,80 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_pe
             }
           }
         }
+    }
+    return;
+  }
+
+  // ---- producer ----
+  const int p = wave - 4;
+  constexpr uint32_t CB = FMT == RQ_Q8_0 ? 512u : 256u, RB = FMT == RQ_Q8_0 ? 32u : 16u;
+  const __amdgpu_buffer_rsrc_t qr = wd_rsrc(q, (uint32_t)(npad / 16) * (uint32_t)nkb * CB);
+  const __amdgpu_buffer_rsrc_t sr = wd_rsrc(sc, (uint32_t)npad * (uint32_t)nkb * (uint32_t)sizeof(ST));
+  const bool has2 = p + 4 < NU;  // the second unit (waves 4, 5 at NF 3; all at NF 4)
+  const int g_last = npad / 16 - 1;
+  int uu[2];
+  uint32_t w_lo[2], w_so[2], w_ks[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    uu[i] = min(p + 4 * i, NU - 1);
+    const uint32_t grp = (uint32_t)min(n0 / 16 + 2 * (uu[i] % NF) + ((lane & 31) >> 4), g_last);
+    w_lo[i] = grp * (uint32_t)nkb * CB + (uint32_t)(lane & 15) * RB + (FMT == RQ_Q8_0 ? 16u * (uint32_t)g : 0u);
+    w_so[i] = (grp * (uint32_t)nkb * 16u + (uint32_t)(lane & 15)) * (uint32_t)sizeof(ST);
+    w_ks[i] = (uint32_t)__builtin_amdgcn_readfirstlane(uu[i] / NF);
+  }
+  WdCodes wc[RW][2];
+#define SP_LOAD(ms_, slot_)                                                                     \
+  do {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) wd_load<FMT, ST>(wc[slot_][i], qr, sr, w_lo[i], w_so[i], \
+                                                                   (uint32_t)(2 * min((ms_), steps - 1)) + w_ks[i]); \
+  } while (0)
+#define SP_DEQUANT(slot_, buf_)                                                                 \
+  do {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                             \
+      if (i == 0 || has2) {                                                                     \
+        bf16x8 f0_, f1_;                                                                        \
+        wd_dequant<FMT, ST>(wc[slot_][i], g, f0_, f1_);                                         \
+        Bs[buf_][uu[i] / NF][0][uu[i] % NF][lane] = f0_;                                        \
+        Bs[buf_][uu[i] / NF][1][uu[i] % NF][lane] = f1_;                                        \
+      }                                                                                         \
+    }                                                                                           \
+  } while (0)
+#define SP_STEP(ms_, u_)                                                                        \
+  do {                                                                                          \
+    SP_LOAD((ms_) + RW - 1, ((u_) + RW - 1) % RW);                                              \
+    SP_DEQUANT(((u_) + 2) % RW, ((u_) + 2) % NB);                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+    __syncthreads();                                                                            \
+    __builtin_amdgcn_sched_barrier(0);                                                          \
+  } while (0)
+#pragma unroll
+  for (int s = 0; s < RW - 1; s++) SP_LOAD(s, s);
+  SP_DEQUANT(0, 0);
+  SP_DEQUANT(1, 1);
+  __syncthreads();
+  int ms = 0;
+  for (; ms + UP <= steps; ms += UP) {
+#pragma unroll
+    for (int u = 0; u < UP; u++) SP_STEP(ms + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u < UP - 1; u++)
+    if (ms + u < steps) SP_STEP(ms + u, u);
+#undef SP_STEP
+#undef SP_DEQUANT
+#undef SP_LOAD
+  if (!staged) return;
+#pragma unroll
+  for (int f = 0; f < 2; f++) {
+    __syncthreads();
+    __syncthreads();
+    for (int pp = lane; pp < 16 * ppr; pp += 64) {
+      const int r = 16 + pp / ppr, pc = pp % ppr;
+      const int m = m0 + 32 * f + r;
+      if (m < M && pc < vpr) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RS + pc * 16);
+        *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(y) + ((int64_t)m * N + n0) * ebytes + pc * 16) = v;
+      }
     }
   }
 }
@@ -752,9 +706,32 @@ hipError_t launch_pack_x32(const MatmulArgs& a) {
   return hipGetLastError();
 }
 
-// K-pair ring depths: activation slots (loads RA - 1 macro steps ahead),
-// weight units in flight, LDS buffers of dequantized fragments
-constexpr int kPairRA = 4, kPairRW = 4, kPairNB = 3;
+// Role-split ring depths: activation slots (loads RA - 1 macro steps ahead),
+// weight units in flight (RW - 1 ahead). Measured at the C2 shape: RA 3
+// against 4 (52.8 against 56.6 us kernel; at NF 4, RA 4 exceeds the
+// register budget and spills).
+constexpr int kRsRA = 3, kRsRW = 6;
+template <int FMT, typename ST, int NF>
+static hipError_t launch_rs_t(const MatmulArgs& a, int tiles_m, int tiles_n) {
+  hipExtLaunchKernelGGL((gemm_rs_kernel<FMT, ST, NF, kRsRA, kRsRW>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
+                        a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
+                        static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
+                        a.y_dtype, tiles_m, (uint32_t)pack_x32_bytes(a.m, a.k));
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_rs(const MatmulArgs& a, int nf) {
+  if ((nf != 3 && nf != 4) || a.k % 64 != 0) return hipErrorInvalidValue;
+  const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.npad + 32 * nf - 1) / (32 * nf));
+  if (hipError_t e = launch_pack_x32(a)) return e;
+#define RQ_RS(FMT_, ST_) \
+  return nf == 3 ? launch_rs_t<FMT_, ST_, 3>(a, tiles_m, tiles_n) : launch_rs_t<FMT_, ST_, 4>(a, tiles_m, tiles_n);
+  if (a.format == RQ_Q8_0) { RQ_RS(RQ_Q8_0, float) }
+  if (a.scale_dtype == RQ_F16) { RQ_RS(RQ_Q4_0, uint16_t) }
+  RQ_RS(RQ_Q4_0, float)
+#undef RQ_RS
+}
+
 template <int FMT, typename ST>
 static hipError_t launch_wide_t(const MatmulArgs& a, const WidePlan& p) {
   hipExtLaunchKernelGGL((gemm_wide_kernel<FMT, ST, 6, 2, 4>), dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(256), 0,
@@ -762,27 +739,6 @@ static hipError_t launch_wide_t(const MatmulArgs& a, const WidePlan& p) {
                         static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
                         a.y_dtype, p.tiles_m, (uint32_t)pack_x32_bytes(a.m, a.k));
   return hipGetLastError();
-}
-
-template <int FMT, typename ST, int NF>
-static hipError_t launch_pair_t(const MatmulArgs& a, int tiles_m, int tiles_n) {
-  hipExtLaunchKernelGGL((gemm_pair_kernel<FMT, ST, kPairRA, kPairRW, kPairNB, NF>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0,
-                        a.stream, nullptr, a.ev_main[1], 0, a.q, static_cast<const ST*>(a.scales),
-                        static_cast<const uint16_t*>(a.scratch), a.y, (int)a.m, (int)a.k, (int)a.n, (int)a.npad,
-                        a.y_dtype, tiles_m, (uint32_t)pack_x32_bytes(a.m, a.k));
-  return hipGetLastError();
-}
-
-hipError_t launch_gemm_pair(const MatmulArgs& a, int nf) {
-  if ((nf != 3 && nf != 4) || a.k % 64 != 0) return hipErrorInvalidValue;
-  const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.npad + 32 * nf - 1) / (32 * nf));
-  if (hipError_t e = launch_pack_x32(a)) return e;
-#define RQ_PAIR(FMT_, ST_) \
-  return nf == 3 ? launch_pair_t<FMT_, ST_, 3>(a, tiles_m, tiles_n) : launch_pair_t<FMT_, ST_, 4>(a, tiles_m, tiles_n);
-  if (a.format == RQ_Q8_0) { RQ_PAIR(RQ_Q8_0, float) }
-  if (a.scale_dtype == RQ_F16) { RQ_PAIR(RQ_Q4_0, uint16_t) }
-  RQ_PAIR(RQ_Q4_0, float)
-#undef RQ_PAIR
 }
 
 hipError_t launch_gemm_wide(const MatmulArgs& a, const WidePlan& p) {

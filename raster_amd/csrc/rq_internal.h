@@ -183,8 +183,9 @@ WidePlan plan_gemm_wide(int64_t m, int64_t k, int64_t npad, int cu_count);
 // bytes of the 32x32x16 operand copy of x (rows rounded up to 32)
 size_t pack_x32_bytes(int64_t m, int64_t k);
 hipError_t launch_gemm_wide(const MatmulArgs& a, const WidePlan& p);
-// 256 x 32 nf tiles, eight waves in K pairs (gemm_wide.hip); K a multiple of 64
-hipError_t launch_gemm_pair(const MatmulArgs& a, int nf);  // nf: 3 or 4 column fragments
+// 256 x 32 nf tiles, eight waves split into MFMA consumers and dequantizing
+// producers (gemm_wide.hip); K a multiple of 64
+hipError_t launch_gemm_rs(const MatmulArgs& a, int nf);  // nf: 3 or 4 column fragments
 // Fragment-major copy of bf16 activations into a.scratch (gemm_bf16.hip).
 hipError_t launch_pack_x(const MatmulArgs& a);
 hipError_t launch_dequant(const Weight& w, float* out, hipStream_t stream);

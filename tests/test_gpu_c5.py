@@ -7,13 +7,13 @@ checked where it is timed:
 
   Q4_0 (fp16 scales)   m = 1 (v_dot4 GEMV), 6 and 16 (MFMA decode, 4 / 8 K-slices),
                        32 and 64 (small-m GEMM with K-slices), 256 and 300
-                       (prefill GEMM: K-pair 256 x 128 tiles, 300 with a
+                       (prefill GEMM: role-split 256 x 128 tiles, 300 with a
                        partial second row tile)
   Q8_0 (f32 scales)    m = 1 (int8-level decode), 12 and 16 (int8-level decode:
                        the weight is above the MFMA decode's 32 Mi elements),
                        32 (small-m GEMM with K-slices), 256 and 300 (prefill GEMM)
 
-and the K-pair 256 x 128 tiles with a partial last column tile (K = 4096,
+and the role-split 256 x 128 tiles with a partial last column tile (K = 4096,
 N = 28656, m = 300).
 
 bf16 activations as the workload defines them, plus f32 activations at the
@@ -138,7 +138,7 @@ def test_c5_q8(torch, orc, q8, m, xdt):
 
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_kpair_128_partial_tiles(torch, ctx, orc, fmt):
-    # m = 300, K = 4096, N = 28656: the tile cost model takes the K-pair
+    # m = 300, K = 4096, N = 28656: the tile cost model takes the role-split
     # kernel's 256 x 128 tiles (448 tiles, two rounds of the CUs, against 512
     # of 256 x 112); the second row tile holds 44 rows and the last column
     # tile 112 columns. Checked against the oracle on rows at both tile edges,
@@ -148,7 +148,7 @@ def test_kpair_128_partial_tiles(torch, ctx, orc, fmt):
     m, k2, n2 = 300, 4096, 28656
     edges = [0, 1, 127, 128, 255, 256, 14335, 14336, n2 - 113, n2 - 112, n2 - 17, n2 - 16, n2 - 1]
     rows = np.unique(np.concatenate([edges, np.linspace(0, n2 - 1, 97).astype(np.int64)]))
-    note(f"K-pair 256x128 partial tiles {fmt} m={m} {n2}x{k2}")
+    note(f"role-split 256x128 partial tiles {fmt} m={m} {n2}x{k2}")
     if fmt == "q8":
         codes, scales = wl.q8_weights(n2, k2, seed=71)
         w = raster_amd.QWeight.q8(codes, scales, n2, k2, ctx)

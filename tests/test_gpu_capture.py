@@ -97,7 +97,7 @@ def test_graph_of_mixed_calls_replays_bit_for_bit(torch, ctx, orc):
     import raster_amd
 
     note("graph: bf16 GEMM + int8 chain + K-quant + no-alloc on two weights")
-    wa = q8(raster_amd, ctx, 11008, 4096, seed=1)      # prefill GEMM (K-pair kernel)
+    wa = q8(raster_amd, ctx, 11008, 4096, seed=1)      # prefill GEMM (role-split kernel)
     wb = q4(raster_amd, ctx, 4096, 4096, seed=2)       # int8 chain: quantize_act_i8 -> int8 GEMM
     wc = q4k(raster_amd, ctx, orc, 2048, 2048, seed=3)  # K-quant, f32 x quantized in the call
     wd = q8(raster_amd, ctx, 4160, 8192, seed=4)       # no-alloc: int8-level decode with K-split

@@ -2,8 +2,8 @@
 bit, and full outputs at C2 and C5 (M = 256) against an f64 product.
 
 One-hot activations: row r of x is 1 at a single k_r and 0 elsewhere. Every
-product with 1 and every sum with 0 is exact in f32 (also across the K-pair
-kernels' two partial sums), so y[r, o] is exactly the operand the kernel used
+product with 1 and every sum with 0 is exact in f32 (also across the K-split
+kernels' partial sums), so y[r, o] is exactly the operand the kernel used
 for W[o, k_r]:
   * bf16 GEMMs (bf16 x, m > 16): RNE-to-bf16 of Raster's dequant,
     f32(scale * code) (raster/quant/train.clj:60-71; Q4_0 scale * (q - 8),
@@ -92,8 +92,8 @@ def one_hot(torch, m, in_, ks, xdt):
 
 # (format, out, in, m, kernel): bf16 x, every weight element read back
 GEMM_CASES = [
-    ("q8", 11008, 4096, 512, "C2: K-pair 256 x 96"),
-    ("q4", 11008, 4096, 512, "K-pair 256 x 96, Q4_0"),
+    ("q8", 11008, 4096, 512, "C2: role-split 256 x 96"),
+    ("q4", 11008, 4096, 512, "role-split 256 x 96, Q4_0"),
     ("q8", 28672, 8192, 256, "C5: 8-wave 256 x 112"),
     ("q4", 28672, 8192, 256, "C5: 8-wave 256 x 112, Q4_0"),
     ("q8", 11008, 4096, 1024, "one wave per SIMD, 256 x 192"),

@@ -84,8 +84,8 @@ CASES = [
     ("q8", 4160, 8192, [12, 3], "f32", "f32"),           # int8-level decode with K-split (above 32 Mi)
     ("q4", 8192, 8192, [64, 32], "bf16", "bf16"),        # small-m GEMM: packed x + K-slices
     ("q8", 28672, 8192, [32, 17], "bf16", "bf16"),       # small-m GEMM, Q8_0: packed x + K-slices
-    ("q8", 11008, 4096, [512, 128], "bf16", "bf16"),     # prefill GEMM: packed x (K-pair kernel, then 128-row tiles)
-    ("q8", 11008, 4096, [1024, 512], "bf16", "bf16"),    # 256 x 192 one-wave GEMM, then the K-pair kernel
+    ("q8", 11008, 4096, [512, 128], "bf16", "bf16"),     # prefill GEMM: packed x (role-split kernel, then 128-row tiles)
+    ("q8", 11008, 4096, [1024, 512], "bf16", "bf16"),    # 256 x 192 one-wave GEMM, then the role-split kernel
     ("q8", 1000, 1024, [300, 17], "f32", "f32"),         # exact-f32 GEMM, no scratch
     ("q4k", 4096, 4096, [8, 1], "f32", "f32"),           # K-quant: q8_K activations in scratch
     ("q6k", 1024, 2048, [40, 3], "f32", "bf16"),         # K-quant, m above the decode range
