@@ -165,7 +165,7 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    at 16 < m <= 64 and for Q8_0 at 16 < m <= 48, or <= 64 when
  *    in >= 8192; for m > 128 and in % 64 == 0, 256 x 192 tiles with one
  *    wave per SIMD where they fill their rounds of the CUs to 80%, else the
- *    cost model's tile, 256 x 96 on the K-pair kernel); f32 x: the
+ *    cost model's tile, 256 x 96 on the role-split kernel); f32 x: the
  *    exact-code f32 GEMM;
  *  - Q4_K / Q6_K weights (f32 x only, any m; bf16 x fails with RQ_ERR_DTYPE):
  *    x is quantized to q8_K in scratch and the K-quant GEMV runs, the same two
@@ -192,9 +192,11 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
  *    NaN; a non-finite activation makes its row's outputs non-finite.
  *  - bf16 x, m > 16: weights are dequantized to bf16 (exact f32 product
  *    scale*code, then one round-to-nearest-even) and multiplied with bf16 MFMA;
- *    on the eight-wave tiles (m > 128 where the tile cost model picks them;
- *    the K-pair kernel) K is summed as two f32 partial sums, of the even and
- *    of the odd 32-blocks, added at the end.
+ *    on the eight-wave 16x16x32 tiles (m > 128 where the tile cost model
+ *    picks 256 x 112, or in % 64 != 0) K is summed as two f32 partial sums,
+ *    of the even and of the odd 32-blocks, added at the end; the 32x32x16
+ *    kernels (256 x 96 / 256 x 128 role-split, 256 x 192) keep one running
+ *    sum over K.
  *  - f32 x, m > 16: exact codes as bf16 with the scale applied in f32 and x
  *    split into two bf16 terms (about 16 mantissa bits).
  *
