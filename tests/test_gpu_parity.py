@@ -238,9 +238,12 @@ def test_gemm_bf16_ragged(torch, ctx, orc, m, in_, out, fmt):
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_gemm_bf16_wide_tiles(torch, ctx, orc, m, in_, out, fmt):
     # wide N: the tile cost model picks an 8-wave tile, one workgroup per CU
-    # (256 x 96 near m = 512, 256 x 112 near N = 28672 at m <= 256), whose
-    # wave pairs split K into even and odd blocks; ragged M and N, 1, 2, 3, 9
-    # (one full ring turn and half a step) and 13 K-blocks
+    # (256 x 96 near m = 512, 256 x 112 near N = 28672 at m <= 256): the
+    # role-split 32x32x16 kernel where K is a multiple of 64 (one macro step at
+    # K = 64; rows of N = 12004 in bf16 are not whole 16-byte pieces, so its
+    # direct stores run), else the 16x16x32 kernel whose wave pairs split K
+    # into even and odd blocks; ragged M and N, 1, 2, 3, 9 (one full ring turn
+    # and half a step) and 13 K-blocks
     import raster_amd
 
     x = wl.activations(m, in_, seed=m + in_, dtype="bf16")
