@@ -1,5 +1,8 @@
-// gemm_wide.hip — prefill GEMM for bf16 activations on 32x32x16 bf16 MFMA,
-// one wave per SIMD, 256 x 192 tiles over the whole K.
+// gemm_wide.hip — prefill GEMMs for bf16 activations on 32x32x16 bf16 MFMA:
+// gemm_wide_kernel (one wave per SIMD, 256 x 192 tiles over the whole K,
+// M >= 1024 at N = 11008) and gemm_rs_kernel (256 x 96 / 256 x 128 tiles,
+// eight waves split into MFMA consumers and dequantizing producers: C2 and
+// C5 at M = 256). Both read the activations from the pack_x32 copy.
 //
 // y[m, o] = sum_k x[m, k] * W[o, k],  W[o, k] = scale[o, k/32] * code[o, k]
 //
@@ -7,7 +10,7 @@
 // bf16 GEMMs do it: the f32 product scale * code with one IEEE rounding
 // (Raster's dequant, raster/quant/train.clj:60-71), then RNE to bf16.
 //
-// Why this shape. Per CU the global-load return path delivers ~50 B/clk and
+// Why 256 x 192 (gemm_wide_kernel). Per CU the global-load return path delivers ~50 B/clk and
 // the LDS ~114 B/clk (measured on MI355X). A 256-row x 192-column tile pulls
 // 256 x 64 B of activations and 192 x 36 B of weights per 32-k step, against
 // 256 * 192 * 64 flop: 30 B/clk at the full MFMA rate (a 256 x 96 tile needs
