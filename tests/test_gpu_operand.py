@@ -94,8 +94,8 @@ def one_hot(torch, m, in_, ks, xdt):
 GEMM_CASES = [
     ("q8", 11008, 4096, 512, "C2: role-split 256 x 96"),
     ("q4", 11008, 4096, 512, "role-split 256 x 96, Q4_0"),
-    ("q8", 28672, 8192, 256, "C5: 8-wave 256 x 112"),
-    ("q4", 28672, 8192, 256, "C5: 8-wave 256 x 112, Q4_0"),
+    ("q8", 28672, 8192, 256, "C5: role-split 256 x 128"),
+    ("q4", 28672, 8192, 256, "C5: role-split 256 x 128, Q4_0"),
     ("q8", 11008, 4096, 1024, "one wave per SIMD, 256 x 192"),
     ("q4", 4096, 2048, 48, "weight-stream small-m GEMM"),
     ("q8", 2048, 2048, 100, "64 < m <= 128 GEMM"),
