@@ -465,6 +465,50 @@ def test_zero_scale_blocks_and_zero_rows(torch, ctx, orc):
     w.destroy()
 
 
+@pytest.mark.parametrize("m,in_,out,route", [(40, 128, 24, "small-m GEMM"), (100, 128, 40, "64 < m <= 128 GEMM"),
+                                             (300, 128, 11008, "role-split 256 x 96"),
+                                             (1024, 128, 11008, "one wave per SIMD, 256 x 192")])
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_gemm_bf16_special_values(torch, ctx, orc, m, in_, out, route, fmt):
+    # every bf16-activation GEMM route with a weight row whose scales are all
+    # zero (output column 5), a zero scale block column, a zero activation
+    # row (3), an inf (row 7) and a NaN (row 9) activation: finite rows match
+    # the oracle, column 5 and row 3 are exactly zero, rows 7 and 9 are
+    # non-finite in every column (inf times a zero weight is NaN)
+    import raster_amd
+
+    note(f"gemm bf16 special values {fmt} {route} m={m} {out}x{in_}")
+    x = wl.activations(m, in_, seed=m + 3, dtype="bf16").reshape(m, in_)
+    x[3] = 0.0
+    x[7, 70] = np.inf
+    x[9, 5] = np.nan
+    x = np.ascontiguousarray(x.ravel())
+    cols = np.union1d(rows_subset(out, 256), [5])
+    if fmt == "q8":
+        codes, scales = wl.q8_weights(out, in_, seed=out + 1)
+        scales.reshape(out, -1)[5, :] = 0.0
+        scales.reshape(out, -1)[:, 2] = 0.0
+        w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+        ref = orc.qlinear_q8(x, codes.reshape(out, in_)[cols].ravel(),
+                             scales.reshape(out, -1)[cols].ravel(), m, in_, len(cols))
+    else:
+        packed, sc16 = wl.q4_weights(out, in_, seed=out + 1)
+        s = sc16.view(np.float16)
+        s.reshape(out, -1)[5, :] = 0.0
+        s.reshape(out, -1)[:, 2] = 0.0
+        w = raster_amd.QWeight.q4(packed, s, out, in_, ctx)
+        ref = orc.qlinear_q4(x, packed.reshape(out, -1)[cols].ravel(), s.view(np.uint16).reshape(out, -1)[cols].ravel(),
+                             m, in_, len(cols))
+    y = run(torch, w, x, m, "bf16", "f32")
+    w.destroy()
+    ref = ref.reshape(m, len(cols))
+    fin = np.setdiff1d(np.arange(m), [7, 9])
+    assert orc.normwise_relerr(y[fin][:, cols], ref[fin]) < TOL_BF16
+    assert np.all(y[fin, 5] == 0.0)
+    assert np.all(y[3] == 0.0)
+    assert not np.any(np.isfinite(y[7])) and not np.any(np.isfinite(y[9]))
+
+
 # ---------------------------------------------------------------- ingestion formats
 @pytest.mark.parametrize("nibble", [True, False])
 def test_x8_layout_ingestion(torch, ctx, orc, nibble):
