@@ -149,7 +149,8 @@ int rq_weight_device_ptrs(rq_weight w, const void** qdata, const void** scales);
 
 /* y[m,o] = sum_i dequant(W)[o,i] * x[m,i] for a resident weight; x is
  * [m x in] of x_dtype (RQ_F32 or RQ_BF16), y is [m x out] of y_dtype (RQ_F32 or
- * RQ_BF16), both device pointers, row-major. Replaces qlinear-q8
+ * RQ_BF16), both device pointers, row-major; x 16-byte aligned and y aligned
+ * to its element (else RQ_ERR_SHAPE). Replaces qlinear-q8
  * (raster/quant/train.clj:77-108) and, for Q4_0, the f32-activation dequant
  * GEMV; m <= 16 runs the HBM-bound GEMV kernels, larger m the MFMA GEMM.
  * m == 0 is a no-op.

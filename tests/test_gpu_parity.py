@@ -509,6 +509,31 @@ def test_gemm_bf16_special_values(torch, ctx, orc, m, in_, out, route, fmt):
     assert not np.any(np.isfinite(y[7])) and not np.any(np.isfinite(y[9]))
 
 
+@pytest.mark.parametrize("m,in_,out", [(40, 128, 24), (100, 128, 40), (300, 128, 11008), (1024, 128, 11008)])
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+def test_gemm_output_one_element_off_alignment(torch, ctx, orc, m, in_, out, ydt):
+    # y may start at any element (only x must be 16-byte aligned): the bf16-x
+    # GEMM routes (small-m, 64 < m <= 128, role-split, 256 x 192) then store
+    # element by element instead of staging whole 16-byte row pieces, and
+    # must give the aligned call's bits
+    import raster_amd
+
+    note(f"gemm misaligned y {ydt} m={m} {out}x{in_}")
+    codes, scales = wl.q8_weights(out, in_, seed=out + 2)
+    w = raster_amd.QWeight.q8(codes, scales, out, in_, ctx)
+    x = dev(torch, wl.activations(m, in_, seed=m + 4, dtype="bf16"), "bf16").reshape(m, in_)
+    dt = torch.bfloat16 if ydt == "bf16" else torch.float32
+    ya = w.matmul(x, out_dtype=dt)
+    buf = torch.full((m * out + 1,), 7.0, dtype=dt, device="cuda")
+    yb = buf[1:].view(m, out)
+    assert yb.data_ptr() % 16 != 0
+    w.matmul(x, y=yb)
+    torch.cuda.synchronize()
+    w.destroy()
+    assert torch.equal(ya, yb)
+    assert buf[0].item() == 7.0
+
+
 # ---------------------------------------------------------------- ingestion formats
 @pytest.mark.parametrize("nibble", [True, False])
 def test_x8_layout_ingestion(torch, ctx, orc, nibble):
