@@ -5,7 +5,9 @@ weight-stream GEMM to 64, the per-wave-weights GEMM to 128, the tile cost model
 above), by format, activation dtype and weight size, and cut K into slices
 by LDS fit and grid fill. The dedicated tests pin each route at chosen edges;
 this sweep draws 48 shapes from a fixed seed over every m band (in a multiple
-of 32, out anything), both formats, f32 and bf16 x, f32 and bf16 y, and holds
+of 32, out anything), both formats, f32 and bf16 x, f32 and bf16 y, and 12
+wide prefill shapes (m 129-1100, out 6000-30000, bf16 x) for the 32x32x16
+GEMMs the tile cost model takes there, and holds
 each to the oracle (qlinear-q8's loop, raster/quant/train.clj:77-108, over the
 Q8_0 or Q4_0 dequant) on a subset of output rows: normwise max|y - ref| /
 max|ref| < 1e-3 for f32 x and y, < 1e-2 with bf16 x or y. Each call is
@@ -15,7 +17,7 @@ rq_qmatmul_noalloc.
 """
 import numpy as np
 import pytest
-from sweep_shapes import SHAPES
+from sweep_shapes import SHAPES, WIDE_SHAPES
 
 from raster_amd import workloads as wl
 
@@ -47,7 +49,8 @@ def ctx(torch):
     c.close()
 
 
-@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", SHAPES, ids=[f"s{s[0]}" for s in SHAPES])
+@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", SHAPES + WIDE_SHAPES,
+                         ids=[f"s{s[0]}" for s in SHAPES + WIDE_SHAPES])
 def test_sweep(torch, ctx, orc, i, m, in_, out, fmt, xdt, ydt):
     import raster_amd
 
