@@ -12,7 +12,7 @@ import ctypes as C
 
 import numpy as np
 import pytest
-from sweep_shapes import SHAPES
+from sweep_shapes import SHAPES, WIDE_SHAPES
 
 from raster_amd import _lib
 from raster_amd import workloads as wl
@@ -127,7 +127,11 @@ def test_noalloc_rejects_calls_beyond_its_scratch(torch, ctx):
         w.destroy()
 
 
-@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", SHAPES, ids=[f"s{s[0]}" for s in SHAPES])
+# the wide prefill shapes need at most 14 MB of packed activations: all within the fixed scratch
+NA_SHAPES = SHAPES + WIDE_SHAPES
+
+
+@pytest.mark.parametrize("i,m,in_,out,fmt,xdt,ydt", NA_SHAPES, ids=[f"s{s[0]}" for s in NA_SHAPES])
 def test_noalloc_sweep(torch, ctx, i, m, in_, out, fmt, xdt, ydt):
     import raster_amd
 
